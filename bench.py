@@ -1,0 +1,228 @@
+"""Throughput of the fused-op hot path on one MI355X.
+
+Workload (one step): SwiGLU forward + backward on gate, up [8192, 6144] bf16
+and RoPE forward + backward on q [4, 16, 2048, 128], k [4, 8, 2048, 128]
+bf16 with positions 0..2047, theta 1e6, cos/sin computed in-kernel. Inputs
+~N(0, 1) drawn on the CPU from seeded generators, resident in HBM before the
+timed region.
+
+value = algorithmic bytes per step / time per step, where algorithmic bytes
+count each input read once and each output written once:
+  SwiGLU fwd 3*N*I*2 + bwd 5*N*I*2 = 805,306,368 B
+  RoPE   fwd (read + write q, k) + bwd (same) = 201,326,592 B
+roofline: the dominant kernel (SwiGLU backward, 503,316,480 B per launch)
+timed with HIP events on the stream it runs on, against 8 TB/s.
+cpu_baseline: the oracle (a CPU restatement of the reference's torch ops)
+on a bounded sample of the same workload, on the host's cores.
+
+Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+N_TOK, INTER = 8192, 6144
+RB, RHQ, RHK, RS, RD = 4, 16, 8, 2048, 128
+THETA = 1e6
+SWIGLU_FWD_BYTES = 3 * N_TOK * INTER * 2
+SWIGLU_BWD_BYTES = 5 * N_TOK * INTER * 2
+ROPE_DIR_BYTES = 2 * RB * (RHQ + RHK) * RS * RD * 2       # read + write q and k
+STEP_BYTES = SWIGLU_FWD_BYTES + SWIGLU_BWD_BYTES + 2 * ROPE_DIR_BYTES
+METRIC = "fused-op fwd+bwd GB/s (% HBM peak); LoRA layer train-step tokens/sec"
+
+
+def seeded(shape, seed, dtype):
+    import torch
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(*shape, generator=g, dtype=torch.float32).to(dtype)
+
+
+def load_traffic():
+    """HBM bytes per launch of the dominant kernel, from the committed
+    rocprofv3 PMC summary (FETCH_SIZE / WRITE_SIZE scaled by the copy-kernel
+    calibration); None when not measured."""
+    path = os.path.join(ROOT, "profiles", "traffic_swiglu_bwd.json")
+    try:
+        with open(path) as f:
+            d = json.load(f)
+        return int(d["hbm_bytes_per_launch"])
+    except (OSError, KeyError, ValueError):
+        return None
+
+
+def cpu_baseline(seconds: float):
+    """Oracle (reference torch ops restated, CPU) on a bounded sample:
+    SwiGLU on 1024 of the 8192 tokens, RoPE on batch 1 of 4 (tables built
+    as the HF rotary module does, cast to bf16 as HF does)."""
+    import torch
+
+    from oracle import reference_ops as ref
+
+    n = 1024
+    g = seeded((n, INTER), 0, torch.bfloat16)
+    u = seeded((n, INTER), 1, torch.bfloat16)
+    dy = seeded((n, INTER), 2, torch.bfloat16)
+    q = seeded((1, RHQ, RS, RD), 3, torch.bfloat16)
+    k = seeded((1, RHK, RS, RD), 4, torch.bfloat16)
+    gq = seeded((1, RHQ, RS, RD), 5, torch.bfloat16)
+    gk = seeded((1, RHK, RS, RD), 6, torch.bfloat16)
+    pos = torch.arange(RS)
+    sample_bytes = 8 * n * INTER * 2 + 2 * 2 * (RHQ + RHK) * RS * RD * 2
+
+    def once():
+        out, sig = ref.swiglu_forward(g, u)
+        ref.swiglu_backward(g, u, sig, dy)
+        cos, sin = ref.rope_tables(pos, RD, THETA)
+        cos, sin = cos.to(torch.bfloat16), sin.to(torch.bfloat16)
+        ref.rope_forward(q, cos, sin)
+        ref.rope_forward(k, cos, sin)
+        ref.rope_backward(gq, cos, sin, torch.bfloat16)
+        ref.rope_backward(gk, cos, sin, torch.bfloat16)
+
+    once()  # warm-up
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        once()
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            break
+    per = el / reps
+    return {
+        "value": round(sample_bytes / per / 1e9, 3),
+        "unit": "GB/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": (f"oracle torch-CPU SwiGLU fwd+bwd on [{n}, {INTER}] bf16 + RoPE fwd+bwd on "
+                   f"q [1,{RHQ},{RS},{RD}], k [1,{RHK},{RS},{RD}] bf16 (tables built per call), "
+                   f"{reps} reps in {el:.1f} s, {sample_bytes} algorithmic bytes per rep"),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(run with --gpus 1)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from metal_liger_amd import hip_ops
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    bf = torch.bfloat16
+    gate = seeded((N_TOK, INTER), 0, bf).to(dev)
+    up = seeded((N_TOK, INTER), 1, bf).to(dev)
+    dy = seeded((N_TOK, INTER), 2, bf).to(dev)
+    q = seeded((RB, RHQ, RS, RD), 3, bf).to(dev)
+    k = seeded((RB, RHK, RS, RD), 4, bf).to(dev)
+    gq = seeded((RB, RHQ, RS, RD), 5, bf).to(dev)
+    gk = seeded((RB, RHK, RS, RD), 6, bf).to(dev)
+    pos = torch.arange(RS, device=dev)
+    inv = hip_ops.rope_inv_freq(RD, THETA, dev)
+    torch.cuda.synchronize()
+
+    stream = torch.cuda.current_stream(dev)
+    ev = {n: [] for n in ("swiglu_fwd", "swiglu_bwd", "rope_fwd", "rope_bwd")}
+
+    def step(record: bool):
+        marks = []
+        if record:
+            marks.append(torch.cuda.Event(enable_timing=True))
+            marks[-1].record(stream)
+        hip_ops.swiglu_fwd(gate, up)
+        if record:
+            marks.append(torch.cuda.Event(enable_timing=True))
+            marks[-1].record(stream)
+        hip_ops.swiglu_bwd(gate, up, dy)
+        if record:
+            marks.append(torch.cuda.Event(enable_timing=True))
+            marks[-1].record(stream)
+        hip_ops.rope_pos(q, k, pos, inv, 1.0)
+        if record:
+            marks.append(torch.cuda.Event(enable_timing=True))
+            marks[-1].record(stream)
+        hip_ops.rope_pos(gq, gk, pos, inv, -1.0)
+        if record:
+            marks.append(torch.cuda.Event(enable_timing=True))
+            marks[-1].record(stream)
+            for name, a, b in zip(ev, marks[:-1], marks[1:]):
+                ev[name].append((a, b))
+
+    for _ in range(args.warmup):
+        step(False)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step(True)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+
+    ms_step = wall * 1e3 / args.steps
+    value = STEP_BYTES / (wall / args.steps) / 1e9
+    per_op = {n: sum(a.elapsed_time(b) for a, b in v) / len(v) for n, v in ev.items()}
+    op_bytes = {"swiglu_fwd": SWIGLU_FWD_BYTES, "swiglu_bwd": SWIGLU_BWD_BYTES,
+                "rope_fwd": ROPE_DIR_BYTES, "rope_bwd": ROPE_DIR_BYTES}
+    breakdown = {n: {"us": round(per_op[n] * 1e3, 2),
+                     "GB/s": round(op_bytes[n] / (per_op[n] * 1e-3) / 1e9, 1)}
+                 for n in per_op}
+    dom_ms = per_op["swiglu_bwd"]
+    achieved = SWIGLU_BWD_BYTES / (dom_ms * 1e-3) / 1e9
+    roofline = {
+        "kernel": "swiglu_bwd_vec<bf16> (ml_swiglu_bwd)",
+        "bound": "hbm",
+        "achieved": round(achieved, 1),
+        "peak": HBM_PEAK_GBS,
+        "unit": "GB/s",
+        "frac": round(achieved / HBM_PEAK_GBS, 4),
+        "traffic": load_traffic(),
+        "algorithmic_bytes_per_launch": SWIGLU_BWD_BYTES,
+        "avg_launch_us": round(dom_ms * 1e3, 2),
+    }
+    line = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": ("SwiGLU + RoPE fwd+bwd bf16: gate/up [8192, 6144]; RoPE q [4,16,2048,128], "
+                         "k [4,8,2048,128], positions 0..2047, theta 1e6, cos/sin in-kernel"),
+            "bytes_per_step": STEP_BYTES,
+            "hbm_frac": round(value / HBM_PEAK_GBS, 4),
+        },
+        "roofline": roofline,
+        "breakdown": breakdown,
+    }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

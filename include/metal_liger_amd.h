@@ -1,0 +1,151 @@
+/*
+ * metal_liger_amd — C ABI of the MI355X (gfx950) fused-op library.
+ *
+ * This is the drop-in boundary that replaces the reference's native bridge
+ * (the pybind module `metal_liger_ext`, declared in csrc/metal_liger_ops.h:13-36
+ * and bound in csrc/bindings.mm:10-33) and the pure-torch bodies of the
+ * autograd functions in ops/fused_*.py.
+ *
+ * Conventions (every entry point):
+ *   - Plain pointers and sizes only. Device pointers are `void*`; sizes,
+ *     strides and leading dimensions are int64_t and count ELEMENTS.
+ *   - The caller allocates every output and every workspace; the library
+ *     allocates no device memory. `*_workspace_bytes` queries give the size.
+ *   - `stream` is a hipStream_t (NULL = the default stream). Work is enqueued
+ *     asynchronously in stream order; nothing synchronizes with the host.
+ *   - Return value 0 = success. Non-zero = error; ml_last_error() returns a
+ *     thread-local message (the reference raised RuntimeError through
+ *     TORCH_CHECK / std::runtime_error, csrc/rms_norm_metal.mm:116-117,
+ *     csrc/swiglu_metal.mm:71-72; the Python layer raises RuntimeError with
+ *     this message).
+ *   - All arithmetic is fp32 internally; outputs are rounded once (RNE) to
+ *     their storage dtype.
+ */
+#ifndef METAL_LIGER_AMD_H
+#define METAL_LIGER_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ML_ABI_VERSION 1
+
+/* dtype tags */
+#define ML_F32 0
+#define ML_BF16 1
+#define ML_F16 2
+
+/* status codes */
+#define ML_OK 0
+#define ML_ERR_INVALID 1 /* bad argument (shape, dtype, pointer, size) */
+#define ML_ERR_HIP 2     /* a HIP runtime call or kernel launch failed */
+
+/* ABI version of the loaded library (== ML_ABI_VERSION it was built with). */
+int ml_abi_version(void);
+
+/* Thread-local message describing the last failed call on this thread. */
+const char* ml_last_error(void);
+
+/* ------------------------------------------------------------------ RMSNorm
+ * Replaces metal_rms_norm_forward (csrc/metal_liger_ops.h:13-17,
+ * csrc/rms_norm_metal.mm:110-160) and the math of
+ * _FusedRMSNormFunction.forward (ops/fused_rms_norm.py:31-41).
+ *
+ *   rrms[r] = 1 / sqrt(mean_c(x[r,c]^2) + eps)
+ *   y[r,c]  = (x[r,c] * rrms[r]) * w[c]        (rounded to x's dtype)
+ *
+ * x, y: [rows, cols] with row strides ldx / ldy (last dim contiguous).
+ * w: [cols] of w_dtype. rrms: [rows] fp32 (may be NULL if not needed).
+ */
+int ml_rmsnorm_fwd(const void* x, int64_t ldx, const void* w, void* y, int64_t ldy,
+                   float* rrms, int64_t rows, int64_t cols, float eps, int x_dtype,
+                   int w_dtype, void* stream);
+
+/* Workspace for ml_rmsnorm_bwd (fp32 per-block dW partials), in bytes. */
+size_t ml_rmsnorm_bwd_workspace_bytes(int64_t rows, int64_t cols);
+
+/*
+ * Replaces metal_rms_norm_backward (csrc/metal_liger_ops.h:19-24,
+ * csrc/rms_norm_metal.mm:164-214) and _FusedRMSNormFunction.backward
+ * (ops/fused_rms_norm.py:43-60).
+ *
+ *   gw  = dy * w
+ *   dx  = gw * r - (x * mean_c(gw * x)) * r^3          (x's dtype)
+ *   dw  = sum_r dy * (x * r)                            (w's dtype)
+ *
+ * r is read from rrms when non-NULL, else recomputed from x and eps (the
+ * reference native backward recomputes it, kernels/rms_norm.metal:106-200).
+ * dy shares x's dtype. dw is reduced deterministically: fp32 per-block
+ * partials in `workspace`, then a fixed-order second pass.
+ */
+int ml_rmsnorm_bwd(const void* x, int64_t ldx, const void* w, const void* dy, int64_t lddy,
+                   const float* rrms, float eps, void* dx, int64_t lddx, void* dw,
+                   void* workspace, size_t workspace_bytes, int64_t rows, int64_t cols,
+                   int x_dtype, int w_dtype, void* stream);
+
+/* ------------------------------------------------------------------- SwiGLU
+ * Replaces metal_swiglu_forward (csrc/metal_liger_ops.h:27-30,
+ * csrc/swiglu_metal.mm:66-100) and _FusedSwiGLUFunction.forward
+ * (ops/fused_swiglu.py:26-35).
+ *
+ *   out = (gate * sigmoid(gate)) * up                   (n contiguous elements)
+ */
+int ml_swiglu_fwd(const void* gate, const void* up, void* out, int64_t n, int dtype,
+                  void* stream);
+
+/*
+ * Replaces metal_swiglu_backward (csrc/metal_liger_ops.h:32-36,
+ * csrc/swiglu_metal.mm:106-144) and _FusedSwiGLUFunction.backward
+ * (ops/fused_swiglu.py:37-50). sigmoid(gate) is recomputed, not stored.
+ *
+ *   dup   = dy * (gate * s)
+ *   dgate = ((dy * up) * s) * (1 + gate * (1 - s)),    s = sigmoid(gate)
+ */
+int ml_swiglu_bwd(const void* gate, const void* up, const void* dy, void* dgate, void* dup,
+                  int64_t n, int dtype, void* stream);
+
+/* --------------------------------------------------------------------- RoPE
+ * Rotate-half rotary embedding over one or two [B, H, S, D] tensors (q and,
+ * optionally, k — they share B, S, D and the angle source).
+ *
+ * geom (9 int64 per tensor): {B, H, S, in_sb, in_sh, in_ss, out_sb, out_sh,
+ * out_ss}; the D dimension is contiguous (stride 1) in input and output.
+ *
+ *   y[..j]      = x[j] * c[j]      - x[j+D/2] * sgn * s[j]
+ *   y[..j+D/2]  = x[j+D/2] * c[j+D/2] + x[j] * sgn * s[j+D/2]
+ *
+ * sgn = +1 applies the rotation (forward); sgn = -1 applies the reference's
+ * backward, rotate_half with -sin (ops/fused_rope.py:48-57).
+ */
+
+/*
+ * Table mode: cos/sin given as tensors broadcastable to [B, H, S, D]
+ * (replaces _FusedRoPEFunction / _apply_rotary_fused, ops/fused_rope.py:22-75,
+ * :110-127). cs_geom (6 int64): {cos_sb, cos_sh, cos_ss, sin_sb, sin_sh, sin_ss}
+ * (0 for broadcast dims); the D dimension of cos/sin is contiguous.
+ * out_dtype must be the promotion of x_dtype and cs_dtype.
+ */
+int ml_rope_table(const void* q, void* q_out, const int64_t* q_geom, const void* k, void* k_out,
+                  const int64_t* k_geom, int64_t D, const void* cos, const void* sin,
+                  const int64_t* cs_geom, float sgn, int x_dtype, int cs_dtype, int out_dtype,
+                  void* stream);
+
+/*
+ * Position mode: cos/sin computed in-kernel, angle = float(pos[b,s]) *
+ * inv_freq[j mod D/2] (fp32, as the HF rotary module builds its tables) —
+ * no table is read. positions: int64 [B, S] with strides pos_sb, pos_ss
+ * (pos_sb = 0 to share one row). inv_freq: fp32 [D/2] device array.
+ * Output dtype = x_dtype.
+ */
+int ml_rope_pos(const void* q, void* q_out, const int64_t* q_geom, const void* k, void* k_out,
+                const int64_t* k_geom, int64_t D, const int64_t* positions, int64_t pos_sb,
+                int64_t pos_ss, const float* inv_freq, float sgn, int x_dtype, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* METAL_LIGER_AMD_H */

@@ -1,0 +1,141 @@
+// Shared helpers for the metal_liger_amd HIP kernels (gfx950 / CDNA4 only).
+//
+// - dtype tags and typed 16-byte packs for coalesced global loads
+// - wave64 reductions
+// - a thread-local last-error string and CHECK macros used by every C-ABI
+//   entry point (status 0 = ok, non-zero = error, message via ml_last_error())
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+
+#include <type_traits>
+
+#include "../../include/metal_liger_amd.h"
+
+namespace mla {
+
+using bf16 = __bf16;
+using f16 = _Float16;
+
+// ---------------------------------------------------------------- errors ---
+void set_error(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
+void clear_error();
+
+#define ML_CHECK(cond, ...)            \
+  do {                                 \
+    if (!(cond)) {                     \
+      ::mla::set_error(__VA_ARGS__);   \
+      return ML_ERR_INVALID;           \
+    }                                  \
+  } while (0)
+
+#define ML_HIP_CHECK(call)                                                   \
+  do {                                                                       \
+    hipError_t e_ = (call);                                                  \
+    if (e_ != hipSuccess) {                                                  \
+      ::mla::set_error("%s failed: %s", #call, hipGetErrorString(e_));       \
+      return ML_ERR_HIP;                                                     \
+    }                                                                        \
+  } while (0)
+
+// Checks the launch that was just enqueued.
+#define ML_LAUNCH_CHECK() ML_HIP_CHECK(hipGetLastError())
+
+// Number of compute units of the current device (cached per device).
+int num_cus();
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// ------------------------------------------------------------- conversions ---
+__device__ __forceinline__ float to_f32(float v) { return v; }
+__device__ __forceinline__ float to_f32(bf16 v) { return static_cast<float>(v); }
+__device__ __forceinline__ float to_f32(f16 v) { return static_cast<float>(v); }
+
+template <typename T>
+__device__ __forceinline__ T from_f32(float v);
+template <>
+__device__ __forceinline__ float from_f32<float>(float v) { return v; }
+template <>
+__device__ __forceinline__ bf16 from_f32<bf16>(float v) { return static_cast<bf16>(v); }  // RNE (v_cvt_pk_bf16_f32)
+template <>
+__device__ __forceinline__ f16 from_f32<f16>(float v) { return static_cast<f16>(v); }
+
+// A 16-byte (or smaller) aligned pack of N elements of T.
+template <typename T, int N>
+struct alignas(sizeof(T) * N) Pack {
+  T v[N];
+};
+
+template <typename T, int N>
+__device__ __forceinline__ void load_pack(const T* __restrict__ p, float (&out)[N]) {
+  Pack<T, N> pk = *reinterpret_cast<const Pack<T, N>*>(p);
+#pragma unroll
+  for (int i = 0; i < N; ++i) out[i] = to_f32(pk.v[i]);
+}
+
+template <typename T, int N>
+__device__ __forceinline__ void store_pack(T* __restrict__ p, const float (&in)[N]) {
+  Pack<T, N> pk;
+#pragma unroll
+  for (int i = 0; i < N; ++i) pk.v[i] = from_f32<T>(in[i]);
+  *reinterpret_cast<Pack<T, N>*>(p) = pk;
+}
+
+// Elements of T per 16-byte transaction.
+template <typename T>
+constexpr int vec16() { return 16 / static_cast<int>(sizeof(T)); }
+
+// Loads N consecutive elements (converted to fp32) from p, which must be
+// 16-byte aligned when N*sizeof(T) >= 16 (split into 16-byte transactions).
+template <typename T, int N>
+__device__ __forceinline__ void load_n(const T* __restrict__ p, float* out) {
+  constexpr int P = (N * (int)sizeof(T) >= 16) ? 16 / (int)sizeof(T) : N;
+#pragma unroll
+  for (int i = 0; i < N; i += P) {
+    Pack<T, P> pk = *reinterpret_cast<const Pack<T, P>*>(p + i);
+#pragma unroll
+    for (int j = 0; j < P; ++j) out[i + j] = to_f32(pk.v[j]);
+  }
+}
+
+template <typename T, int N>
+__device__ __forceinline__ void store_n(T* __restrict__ p, const float* in) {
+  constexpr int P = (N * (int)sizeof(T) >= 16) ? 16 / (int)sizeof(T) : N;
+#pragma unroll
+  for (int i = 0; i < N; i += P) {
+    Pack<T, P> pk;
+#pragma unroll
+    for (int j = 0; j < P; ++j) pk.v[j] = from_f32<T>(in[i + j]);
+    *reinterpret_cast<Pack<T, P>*>(p + i) = pk;
+  }
+}
+
+// ------------------------------------------------------------- reductions ---
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+
+// Dispatch helper: calls f(T{}) for the element type named by a dtype tag.
+template <typename F>
+int dispatch_dtype(int dtype, F&& f) {
+  switch (dtype) {
+    case ML_F32: return f(float{});
+    case ML_BF16: return f(bf16{});
+    case ML_F16: return f(f16{});
+    default:
+      set_error("unsupported dtype tag %d", dtype);
+      return ML_ERR_INVALID;
+  }
+}
+
+}  // namespace mla

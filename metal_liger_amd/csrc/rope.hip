@@ -1,0 +1,271 @@
+// Rotate-half rotary embedding for gfx950 (ops/fused_rope.py:22-75, :110-127).
+//
+// One launch rotates q and k together. A thread owns one (b, s) position and
+// VEC consecutive pairs (j, j + D/2) of the head dimension, gets the VEC
+// cos/sin values once (from the tables, or computed in-kernel from the
+// position and inv_freq), then walks up to kHeadsPerThread heads of the
+// concatenated [q heads | k heads] list reusing them. Eight threads cover a
+// 128-wide head; a wave covers 8 consecutive positions, so each 16-byte
+// load/store instruction of a wave touches 2 KiB of contiguous rows for a
+// contiguous [B, H, S, D] tensor (and whole rows for HF's transposed views).
+#include "common.h"
+
+#pragma clang fp contract(off)
+
+namespace mla {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kHeadsPerThread = 4;
+
+struct RopeTensor {
+  const void* in;
+  void* out;
+  int64_t H;
+  int64_t sb, sh, ss;     // input strides (elements)
+  int64_t osb, osh, oss;  // output strides
+};
+
+struct RopeArgs {
+  RopeTensor t[2];  // q, k (k.H == 0 when absent)
+  int64_t B, S;
+  int half;          // D / 2
+  int chunks;        // half / VEC
+  int groups;        // ceil((Hq + Hk) / kHeadsPerThread)
+  float sgn;
+  // table mode
+  const void* cos;
+  const void* sin;
+  int64_t csb, csh, css, ssb, ssh, sss;
+  // position mode
+  const int64_t* pos;
+  int64_t psb, pss;
+  const float* inv_freq;
+};
+
+template <typename T, int N>
+__device__ __forceinline__ void load_any(const T* p, float* out) {
+  if constexpr (N * sizeof(T) >= 16 || N == 1) {
+    load_n<T, N>(p, out);
+  } else {
+#pragma unroll
+    for (int i = 0; i < N; ++i) out[i] = to_f32(p[i]);
+  }
+}
+
+template <typename T, int N>
+__device__ __forceinline__ void store_any(T* p, const float* in) {
+  if constexpr (N * sizeof(T) >= 16 || N == 1) {
+    store_n<T, N>(p, in);
+  } else {
+#pragma unroll
+    for (int i = 0; i < N; ++i) p[i] = from_f32<T>(in[i]);
+  }
+}
+
+// POS_MODE: cos/sin from positions; otherwise from tables of type TC.
+template <typename TX, typename TC, typename TO, int VEC, bool POS_MODE>
+__global__ __launch_bounds__(kThreads) void rope_kernel(const RopeArgs a) {
+  const int64_t per_group = a.B * a.S * a.chunks;
+  const int64_t gid = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (gid >= per_group * a.groups) return;
+  const int group = (int)(gid / per_group);
+  int64_t rem = gid - (int64_t)group * per_group;
+  const int chunk = (int)(rem % a.chunks);
+  rem /= a.chunks;
+  const int64_t s = rem % a.S;
+  const int64_t b = rem / a.S;
+  const int j0 = chunk * VEC;
+
+  float c_lo[VEC], c_hi[VEC], s_lo[VEC], s_hi[VEC];
+  const bool table_per_head = !POS_MODE && (a.csh != 0 || a.ssh != 0);
+  if constexpr (POS_MODE) {
+    const float p = (float)a.pos[b * a.psb + s * a.pss];
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      const float ang = p * a.inv_freq[j0 + e];
+      float sn, cs;
+      sincosf(ang, &sn, &cs);
+      c_lo[e] = c_hi[e] = cs;
+      s_lo[e] = s_hi[e] = sn * a.sgn;
+    }
+  }
+  auto load_table = [&](int64_t h) {
+    const TC* cp = static_cast<const TC*>(a.cos) + b * a.csb + h * a.csh + s * a.css + j0;
+    const TC* sp = static_cast<const TC*>(a.sin) + b * a.ssb + h * a.ssh + s * a.sss + j0;
+    load_any<TC, VEC>(cp, c_lo);
+    load_any<TC, VEC>(cp + a.half, c_hi);
+    load_any<TC, VEC>(sp, s_lo);
+    load_any<TC, VEC>(sp + a.half, s_hi);
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      s_lo[e] *= a.sgn;
+      s_hi[e] *= a.sgn;
+    }
+  };
+  if constexpr (!POS_MODE) {
+    if (!table_per_head) load_table(0);
+  }
+
+  const int64_t Hq = a.t[0].H;
+  const int64_t Htot = Hq + a.t[1].H;
+  const int64_t h_begin = (int64_t)group * kHeadsPerThread;
+  const int64_t h_end = (h_begin + kHeadsPerThread < Htot) ? h_begin + kHeadsPerThread : Htot;
+  for (int64_t vh = h_begin; vh < h_end; ++vh) {
+    const int ti = vh < Hq ? 0 : 1;
+    const RopeTensor& t = a.t[ti];
+    const int64_t h = vh - (ti ? Hq : 0);
+    if constexpr (!POS_MODE) {
+      if (table_per_head) load_table(h);
+    }
+    const TX* xp = static_cast<const TX*>(t.in) + b * t.sb + h * t.sh + s * t.ss + j0;
+    TO* yp = static_cast<TO*>(t.out) + b * t.osb + h * t.osh + s * t.oss + j0;
+    float x_lo[VEC], x_hi[VEC], y_lo[VEC], y_hi[VEC];
+    load_any<TX, VEC>(xp, x_lo);
+    load_any<TX, VEC>(xp + a.half, x_hi);
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      // x * cos + rotate_half(x) * sin, rotate_half([x1, x2]) = [-x2, x1]
+      y_lo[e] = x_lo[e] * c_lo[e] + (-x_hi[e]) * s_lo[e];
+      y_hi[e] = x_hi[e] * c_hi[e] + x_lo[e] * s_hi[e];
+    }
+    store_any<TO, VEC>(yp, y_lo);
+    store_any<TO, VEC>(yp + a.half, y_hi);
+  }
+}
+
+bool fill_tensor(RopeTensor& t, const void* in, void* out, const int64_t* g, int64_t& B,
+                 int64_t& S, bool first) {
+  t.in = in;
+  t.out = out;
+  t.H = g[1];
+  t.sb = g[3];
+  t.sh = g[4];
+  t.ss = g[5];
+  t.osb = g[6];
+  t.osh = g[7];
+  t.oss = g[8];
+  if (first) {
+    B = g[0];
+    S = g[2];
+    return true;
+  }
+  return g[0] == B && g[2] == S;
+}
+
+template <typename TX, typename TC, typename TO, bool POS_MODE>
+int launch_rope(RopeArgs& a, int64_t D, hipStream_t st) {
+  constexpr int V_FULL = vec16<TX>();
+  // Vector path: every 16-byte chunk of x / out / tables stays aligned.
+  bool vec_ok = (a.half % V_FULL) == 0;
+  for (int i = 0; i < 2 && vec_ok; ++i) {
+    const RopeTensor& t = a.t[i];
+    if (t.H == 0) continue;
+    vec_ok = aligned16(t.in) && aligned16(t.out) &&
+             ((t.sb | t.sh | t.ss) * (int64_t)sizeof(TX)) % 16 == 0 &&
+             ((t.osb | t.osh | t.oss) * (int64_t)sizeof(TO)) % 16 == 0;
+  }
+  if (!POS_MODE && vec_ok)
+    vec_ok = aligned16(a.cos) && aligned16(a.sin) &&
+             ((a.csb | a.csh | a.css | a.ssb | a.ssh | a.sss) * (int64_t)sizeof(TC)) % 16 == 0 &&
+             ((int64_t)a.half * (int64_t)sizeof(TC)) % 16 == 0;
+  const int vec = vec_ok ? V_FULL : 1;
+  a.chunks = a.half / vec;
+  const int64_t Htot = a.t[0].H + a.t[1].H;
+  a.groups = (int)((Htot + kHeadsPerThread - 1) / kHeadsPerThread);
+  const int64_t total = a.B * a.S * (int64_t)a.chunks * a.groups;
+  if (total == 0) return ML_OK;
+  const int64_t blocks = (total + kThreads - 1) / kThreads;
+  ML_CHECK(blocks <= 0x7fffffffLL, "rope: problem too large");
+  if (vec_ok)
+    rope_kernel<TX, TC, TO, V_FULL, POS_MODE><<<dim3((unsigned)blocks), kThreads, 0, st>>>(a);
+  else
+    rope_kernel<TX, TC, TO, 1, POS_MODE><<<dim3((unsigned)blocks), kThreads, 0, st>>>(a);
+  ML_LAUNCH_CHECK();
+  (void)D;
+  return ML_OK;
+}
+
+int setup_common(RopeArgs& a, const void* q, void* q_out, const int64_t* q_geom, const void* k,
+                 void* k_out, const int64_t* k_geom, int64_t D, float sgn) {
+  ML_CHECK(q_geom != nullptr, "rope: null q geometry");
+  ML_CHECK(D > 0 && D % 2 == 0, "rope: head dim must be even and positive (got %lld)",
+           (long long)D);
+  ML_CHECK(D / 2 <= 0x7fffffff, "rope: head dim too large");
+  a = RopeArgs{};
+  fill_tensor(a.t[0], q, q_out, q_geom, a.B, a.S, true);
+  if (k != nullptr) {
+    ML_CHECK(k_geom != nullptr, "rope: null k geometry");
+    ML_CHECK(fill_tensor(a.t[1], k, k_out, k_geom, a.B, a.S, false),
+             "rope: q and k must share batch and sequence sizes");
+  } else {
+    a.t[1] = RopeTensor{};
+  }
+  ML_CHECK(a.B >= 0 && a.S >= 0 && a.t[0].H >= 0 && a.t[1].H >= 0, "rope: negative size");
+  const int64_t elems = a.B * a.S * (a.t[0].H + a.t[1].H);
+  ML_CHECK(elems == 0 || (q && q_out), "rope: null tensor pointer");
+  ML_CHECK(k == nullptr || a.t[1].H == 0 || k_out != nullptr, "rope: null k output");
+  a.half = (int)(D / 2);
+  a.sgn = sgn;
+  return ML_OK;
+}
+
+}  // namespace
+}  // namespace mla
+
+using namespace mla;
+
+extern "C" int ml_rope_table(const void* q, void* q_out, const int64_t* q_geom, const void* k,
+                             void* k_out, const int64_t* k_geom, int64_t D, const void* cos,
+                             const void* sin, const int64_t* cs_geom, float sgn, int x_dtype,
+                             int cs_dtype, int out_dtype, void* stream) {
+  RopeArgs a;
+  int rc = setup_common(a, q, q_out, q_geom, k, k_out, k_geom, D, sgn);
+  if (rc) return rc;
+  ML_CHECK(cos && sin && cs_geom, "rope: null cos/sin");
+  a.cos = cos;
+  a.sin = sin;
+  a.csb = cs_geom[0];
+  a.csh = cs_geom[1];
+  a.css = cs_geom[2];
+  a.ssb = cs_geom[3];
+  a.ssh = cs_geom[4];
+  a.sss = cs_geom[5];
+  hipStream_t st = (hipStream_t)stream;
+  // Output dtype is torch's promotion: x's dtype when the tables match it,
+  // fp32 for any mixed pair of {fp32, bf16, fp16}.
+  const int expect_out = (x_dtype == cs_dtype) ? x_dtype : ML_F32;
+  ML_CHECK(out_dtype == expect_out,
+           "rope: output dtype %d is not the promotion of x dtype %d and table dtype %d",
+           out_dtype, x_dtype, cs_dtype);
+  return dispatch_dtype(x_dtype, [&](auto tx) -> int {
+    using TX = decltype(tx);
+    return dispatch_dtype(cs_dtype, [&](auto tc) -> int {
+      using TC = decltype(tc);
+      if constexpr (std::is_same<TX, TC>::value) {
+        return launch_rope<TX, TC, TX, false>(a, D, st);
+      } else {
+        return launch_rope<TX, TC, float, false>(a, D, st);
+      }
+    });
+  });
+}
+
+extern "C" int ml_rope_pos(const void* q, void* q_out, const int64_t* q_geom, const void* k,
+                           void* k_out, const int64_t* k_geom, int64_t D,
+                           const int64_t* positions, int64_t pos_sb, int64_t pos_ss,
+                           const float* inv_freq, float sgn, int x_dtype, void* stream) {
+  RopeArgs a;
+  int rc = setup_common(a, q, q_out, q_geom, k, k_out, k_geom, D, sgn);
+  if (rc) return rc;
+  ML_CHECK(positions && inv_freq, "rope: null positions / inv_freq");
+  a.pos = positions;
+  a.psb = pos_sb;
+  a.pss = pos_ss;
+  a.inv_freq = inv_freq;
+  hipStream_t st = (hipStream_t)stream;
+  return dispatch_dtype(x_dtype, [&](auto tx) -> int {
+    using TX = decltype(tx);
+    return launch_rope<TX, float, TX, true>(a, D, st);
+  });
+}

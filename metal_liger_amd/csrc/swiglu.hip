@@ -1,0 +1,195 @@
+// SwiGLU forward / backward for gfx950 (ops/fused_swiglu.py:26-50).
+//
+// Pure streaming kernels: 16-byte loads/stores, UNROLL independent 16-byte
+// chunks per thread in flight, grid sized to a few waves per SIMD and
+// striding over the tensor. sigmoid(gate) is recomputed in the backward
+// (the reference saved it as an extra fp32 tensor, ops/fused_swiglu.py:34;
+// recomputing it costs no HBM traffic). All math in fp32, products evaluated
+// in the reference's order with one rounding each.
+#include "common.h"
+
+#pragma clang fp contract(off)
+
+namespace mla {
+namespace {
+
+constexpr int kThreads = 256;
+
+// sigmoid(x) = 1 / (1 + e^-x) with the hardware exp2 and reciprocal
+// (each ~1 ulp); saturates correctly to 0 / 1 for large |x|.
+__device__ __forceinline__ float sigmoid_f(float x) {
+  const float e = __builtin_amdgcn_exp2f(-x * 1.4426950408889634f);
+  return __builtin_amdgcn_rcpf(1.0f + e);
+}
+
+template <typename T, int UNROLL>
+__global__ __launch_bounds__(kThreads) void swiglu_fwd_vec(const T* __restrict__ g,
+                                                            const T* __restrict__ u,
+                                                            T* __restrict__ o, int64_t nvec) {
+  constexpr int VEC = vec16<T>();
+  const int64_t stride = (int64_t)gridDim.x * kThreads * UNROLL;
+  for (int64_t base = (int64_t)blockIdx.x * kThreads * UNROLL + threadIdx.x; base < nvec;
+       base += stride) {
+    float gv[UNROLL][VEC], uv[UNROLL][VEC];
+#pragma unroll
+    for (int k = 0; k < UNROLL; ++k) {
+      const int64_t i = base + (int64_t)k * kThreads;
+      if (i < nvec) {
+        load_n<T, VEC>(g + i * VEC, gv[k]);
+        load_n<T, VEC>(u + i * VEC, uv[k]);
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < UNROLL; ++k) {
+      const int64_t i = base + (int64_t)k * kThreads;
+      if (i < nvec) {
+        float ov[VEC];
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) ov[e] = (gv[k][e] * sigmoid_f(gv[k][e])) * uv[k][e];
+        store_n<T, VEC>(o + i * VEC, ov);
+      }
+    }
+  }
+}
+
+template <typename T, int UNROLL>
+__global__ __launch_bounds__(kThreads) void swiglu_bwd_vec(
+    const T* __restrict__ g, const T* __restrict__ u, const T* __restrict__ dy,
+    T* __restrict__ dg, T* __restrict__ du, int64_t nvec) {
+  constexpr int VEC = vec16<T>();
+  const int64_t stride = (int64_t)gridDim.x * kThreads * UNROLL;
+  for (int64_t base = (int64_t)blockIdx.x * kThreads * UNROLL + threadIdx.x; base < nvec;
+       base += stride) {
+    float gv[UNROLL][VEC], uv[UNROLL][VEC], yv[UNROLL][VEC];
+#pragma unroll
+    for (int k = 0; k < UNROLL; ++k) {
+      const int64_t i = base + (int64_t)k * kThreads;
+      if (i < nvec) {
+        load_n<T, VEC>(g + i * VEC, gv[k]);
+        load_n<T, VEC>(u + i * VEC, uv[k]);
+        load_n<T, VEC>(dy + i * VEC, yv[k]);
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < UNROLL; ++k) {
+      const int64_t i = base + (int64_t)k * kThreads;
+      if (i < nvec) {
+        float dgv[VEC], duv[VEC];
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+          const float s = sigmoid_f(gv[k][e]);
+          duv[e] = yv[k][e] * (gv[k][e] * s);
+          dgv[e] = ((yv[k][e] * uv[k][e]) * s) * (1.0f + gv[k][e] * (1.0f - s));
+        }
+        store_n<T, VEC>(dg + i * VEC, dgv);
+        store_n<T, VEC>(du + i * VEC, duv);
+      }
+    }
+  }
+}
+
+// Scalar kernels for the unaligned case and the tail of the vector path.
+template <typename T>
+__global__ __launch_bounds__(kThreads) void swiglu_fwd_scalar(const T* __restrict__ g,
+                                                               const T* __restrict__ u,
+                                                               T* __restrict__ o, int64_t begin,
+                                                               int64_t n) {
+  for (int64_t i = begin + (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * kThreads) {
+    const float gv = to_f32(g[i]);
+    o[i] = from_f32<T>((gv * sigmoid_f(gv)) * to_f32(u[i]));
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(kThreads) void swiglu_bwd_scalar(
+    const T* __restrict__ g, const T* __restrict__ u, const T* __restrict__ dy,
+    T* __restrict__ dg, T* __restrict__ du, int64_t begin, int64_t n) {
+  for (int64_t i = begin + (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * kThreads) {
+    const float gv = to_f32(g[i]);
+    const float uv = to_f32(u[i]);
+    const float yv = to_f32(dy[i]);
+    const float s = sigmoid_f(gv);
+    du[i] = from_f32<T>(yv * (gv * s));
+    dg[i] = from_f32<T>(((yv * uv) * s) * (1.0f + gv * (1.0f - s)));
+  }
+}
+
+constexpr int kUnrollFwd = 4;
+constexpr int kUnrollBwd = 2;
+
+unsigned stream_grid(int64_t work_items, int per_block) {
+  const int64_t need = (work_items + per_block - 1) / per_block;
+  const int64_t cap = (int64_t)num_cus() * 16;  // ~16 blocks (64 waves) per CU in flight
+  const int64_t g = need < cap ? need : cap;
+  return (unsigned)(g < 1 ? 1 : g);
+}
+
+}  // namespace
+}  // namespace mla
+
+using namespace mla;
+
+extern "C" int ml_swiglu_fwd(const void* gate, const void* up, void* out, int64_t n, int dtype,
+                             void* stream) {
+  ML_CHECK(n >= 0, "swiglu: negative size");
+  if (n == 0) return ML_OK;
+  ML_CHECK(gate && up && out, "swiglu: null pointer");
+  hipStream_t st = (hipStream_t)stream;
+  return dispatch_dtype(dtype, [&](auto tv) -> int {
+    using T = decltype(tv);
+    constexpr int VEC = vec16<T>();
+    const T* g = static_cast<const T*>(gate);
+    const T* u = static_cast<const T*>(up);
+    T* o = static_cast<T*>(out);
+    int64_t done = 0;
+    if (aligned16(g) && aligned16(u) && aligned16(o)) {
+      const int64_t nvec = n / VEC;
+      if (nvec > 0) {
+        swiglu_fwd_vec<T, kUnrollFwd>
+            <<<stream_grid(nvec, kThreads * kUnrollFwd), kThreads, 0, st>>>(g, u, o, nvec);
+        ML_LAUNCH_CHECK();
+      }
+      done = nvec * VEC;
+    }
+    if (done < n) {
+      swiglu_fwd_scalar<T><<<stream_grid(n - done, kThreads), kThreads, 0, st>>>(g, u, o, done, n);
+      ML_LAUNCH_CHECK();
+    }
+    return ML_OK;
+  });
+}
+
+extern "C" int ml_swiglu_bwd(const void* gate, const void* up, const void* dy, void* dgate,
+                             void* dup, int64_t n, int dtype, void* stream) {
+  ML_CHECK(n >= 0, "swiglu backward: negative size");
+  if (n == 0) return ML_OK;
+  ML_CHECK(gate && up && dy && dgate && dup, "swiglu backward: null pointer");
+  hipStream_t st = (hipStream_t)stream;
+  return dispatch_dtype(dtype, [&](auto tv) -> int {
+    using T = decltype(tv);
+    constexpr int VEC = vec16<T>();
+    const T* g = static_cast<const T*>(gate);
+    const T* u = static_cast<const T*>(up);
+    const T* y = static_cast<const T*>(dy);
+    T* dg = static_cast<T*>(dgate);
+    T* du = static_cast<T*>(dup);
+    int64_t done = 0;
+    if (aligned16(g) && aligned16(u) && aligned16(y) && aligned16(dg) && aligned16(du)) {
+      const int64_t nvec = n / VEC;
+      if (nvec > 0) {
+        swiglu_bwd_vec<T, kUnrollBwd>
+            <<<stream_grid(nvec, kThreads * kUnrollBwd), kThreads, 0, st>>>(g, u, y, dg, du, nvec);
+        ML_LAUNCH_CHECK();
+      }
+      done = nvec * VEC;
+    }
+    if (done < n) {
+      swiglu_bwd_scalar<T>
+          <<<stream_grid(n - done, kThreads), kThreads, 0, st>>>(g, u, y, dg, du, done, n);
+      ML_LAUNCH_CHECK();
+    }
+    return ML_OK;
+  });
+}

@@ -1,0 +1,72 @@
+"""The C-ABI library: loads, exports every symbol include/*.h declares, and
+rejects bad arguments on the host (no GPU work is issued by these calls)."""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from metal_liger_amd import _hip
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def header_functions():
+    names = []
+    for h in sorted((ROOT / "include").glob("*.h")):
+        text = re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S)
+        names += re.findall(r"^\s*(?:const\s+)?[a-z_0-9]+\s*\*?\s*(ml_[a-z_0-9]+)\s*\(", text, flags=re.M)
+    return names
+
+
+def lib():
+    if not _hip.LIB_PATH.exists():
+        pytest.fail(f"{_hip.LIB_PATH} not built (run __graft_entry__.build())")
+    return _hip.lib()
+
+
+def test_header_declares_entry_points():
+    names = header_functions()
+    assert len(names) >= 9, names
+    assert "ml_last_error" in names and "ml_abi_version" in names
+
+
+def test_library_exports_every_declared_symbol():
+    L = lib()
+    missing = [n for n in header_functions() if not hasattr(L, n)]
+    assert not missing, f"not exported: {missing}"
+
+
+def test_python_bindings_cover_the_header():
+    assert set(header_functions()) == set(_hip.SIGNATURES)
+
+
+def test_abi_version():
+    assert lib().ml_abi_version() == _hip.ABI_VERSION
+
+
+def test_host_side_argument_errors():
+    L = lib()
+    # cols = 0 is rejected before any HIP call
+    rc = L.ml_rmsnorm_fwd(None, 0, None, None, 0, None, 4, 0, 1e-6, 0, 0, None)
+    assert rc == 1 and b"bad shape" in L.ml_last_error()
+    rc = L.ml_swiglu_fwd(None, None, None, 16, 0, None)
+    assert rc == 1 and b"null pointer" in L.ml_last_error()
+    rc = L.ml_swiglu_fwd(None, None, None, 16, 7, None)  # still null pointers first
+    assert rc == 1
+    g = _hip.geom([1, 1, 1, 0, 0, 0, 0, 0, 0])
+    rc = L.ml_rope_pos(None, None, g, None, None, None, 3, None, 0, 0, None, 1.0, 1, None)
+    assert rc == 1 and b"even" in L.ml_last_error()
+    with pytest.raises(RuntimeError, match="ml_swiglu_fwd"):
+        _hip.call("ml_swiglu_fwd", None, None, None, 16, 0, None)
+    assert L.ml_rmsnorm_bwd_workspace_bytes(8192, 2048) >= 8192 // 8 * 2048 * 4 // 8
+
+
+def test_unsupported_dtype_is_an_error():
+    L = lib()
+    buf = ctypes.create_string_buffer(64)
+    p = ctypes.cast(buf, ctypes.c_void_p)
+    # host pointers are fine here: the dtype check fails before any launch
+    rc = L.ml_swiglu_fwd(p, p, p, 4, 9, None)
+    assert rc == 1 and b"dtype" in L.ml_last_error()
