@@ -10,8 +10,9 @@ value = algorithmic bytes per step / time per step, where algorithmic bytes
 count each input read once and each output written once:
   SwiGLU fwd 3*N*I*2 + bwd 5*N*I*2 = 805,306,368 B
   RoPE   fwd (read + write q, k) + bwd (same) = 201,326,592 B
-roofline: the dominant kernel (SwiGLU backward, 503,316,480 B per launch)
-timed with HIP events on the stream it runs on, against 8 TB/s.
+roofline: the dominant kernel (SwiGLU backward, 503,316,480 B per launch),
+its average launch duration from HIP events on its stream around 20
+back-to-back launches, against 8 TB/s.
 cpu_baseline: the oracle (a CPU restatement of the reference's torch ops)
 on a bounded sample of the same workload, on the host's cores.
 
@@ -141,49 +142,56 @@ def main():
     torch.cuda.synchronize()
 
     stream = torch.cuda.current_stream(dev)
-    ev = {n: [] for n in ("swiglu_fwd", "swiglu_bwd", "rope_fwd", "rope_bwd")}
+    ops = {
+        "swiglu_fwd": lambda: hip_ops.swiglu_fwd(gate, up),
+        "swiglu_bwd": lambda: hip_ops.swiglu_bwd(gate, up, dy),
+        "rope_fwd": lambda: hip_ops.rope_pos(q, k, pos, inv, 1.0),
+        "rope_bwd": lambda: hip_ops.rope_pos(gq, gk, pos, inv, -1.0),
+    }
 
-    def step(record: bool):
-        marks = []
-        if record:
-            marks.append(torch.cuda.Event(enable_timing=True))
-            marks[-1].record(stream)
-        hip_ops.swiglu_fwd(gate, up)
-        if record:
-            marks.append(torch.cuda.Event(enable_timing=True))
-            marks[-1].record(stream)
-        hip_ops.swiglu_bwd(gate, up, dy)
-        if record:
-            marks.append(torch.cuda.Event(enable_timing=True))
-            marks[-1].record(stream)
-        hip_ops.rope_pos(q, k, pos, inv, 1.0)
-        if record:
-            marks.append(torch.cuda.Event(enable_timing=True))
-            marks[-1].record(stream)
-        hip_ops.rope_pos(gq, gk, pos, inv, -1.0)
-        if record:
-            marks.append(torch.cuda.Event(enable_timing=True))
-            marks[-1].record(stream)
-            for name, a, b in zip(ev, marks[:-1], marks[1:]):
-                ev[name].append((a, b))
+    def step():
+        for fn in ops.values():
+            fn()
 
     for _ in range(args.warmup):
-        step(False)
+        step()
     torch.cuda.synchronize()
+    # Timed region: exactly K steps, no per-kernel events (each event record
+    # inserts ~4.6 us of idle time between kernels on this GPU).
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
+    e0.record(stream)
     for _ in range(args.steps):
-        step(True)
+        step()
+    e1.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
+    gpu_ms_step = e0.elapsed_time(e1) / args.steps
+
+    # Per-kernel launch duration: events on the kernel's stream around a
+    # batch of back-to-back launches of that kernel alone.
+    reps = 20
+    per_op = {}
+    for name, fn in ops.items():
+        fn()
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for _ in range(reps):
+            fn()
+        b.record(stream)
+        torch.cuda.synchronize()
+        per_op[name] = a.elapsed_time(b) / reps
 
     ms_step = wall * 1e3 / args.steps
     value = STEP_BYTES / (wall / args.steps) / 1e9
-    per_op = {n: sum(a.elapsed_time(b) for a, b in v) / len(v) for n, v in ev.items()}
     op_bytes = {"swiglu_fwd": SWIGLU_FWD_BYTES, "swiglu_bwd": SWIGLU_BWD_BYTES,
                 "rope_fwd": ROPE_DIR_BYTES, "rope_bwd": ROPE_DIR_BYTES}
     breakdown = {n: {"us": round(per_op[n] * 1e3, 2),
                      "GB/s": round(op_bytes[n] / (per_op[n] * 1e-3) / 1e9, 1)}
                  for n in per_op}
+    breakdown["gpu_ms_per_step"] = round(gpu_ms_step, 4)
     dom_ms = per_op["swiglu_bwd"]
     achieved = SWIGLU_BWD_BYTES / (dom_ms * 1e-3) / 1e9
     roofline = {

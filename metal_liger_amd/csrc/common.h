@@ -112,6 +112,32 @@ __device__ __forceinline__ void store_n(T* __restrict__ p, const float* in) {
   }
 }
 
+// Same as store_n, with the non-temporal hint: streamed outputs that this
+// kernel never re-reads do not accumulate as dirty lines in the per-XCD L2
+// (which would otherwise be written back at the end of the kernel).
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
+
+template <typename T, int N>
+__device__ __forceinline__ void store_n_nt(T* __restrict__ p, const float* in) {
+  constexpr int P = (N * (int)sizeof(T) >= 16) ? 16 / (int)sizeof(T) : N;
+#pragma unroll
+  for (int i = 0; i < N; i += P) {
+    Pack<T, P> pk;
+#pragma unroll
+    for (int j = 0; j < P; ++j) pk.v[j] = from_f32<T>(in[i + j]);
+    if constexpr (sizeof(pk) == 16) {
+      __builtin_nontemporal_store(__builtin_bit_cast(u32x4_t, pk), reinterpret_cast<u32x4_t*>(p + i));
+    } else if constexpr (sizeof(pk) == 8) {
+      __builtin_nontemporal_store(__builtin_bit_cast(u32x2_t, pk), reinterpret_cast<u32x2_t*>(p + i));
+    } else if constexpr (sizeof(pk) == 4) {
+      __builtin_nontemporal_store(__builtin_bit_cast(unsigned int, pk), reinterpret_cast<unsigned int*>(p + i));
+    } else {
+      *reinterpret_cast<Pack<T, P>*>(p + i) = pk;
+    }
+  }
+}
+
 // ------------------------------------------------------------- reductions ---
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

@@ -27,6 +27,12 @@ constexpr int kBwdWaves = 8;        // waves per backward block
 constexpr int kMaxBwdBlocks = 512;  // dW partial rows
 constexpr int kGenericThreads = 256;
 
+// Column of chunk `it` for `lane`, clamped to the last valid chunk of the row.
+__device__ __forceinline__ int clamp_col(int it, int lane, int cols, int vec) {
+  const int c = (it * 64 + lane) * vec;
+  return c < cols ? c : cols - vec;
+}
+
 __device__ __forceinline__ float block_sum_256(float v, float* red /* [4] */) {
   v = wave_sum(v);
   const int wave = threadIdx.x >> 6;
@@ -47,13 +53,14 @@ __global__ __launch_bounds__(64 * kFwdWaves) void rms_fwd_reg(
   if (row >= rows) return;
   const TX* xr = x + row * ldx;
 
+  // Chunks past the row end load the last valid chunk (no branch around the
+  // load, so all ITERS loads are in flight together) and are zeroed after.
   float v[ITERS][VEC];
 #pragma unroll
+  for (int it = 0; it < ITERS; ++it) load_n<TX, VEC>(xr + clamp_col(it, lane, cols, VEC), v[it]);
+#pragma unroll
   for (int it = 0; it < ITERS; ++it) {
-    const int c = (it * 64 + lane) * VEC;
-    if (c < cols) {
-      load_n<TX, VEC>(xr + c, v[it]);
-    } else {
+    if ((it * 64 + lane) * VEC >= cols) {
 #pragma unroll
       for (int e = 0; e < VEC; ++e) v[it][e] = 0.f;
     }
@@ -76,7 +83,7 @@ __global__ __launch_bounds__(64 * kFwdWaves) void rms_fwd_reg(
       load_n<TW, VEC>(w + c, wv);
 #pragma unroll
       for (int e = 0; e < VEC; ++e) o[e] = (v[it][e] * r) * wv[e];
-      store_n<TX, VEC>(yr + c, o);
+      store_n_nt<TX, VEC>(yr + c, o);
     }
   }
 }
@@ -118,10 +125,8 @@ __global__ __launch_bounds__(64 * kBwdWaves) void rms_bwd_reg(
   constexpr bool W_IN_REGS = ITERS * VEC <= 32;
   float wv[W_IN_REGS ? ITERS : 1][VEC], acc[ITERS][VEC];
   auto load_w = [&](int it, float* dst) {
-    const int c = (it * 64 + lane) * VEC;
-    if (c < cols) {
-      load_n<TW, VEC>(w + c, dst);
-    } else {
+    load_n<TW, VEC>(w + clamp_col(it, lane, cols, VEC), dst);
+    if ((it * 64 + lane) * VEC >= cols) {
 #pragma unroll
       for (int e = 0; e < VEC; ++e) dst[e] = 0.f;
     }
@@ -141,11 +146,13 @@ __global__ __launch_bounds__(64 * kBwdWaves) void rms_bwd_reg(
     float xv[ITERS][VEC], gv[ITERS][VEC];
 #pragma unroll
     for (int it = 0; it < ITERS; ++it) {
-      const int c = (it * 64 + lane) * VEC;
-      if (c < cols) {
-        load_n<TX, VEC>(xr + c, xv[it]);
-        load_n<TX, VEC>(gr + c, gv[it]);
-      } else {
+      const int c = clamp_col(it, lane, cols, VEC);
+      load_n<TX, VEC>(xr + c, xv[it]);
+      load_n<TX, VEC>(gr + c, gv[it]);
+    }
+#pragma unroll
+    for (int it = 0; it < ITERS; ++it) {
+      if ((it * 64 + lane) * VEC >= cols) {
 #pragma unroll
         for (int e = 0; e < VEC; ++e) xv[it][e] = gv[it][e] = 0.f;
       }
@@ -190,7 +197,7 @@ __global__ __launch_bounds__(64 * kBwdWaves) void rms_bwd_reg(
       float o[VEC];
 #pragma unroll
       for (int e = 0; e < VEC; ++e) o[e] = gv[it][e] * r - (xv[it][e] * mean) * r3;
-      if (c < cols) store_n<TX, VEC>(dxr + c, o);
+      if (c < cols) store_n_nt<TX, VEC>(dxr + c, o);
     }
   }
 

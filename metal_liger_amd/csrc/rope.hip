@@ -3,11 +3,16 @@
 // One launch rotates q and k together. A thread owns one (b, s) position and
 // VEC consecutive pairs (j, j + D/2) of the head dimension, gets the VEC
 // cos/sin values once (from the tables, or computed in-kernel from the
-// position and inv_freq), then walks up to kHeadsPerThread heads of the
-// concatenated [q heads | k heads] list reusing them. Eight threads cover a
+// position and inv_freq), then rotates up to kHeadsPerThread heads of the
+// concatenated [q heads | k heads] list with them, issuing all of those
+// heads' loads before any arithmetic (measured on MI355X: 8 heads per
+// thread with hoisted loads moves the q+k config at 5.4 TB/s, against 3.8
+// TB/s for 4 heads loaded one at a time). Eight threads cover a
 // 128-wide head; a wave covers 8 consecutive positions, so each 16-byte
 // load/store instruction of a wave touches 2 KiB of contiguous rows for a
 // contiguous [B, H, S, D] tensor (and whole rows for HF's transposed views).
+#include <algorithm>
+
 #include "common.h"
 
 #pragma clang fp contract(off)
@@ -16,7 +21,7 @@ namespace mla {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kHeadsPerThread = 4;
+constexpr int kHeadsPerThread = 8;
 
 struct RopeTensor {
   const void* in;
@@ -64,73 +69,106 @@ __device__ __forceinline__ void store_any(T* p, const float* in) {
 }
 
 // POS_MODE: cos/sin from positions; otherwise from tables of type TC.
-template <typename TX, typename TC, typename TO, int VEC, bool POS_MODE>
+// IDX: int32_t when every element offset of every operand fits in 31 bits
+// (checked on the host), which halves the address registers per head.
+template <typename TX, typename TC, typename TO, int VEC, bool POS_MODE, typename IDX>
 __global__ __launch_bounds__(kThreads) void rope_kernel(const RopeArgs a) {
+  // blockIdx.y picks the head group, so head selection (q or k, strides)
+  // is uniform across the block and lives in scalar registers.
   const int64_t per_group = a.B * a.S * a.chunks;
   const int64_t gid = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-  if (gid >= per_group * a.groups) return;
-  const int group = (int)(gid / per_group);
-  int64_t rem = gid - (int64_t)group * per_group;
+  if (gid >= per_group) return;
+  const int group = (int)blockIdx.y;
+  int64_t rem = gid;
   const int chunk = (int)(rem % a.chunks);
   rem /= a.chunks;
-  const int64_t s = rem % a.S;
-  const int64_t b = rem / a.S;
+  const IDX s = (IDX)(rem % a.S);
+  const IDX b = (IDX)(rem / a.S);
   const int j0 = chunk * VEC;
 
-  float c_lo[VEC], c_hi[VEC], s_lo[VEC], s_hi[VEC];
+  const int64_t Hq = a.t[0].H;
+  const int64_t Htot = Hq + a.t[1].H;
+  const int64_t h_begin = (int64_t)group * kHeadsPerThread;
+
+  // Issue every head's loads before any math: up to 2 * kHeadsPerThread
+  // 16-byte loads in flight per thread, kept as raw packs until used. Heads
+  // past the end re-load the last head (no branch around the loads); their
+  // results are not stored.
+  Pack<TX, VEC> raw_lo[kHeadsPerThread], raw_hi[kHeadsPerThread];
+#pragma unroll
+  for (int t = 0; t < kHeadsPerThread; ++t) {
+    const int64_t vh = (h_begin + t < Htot) ? h_begin + t : Htot - 1;
+    {
+      const int ti = vh < Hq ? 0 : 1;
+      const RopeTensor& tt = a.t[ti];
+      const int64_t h = vh - (ti ? Hq : 0);
+      const TX* xp = static_cast<const TX*>(tt.in) + (b * (IDX)tt.sb + (IDX)h * (IDX)tt.sh + s * (IDX)tt.ss + j0);
+      raw_lo[t] = *reinterpret_cast<const Pack<TX, VEC>*>(xp);
+      raw_hi[t] = *reinterpret_cast<const Pack<TX, VEC>*>(xp + a.half);
+    }
+  }
+
+  // cos/sin are computed while the loads above are in flight.
+  float c_lo[VEC], s_lo[VEC];
+  float c_hi_t[POS_MODE ? 1 : VEC], s_hi_t[POS_MODE ? 1 : VEC];
+  // position mode duplicates the angle across the two halves (HF layout)
+  float* c_hi = POS_MODE ? c_lo : c_hi_t;
+  float* s_hi = POS_MODE ? s_lo : s_hi_t;
   const bool table_per_head = !POS_MODE && (a.csh != 0 || a.ssh != 0);
   if constexpr (POS_MODE) {
-    const float p = (float)a.pos[b * a.psb + s * a.pss];
+    const float p = (float)a.pos[(int64_t)b * a.psb + (int64_t)s * a.pss];
+    float invf[VEC];
+    load_any<float, VEC>(a.inv_freq + j0, invf);
 #pragma unroll
     for (int e = 0; e < VEC; ++e) {
-      const float ang = p * a.inv_freq[j0 + e];
+      const float ang = p * invf[e];
       float sn, cs;
       sincosf(ang, &sn, &cs);
-      c_lo[e] = c_hi[e] = cs;
-      s_lo[e] = s_hi[e] = sn * a.sgn;
+      c_lo[e] = cs;
+      s_lo[e] = sn * a.sgn;
     }
   }
   auto load_table = [&](int64_t h) {
-    const TC* cp = static_cast<const TC*>(a.cos) + b * a.csb + h * a.csh + s * a.css + j0;
-    const TC* sp = static_cast<const TC*>(a.sin) + b * a.ssb + h * a.ssh + s * a.sss + j0;
+    const TC* cp = static_cast<const TC*>(a.cos) + (b * (IDX)a.csb + (IDX)h * (IDX)a.csh + s * (IDX)a.css + j0);
+    const TC* sp = static_cast<const TC*>(a.sin) + (b * (IDX)a.ssb + (IDX)h * (IDX)a.ssh + s * (IDX)a.sss + j0);
     load_any<TC, VEC>(cp, c_lo);
     load_any<TC, VEC>(cp + a.half, c_hi);
     load_any<TC, VEC>(sp, s_lo);
     load_any<TC, VEC>(sp + a.half, s_hi);
 #pragma unroll
-    for (int e = 0; e < VEC; ++e) {
-      s_lo[e] *= a.sgn;
-      s_hi[e] *= a.sgn;
+    for (int e = 0; e < VEC; ++e) s_lo[e] *= a.sgn;
+    if constexpr (!POS_MODE) {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) s_hi[e] *= a.sgn;
     }
   };
   if constexpr (!POS_MODE) {
     if (!table_per_head) load_table(0);
   }
 
-  const int64_t Hq = a.t[0].H;
-  const int64_t Htot = Hq + a.t[1].H;
-  const int64_t h_begin = (int64_t)group * kHeadsPerThread;
-  const int64_t h_end = (h_begin + kHeadsPerThread < Htot) ? h_begin + kHeadsPerThread : Htot;
-  for (int64_t vh = h_begin; vh < h_end; ++vh) {
-    const int ti = vh < Hq ? 0 : 1;
-    const RopeTensor& t = a.t[ti];
-    const int64_t h = vh - (ti ? Hq : 0);
-    if constexpr (!POS_MODE) {
-      if (table_per_head) load_table(h);
-    }
-    const TX* xp = static_cast<const TX*>(t.in) + b * t.sb + h * t.sh + s * t.ss + j0;
-    TO* yp = static_cast<TO*>(t.out) + b * t.osb + h * t.osh + s * t.oss + j0;
-    float x_lo[VEC], x_hi[VEC], y_lo[VEC], y_hi[VEC];
-    load_any<TX, VEC>(xp, x_lo);
-    load_any<TX, VEC>(xp + a.half, x_hi);
 #pragma unroll
-    for (int e = 0; e < VEC; ++e) {
-      // x * cos + rotate_half(x) * sin, rotate_half([x1, x2]) = [-x2, x1]
-      y_lo[e] = x_lo[e] * c_lo[e] + (-x_hi[e]) * s_lo[e];
-      y_hi[e] = x_hi[e] * c_hi[e] + x_lo[e] * s_hi[e];
+  for (int t = 0; t < kHeadsPerThread; ++t) {
+    const int64_t vh = h_begin + t;
+    if (vh < Htot) {
+      const int ti = vh < Hq ? 0 : 1;
+      const RopeTensor& tt = a.t[ti];
+      const int64_t h = vh - (ti ? Hq : 0);
+      if constexpr (!POS_MODE) {
+        if (table_per_head) load_table(h);
+      }
+      TO* yp = static_cast<TO*>(tt.out) + (b * (IDX)tt.osb + (IDX)h * (IDX)tt.osh + s * (IDX)tt.oss + j0);
+      float y_lo[VEC], y_hi[VEC];
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        const float xl = to_f32(raw_lo[t].v[e]);
+        const float xh = to_f32(raw_hi[t].v[e]);
+        // x * cos + rotate_half(x) * sin, rotate_half([x1, x2]) = [-x2, x1]
+        y_lo[e] = xl * c_lo[e] + (-xh) * s_lo[e];
+        y_hi[e] = xh * c_hi[e] + xl * s_hi[e];
+      }
+      store_any<TO, VEC>(yp, y_lo);
+      store_any<TO, VEC>(yp + a.half, y_hi);
     }
-    store_any<TO, VEC>(yp, y_lo);
-    store_any<TO, VEC>(yp + a.half, y_hi);
   }
 }
 
@@ -165,6 +203,7 @@ int launch_rope(RopeArgs& a, int64_t D, hipStream_t st) {
              ((t.sb | t.sh | t.ss) * (int64_t)sizeof(TX)) % 16 == 0 &&
              ((t.osb | t.osh | t.oss) * (int64_t)sizeof(TO)) % 16 == 0;
   }
+  if (POS_MODE && vec_ok) vec_ok = aligned16(a.inv_freq);
   if (!POS_MODE && vec_ok)
     vec_ok = aligned16(a.cos) && aligned16(a.sin) &&
              ((a.csb | a.csh | a.css | a.ssb | a.ssh | a.sss) * (int64_t)sizeof(TC)) % 16 == 0 &&
@@ -173,16 +212,35 @@ int launch_rope(RopeArgs& a, int64_t D, hipStream_t st) {
   a.chunks = a.half / vec;
   const int64_t Htot = a.t[0].H + a.t[1].H;
   a.groups = (int)((Htot + kHeadsPerThread - 1) / kHeadsPerThread);
-  const int64_t total = a.B * a.S * (int64_t)a.chunks * a.groups;
-  if (total == 0) return ML_OK;
-  const int64_t blocks = (total + kThreads - 1) / kThreads;
-  ML_CHECK(blocks <= 0x7fffffffLL, "rope: problem too large");
-  if (vec_ok)
-    rope_kernel<TX, TC, TO, V_FULL, POS_MODE><<<dim3((unsigned)blocks), kThreads, 0, st>>>(a);
-  else
-    rope_kernel<TX, TC, TO, 1, POS_MODE><<<dim3((unsigned)blocks), kThreads, 0, st>>>(a);
+  const int64_t per_group = a.B * a.S * (int64_t)a.chunks;
+  if (per_group == 0 || a.groups == 0) return ML_OK;
+  const int64_t blocks = (per_group + kThreads - 1) / kThreads;
+  ML_CHECK(blocks <= 0x7fffffffLL && a.groups <= 65535, "rope: problem too large");
+  const dim3 grid((unsigned)blocks, (unsigned)a.groups);
+  // Largest element offset any thread forms (all strides are non-negative).
+  auto span = [](int64_t B, int64_t H, int64_t S, int64_t sb, int64_t sh, int64_t ss, int64_t D) {
+    return (B - 1) * sb + (H > 0 ? H - 1 : 0) * sh + (S - 1) * ss + D;
+  };
+  int64_t max_off = 0;
+  for (int i = 0; i < 2; ++i) {
+    const RopeTensor& t = a.t[i];
+    if (t.H == 0) continue;
+    max_off = std::max(max_off, span(a.B, t.H, a.S, t.sb, t.sh, t.ss, D));
+    max_off = std::max(max_off, span(a.B, t.H, a.S, t.osb, t.osh, t.oss, D));
+    if (!POS_MODE) {
+      max_off = std::max(max_off, span(a.B, t.H, a.S, a.csb, a.csh, a.css, D));
+      max_off = std::max(max_off, span(a.B, t.H, a.S, a.ssb, a.ssh, a.sss, D));
+    }
+  }
+  const bool small = max_off < ((int64_t)1 << 31);
+#define ML_ROPE(V, I) rope_kernel<TX, TC, TO, V, POS_MODE, I><<<grid, kThreads, 0, st>>>(a)
+  if (vec_ok) {
+    if (small) ML_ROPE(V_FULL, int32_t); else ML_ROPE(V_FULL, int64_t);
+  } else {
+    if (small) ML_ROPE(1, int32_t); else ML_ROPE(1, int64_t);
+  }
+#undef ML_ROPE
   ML_LAUNCH_CHECK();
-  (void)D;
   return ML_OK;
 }
 
