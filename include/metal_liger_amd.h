@@ -144,6 +144,66 @@ int ml_rope_pos(const void* q, void* q_out, const int64_t* q_geom, const void* k
                 const int64_t* k_geom, int64_t D, const int64_t* positions, int64_t pos_sb,
                 int64_t pos_ss, const float* inv_freq, float sgn, int x_dtype, void* stream);
 
+/* ------------------------------------------- fused linear cross-entropy (FLCE)
+ * Replaces _FusedLinearCrossEntropyFunction (ops/fused_linear_cross_entropy.py:
+ * 82-185) and its chunk loops (:39-80). bf16 hidden [n_tokens, hidden_size]
+ * (row stride ldh) and weight [vocab, hidden_size] (row stride ldw); optional
+ * bias [vocab] (fp32 or bf16, bias_dtype; NULL for none); int64 labels
+ * [n_tokens] where ignore_index marks ignored tokens. hidden_size and vocab
+ * must be multiples of 8.
+ *
+ * Forward: loss = sum_valid (lse - z_label) / max(#valid, 1) (fp32 scalar),
+ * lse fp32 [n_tokens], n_valid fp32 scalar (#valid tokens). No [tokens,
+ * vocab] tensor is ever allocated; the workspace holds per-row partials.
+ */
+size_t ml_flce_fwd_workspace_bytes(int64_t n_tokens, int64_t vocab);
+int ml_flce_fwd(const void* hidden, int64_t ldh, const void* weight, int64_t ldw, const void* bias,
+                int bias_dtype, const int64_t* labels, int64_t n_tokens, int64_t vocab,
+                int64_t hidden_size, int64_t ignore_index, float* loss, float* lse, float* n_valid,
+                void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Backward for d(loss) = *grad_loss (device fp32 scalar): d_hidden bf16
+ * [n_tokens, hidden_size] and d_weight bf16 [vocab, hidden_size] (dense),
+ * either may be NULL to skip it (a frozen lm_head skips the dW GEMMs). chunk
+ * (multiple of 8) is the vocabulary slice whose bf16 dlogits are held at once:
+ * the workspace is n_tokens * chunk * 2 bytes (+ an fp32 dH accumulator).
+ * No bias gradient, as in the reference.
+ */
+size_t ml_flce_bwd_workspace_bytes(int64_t n_tokens, int64_t hidden_size, int64_t chunk,
+                                   int need_dhidden);
+int ml_flce_bwd(const void* hidden, int64_t ldh, const void* weight, int64_t ldw, const void* bias,
+                int bias_dtype, const int64_t* labels, int64_t n_tokens, int64_t vocab,
+                int64_t hidden_size, int64_t ignore_index, const float* lse, const float* n_valid,
+                const float* grad_loss, int64_t chunk, void* d_hidden, void* d_weight,
+                void* workspace, size_t workspace_bytes, void* stream);
+
+/* --------------------------------------------------------------------- GEMM
+ * bf16 MFMA GEMM (fp32 accumulation): C = alpha * A B + beta * C.
+ * No reference counterpart: the reference's contractions are torch.mm /
+ * F.linear calls inside ops/fused_linear_cross_entropy.py:44,64,78-79 and
+ * ops/fused_lora.py:79-81,142-161,228-258; this is the engine those paths
+ * run on here, exported for tests and for callers that need a plain product.
+ *
+ * a_layout 0: A is [M, K] row-major (element (m, k) at A[m * lda + k]);
+ *          1: A is stored transposed, [K, M] row-major (A[k * lda + m]).
+ * b_layout 0: B is stored transposed, [N, K] row-major (an nn.Linear weight);
+ *          1: B is [K, N] row-major.
+ * K (and every segment length) must be a multiple of 8, leading dimensions
+ * multiples of 8, pointers 16-byte aligned, and M (N) a multiple of 8 when A
+ * (B) is stored transposed. C is fp32 or bf16 (c_dtype), row-major with ldc.
+ */
+int ml_gemm_bf16(int64_t M, int64_t N, int64_t K, const void* A, int64_t lda, int a_layout,
+                 const void* B, int64_t ldb, int b_layout, void* C, int64_t ldc, int c_dtype,
+                 float alpha, float beta, void* stream);
+
+/* Same product with K split into nseg (1..4) segments, segment s pairing
+ * A_s (lda_s) with B_s (ldb_s) over k_lens[s]: C = alpha * sum_s A_s B_s + beta * C. */
+int ml_gemm_bf16_segments(int64_t M, int64_t N, int nseg, const int64_t* k_lens,
+                          const void* const* a_ptrs, const int64_t* ldas, const void* const* b_ptrs,
+                          const int64_t* ldbs, int a_layout, int b_layout, void* C, int64_t ldc,
+                          int c_dtype, float alpha, float beta, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

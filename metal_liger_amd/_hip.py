@@ -49,6 +49,26 @@ SIGNATURES: dict[str, tuple] = {
         _i32,
         [_p, _p, _i64p, _p, _p, _i64p, _i64, _p, _i64, _i64, _p, _f32, _i32, _p],
     ),
+    "ml_gemm_bf16": (
+        _i32,
+        [_i64, _i64, _i64, _p, _i64, _i32, _p, _i64, _i32, _p, _i64, _i32, _f32, _f32, _p],
+    ),
+    "ml_gemm_bf16_segments": (
+        _i32,
+        [_i64, _i64, _i32, _i64p, ctypes.POINTER(_p), _i64p, ctypes.POINTER(_p), _i64p, _i32, _i32,
+         _p, _i64, _i32, _f32, _f32, _p],
+    ),
+    "ml_flce_fwd_workspace_bytes": (_sz, [_i64, _i64]),
+    "ml_flce_fwd": (
+        _i32,
+        [_p, _i64, _p, _i64, _p, _i32, _p, _i64, _i64, _i64, _i64, _p, _p, _p, _p, _sz, _p],
+    ),
+    "ml_flce_bwd_workspace_bytes": (_sz, [_i64, _i64, _i64, _i32]),
+    "ml_flce_bwd": (
+        _i32,
+        [_p, _i64, _p, _i64, _p, _i32, _p, _i64, _i64, _i64, _i64, _p, _p, _p, _i64, _p, _p, _p,
+         _sz, _p],
+    ),
 }
 
 ABI_VERSION = 1
@@ -110,6 +130,10 @@ def ptr(t: torch.Tensor | None) -> int | None:
 def geom(vals) -> ctypes.Array:
     arr = (ctypes.c_int64 * len(vals))(*[int(v) for v in vals])
     return arr
+
+
+def ptrs(vals) -> ctypes.Array:
+    return (ctypes.c_void_p * len(vals))(*[v for v in vals])
 
 
 def stream_of(t: torch.Tensor) -> int:

@@ -263,3 +263,119 @@ def rope_pos(q: torch.Tensor, k: torch.Tensor | None, positions: torch.Tensor,
         dtype_tag(q, "q"), stream_of(q),
     )
     return o4s[0], (o4s[1] if k is not None else None)
+
+
+# -------------------------------------------------------------------- GEMM --
+
+
+def _gemm_operand(t: torch.Tensor, what: str) -> torch.Tensor:
+    if t.dtype != torch.bfloat16:
+        raise TypeError(f"gemm: {what} must be bfloat16 (got {t.dtype})")
+    if t.dim() != 2:
+        raise ValueError(f"gemm: {what} must be 2-D")
+    if t.stride(1) != 1 or t.stride(0) % 8 != 0 or t.data_ptr() % 16 != 0:
+        t = t.contiguous()
+    return t
+
+
+def matmul(a: torch.Tensor, b: torch.Tensor, *, a_t: bool = False, b_t: bool = False,
+           out: torch.Tensor | None = None, out_dtype: torch.dtype = torch.float32,
+           alpha: float = 1.0, beta: float = 0.0) -> torch.Tensor:
+    """op(a) @ op(b) on the MFMA engine, op(x) = x.T when the flag is set.
+
+    a: [M, K] (or [K, M] with a_t); b: [K, N] (or [N, K] with b_t, an
+    nn.Linear weight). bf16 inputs, fp32 accumulation; out fp32 or bf16.
+    With out given, computes out = alpha * op(a) op(b) + beta * out.
+    """
+    ensure_rocm_device(a, b, out)
+    a = _gemm_operand(a, "a")
+    b = _gemm_operand(b, "b")
+    M, K = (a.shape[1], a.shape[0]) if a_t else (a.shape[0], a.shape[1])
+    Kb, N = (b.shape[1], b.shape[0]) if b_t else (b.shape[0], b.shape[1])
+    if K != Kb:
+        raise ValueError(f"gemm: inner dimensions differ ({K} vs {Kb})")
+    if out is None:
+        out = torch.empty(M, N, dtype=out_dtype, device=a.device)
+        beta = 0.0
+    elif out.shape != (M, N) or out.stride(1) != 1:
+        raise ValueError("gemm: out must be a row-major [M, N] tensor")
+    call(
+        "ml_gemm_bf16", M, N, K, ptr(a), a.stride(0), 1 if a_t else 0, ptr(b), b.stride(0),
+        0 if b_t else 1, ptr(out), out.stride(0), dtype_tag(out, "out"), float(alpha), float(beta),
+        stream_of(a),
+    )
+    return out
+
+
+# -------------------------------------------------------------------- FLCE --
+
+
+def _flce_operands(hidden, weight, labels, bias):
+    ensure_rocm_device(hidden, weight, labels, bias)
+    if hidden.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16:
+        raise TypeError(
+            "fused linear cross-entropy runs bf16 MFMA GEMMs: hidden and weight must be bfloat16 "
+            f"(got {hidden.dtype}, {weight.dtype})"
+        )
+    if hidden.dim() != 2 or weight.dim() != 2 or hidden.shape[1] != weight.shape[1]:
+        raise ValueError(f"flce: hidden {tuple(hidden.shape)} / weight {tuple(weight.shape)} mismatch")
+    if labels.shape != (hidden.shape[0],):
+        raise ValueError(f"flce: labels shape {tuple(labels.shape)} != ({hidden.shape[0]},)")
+
+    def rowmajor(t):
+        ok = t.stride(1) == 1 and t.stride(0) % 8 == 0 and t.data_ptr() % 16 == 0
+        return t if ok and t.shape[0] > 0 else t.contiguous()
+
+    hidden = rowmajor(hidden)
+    weight = rowmajor(weight)
+    labels = labels.to(torch.int64).contiguous()
+    if bias is not None:
+        if bias.shape != (weight.shape[0],):
+            raise ValueError("flce: bias must be [vocab]")
+        bias = bias if bias.dtype in (torch.float32, torch.bfloat16) else bias.float()
+        bias = bias.contiguous()
+    return hidden, weight, labels, bias
+
+
+def flce_fwd(hidden, weight, labels, bias=None, ignore_index: int = -100):
+    """Returns (loss 0-d fp32, lse [N] fp32, n_valid [1] fp32)."""
+    hidden, weight, labels, bias = _flce_operands(hidden, weight, labels, bias)
+    N, H = hidden.shape
+    V = weight.shape[0]
+    dev = hidden.device
+    loss = torch.empty((), dtype=torch.float32, device=dev)
+    lse = torch.empty(N, dtype=torch.float32, device=dev)
+    n_valid = torch.empty(1, dtype=torch.float32, device=dev)
+    wsb = _hip.query("ml_flce_fwd_workspace_bytes", N, V)
+    ws = torch.empty(max(wsb, 16), dtype=torch.uint8, device=dev)
+    call(
+        "ml_flce_fwd", ptr(hidden), hidden.stride(0) if N > 0 else H, ptr(weight), weight.stride(0),
+        ptr(bias), dtype_tag(bias, "bias") if bias is not None else 0, ptr(labels), N, V, H,
+        int(ignore_index), ptr(loss), ptr(lse), ptr(n_valid), ptr(ws), ws.numel(), stream_of(weight),
+    )
+    return loss, lse, n_valid
+
+
+def flce_bwd(hidden, weight, labels, bias, ignore_index, lse, n_valid, grad_loss, chunk_size,
+             need_dhidden=True, need_dweight=True):
+    """Returns (d_hidden bf16 or None, d_weight bf16 or None)."""
+    hidden, weight, labels, bias = _flce_operands(hidden, weight, labels, bias)
+    N, H = hidden.shape
+    V = weight.shape[0]
+    dev = hidden.device
+    g = grad_loss.detach().to(device=dev, dtype=torch.float32).reshape(1).contiguous()
+    dh = torch.empty(N, H, dtype=torch.bfloat16, device=dev) if need_dhidden else None
+    dw = torch.empty(V, H, dtype=torch.bfloat16, device=dev) if need_dweight else None
+    if dh is None and dw is None:
+        return None, None
+    chunk = int(chunk_size)
+    chunk = max(8, (min(chunk, V) + 7) // 8 * 8)
+    wsb = _hip.query("ml_flce_bwd_workspace_bytes", N, H, chunk, 1 if need_dhidden else 0)
+    ws = torch.empty(max(wsb, 16), dtype=torch.uint8, device=dev)
+    call(
+        "ml_flce_bwd", ptr(hidden), hidden.stride(0) if N > 0 else H, ptr(weight), weight.stride(0),
+        ptr(bias), dtype_tag(bias, "bias") if bias is not None else 0, ptr(labels), N, V, H,
+        int(ignore_index), ptr(lse), ptr(n_valid), ptr(g), chunk, ptr(dh), ptr(dw), ptr(ws),
+        ws.numel(), stream_of(weight),
+    )
+    return dh, dw

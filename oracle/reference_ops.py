@@ -121,8 +121,8 @@ def flce_forward(hidden: torch.Tensor, weight: torch.Tensor, labels: torch.Tenso
     N = hidden.shape[0]
     hf = hidden.float()
     wf = weight.float()
-    run_max = torch.full((N,), float("-inf"), dtype=torch.float32)
-    run_sum = torch.zeros(N, dtype=torch.float32)
+    run_max = torch.full((N,), float("-inf"), dtype=torch.float32, device=hidden.device)
+    run_sum = torch.zeros(N, dtype=torch.float32, device=hidden.device)
     for lo in range(0, V, chunk_size):
         hi = min(lo + chunk_size, V)
         bc = bias[lo:hi].float() if bias is not None else None
@@ -155,14 +155,14 @@ def flce_backward(hidden: torch.Tensor, weight: torch.Tensor, labels: torch.Tens
     n_valid = torch.clamp(mask.sum().float(), min=1.0)
     dh = torch.zeros_like(hf)
     dw = torch.zeros_like(wf)
-    scale = grad_out.float() / n_valid
+    scale = grad_out.float().to(hidden.device) / n_valid
     m2 = mask.float().unsqueeze(-1)
     for lo in range(0, V, chunk_size):
         hi = min(lo + chunk_size, V)
         wc = wf[lo:hi]
         bc = bias[lo:hi].float() if bias is not None else None
         p = (F.linear(hf, wc, bc) - lse.unsqueeze(-1)).exp()
-        cls = torch.arange(lo, hi, dtype=labels.dtype).unsqueeze(0)
+        cls = torch.arange(lo, hi, dtype=labels.dtype, device=labels.device).unsqueeze(0)
         p = torch.where(labels.unsqueeze(1) == cls, p - 1.0, p)
         p = p * m2 * scale
         dh.addmm_(p, wc)
