@@ -178,6 +178,46 @@ int ml_flce_bwd(const void* hidden, int64_t ldh, const void* weight, int64_t ldw
                 const float* grad_loss, int64_t chunk, void* d_hidden, void* d_weight,
                 void* workspace, size_t workspace_bytes, void* stream);
 
+/* ----------------------------------------------------------- fused LoRA bwd
+ * Replaces _LoRA_QKV.backward (ops/fused_lora.py:121-171). Three adapters
+ * (q, k, v) share the saved input X [n_tokens, in_features] (bf16). For
+ * adapter i: dY[i] [n_tokens, out_features[i]], base W[i] [out, in], B[i]
+ * [out, rank] (bf16), scale[i] a HOST float (PEFT's lora_alpha / r).
+ * A_stack [3 rank, in] stacks A_q, A_k, A_v (bf16); XA [n_tokens, 3 rank] is
+ * X A_stack^T from the forward. Outputs: dX bf16 [n_tokens, in];
+ * dA fp32 [3 rank, in] (dA_q, dA_k, dA_v stacked); dB[i] fp32 [out, rank].
+ * in_features, out_features and rank must be multiples of 8. No gradient
+ * for the frozen base weights, as in the reference.
+ */
+size_t ml_lora_qkv_bwd_workspace_bytes(int64_t n_tokens, int64_t in_features,
+                                       const int64_t* out_features, int64_t rank);
+int ml_lora_qkv_bwd(const void* X, int64_t n_tokens, int64_t in_features, const void* const* dY,
+                    const int64_t* out_features, const void* const* W, const void* A_stack,
+                    const void* const* B, const float* scale, const void* XA, int64_t rank,
+                    void* dX, float* dA, float* const* dB, void* workspace, size_t workspace_bytes,
+                    void* stream);
+
+/*
+ * Replaces _LoRA_MLP.backward (ops/fused_lora.py:209-266): SwiGLU MLP with
+ * LoRA on gate / up / down. Saved from the forward (bf16): X [n, hidden],
+ * gate / up / h [n, intermediate], XA_GU = X [A_G; A_U]^T [n, 2 rank],
+ * hA_D = h A_D^T [n, rank]. Weights: WG, WU [intermediate, hidden], WD
+ * [hidden, intermediate], A_GU [2 rank, hidden] (A_G; A_U), A_D [rank,
+ * intermediate], BG, BU [intermediate, rank], BD [hidden, rank]; scale = HOST
+ * floats {s_G, s_U, s_D}. Outputs: dX bf16 [n, hidden]; fp32 dA_GU [2 rank,
+ * hidden], dA_D [rank, intermediate], dB_G, dB_U [intermediate, rank], dB_D
+ * [hidden, rank]. The SwiGLU backward runs in the dH GEMM's epilogue.
+ */
+size_t ml_lora_mlp_bwd_workspace_bytes(int64_t n_tokens, int64_t hidden, int64_t intermediate,
+                                       int64_t rank);
+int ml_lora_mlp_bwd(const void* X, int64_t n_tokens, int64_t hidden, int64_t intermediate,
+                    const void* gate, const void* up, const void* h, const void* dY, const void* WG,
+                    const void* WU, const void* WD, const void* A_GU, const void* A_D,
+                    const void* BG, const void* BU, const void* BD, const float* scale,
+                    const void* XA_GU, const void* hA_D, int64_t rank, void* dX, float* dA_GU,
+                    float* dA_D, float* dB_G, float* dB_U, float* dB_D, void* workspace,
+                    size_t workspace_bytes, void* stream);
+
 /* --------------------------------------------------------------------- GEMM
  * bf16 MFMA GEMM (fp32 accumulation): C = alpha * A B + beta * C.
  * No reference counterpart: the reference's contractions are torch.mm /
@@ -203,6 +243,16 @@ int ml_gemm_bf16_segments(int64_t M, int64_t N, int nseg, const int64_t* k_lens,
                           const void* const* a_ptrs, const int64_t* ldas, const void* const* b_ptrs,
                           const int64_t* ldbs, int a_layout, int b_layout, void* C, int64_t ldc,
                           int c_dtype, float alpha, float beta, void* stream);
+
+/* Split-K form with a tile shape (tile_cfg 0: 256x256, 1: 256x32 for
+ * rank-r outputs, 2: 64x256 for few-row outputs): ksplit slices of K write
+ * fp32 partials to `workspace` (ml_gemm_splitk_workspace_bytes), summed in a
+ * fixed order into C = alpha * A B + beta * C. Same operand rules as above. */
+size_t ml_gemm_splitk_workspace_bytes(int64_t M, int64_t N, int64_t K, int ksplit);
+int ml_gemm_bf16_splitk(int64_t M, int64_t N, int64_t K, const void* A, int64_t lda, int a_layout,
+                        const void* B, int64_t ldb, int b_layout, void* C, int64_t ldc, int c_dtype,
+                        float alpha, float beta, int tile_cfg, int ksplit, void* workspace,
+                        size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

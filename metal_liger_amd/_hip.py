@@ -69,6 +69,24 @@ SIGNATURES: dict[str, tuple] = {
         [_p, _i64, _p, _i64, _p, _i32, _p, _i64, _i64, _i64, _i64, _p, _p, _p, _i64, _p, _p, _p,
          _sz, _p],
     ),
+    "ml_gemm_splitk_workspace_bytes": (_sz, [_i64, _i64, _i64, _i32]),
+    "ml_gemm_bf16_splitk": (
+        _i32,
+        [_i64, _i64, _i64, _p, _i64, _i32, _p, _i64, _i32, _p, _i64, _i32, _f32, _f32, _i32, _i32,
+         _p, _sz, _p],
+    ),
+    "ml_lora_qkv_bwd_workspace_bytes": (_sz, [_i64, _i64, _i64p, _i64]),
+    "ml_lora_qkv_bwd": (
+        _i32,
+        [_p, _i64, _i64, ctypes.POINTER(_p), _i64p, ctypes.POINTER(_p), _p, ctypes.POINTER(_p),
+         ctypes.POINTER(_f32), _p, _i64, _p, _p, ctypes.POINTER(_p), _p, _sz, _p],
+    ),
+    "ml_lora_mlp_bwd_workspace_bytes": (_sz, [_i64, _i64, _i64, _i64]),
+    "ml_lora_mlp_bwd": (
+        _i32,
+        [_p, _i64, _i64, _i64, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p,
+         ctypes.POINTER(_f32), _p, _p, _i64, _p, _p, _p, _p, _p, _p, _p, _sz, _p],
+    ),
 }
 
 ABI_VERSION = 1
@@ -134,6 +152,10 @@ def geom(vals) -> ctypes.Array:
 
 def ptrs(vals) -> ctypes.Array:
     return (ctypes.c_void_p * len(vals))(*[v for v in vals])
+
+
+def floats(vals) -> ctypes.Array:
+    return (ctypes.c_float * len(vals))(*[float(v) for v in vals])
 
 
 def stream_of(t: torch.Tensor) -> int:

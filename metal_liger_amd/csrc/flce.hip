@@ -59,7 +59,7 @@ struct EpiLse {
   int M, V, nblk;
 
   __device__ __forceinline__ void operator()(f32x16_t (&acc)[kTM][kTN], int m0, int n0, int lane,
-                                             char*) const {
+                                             char*, int) const {
     // a wave whose 128 columns all lie past the vocabulary (second half of
     // the last tile) owns no partial slot
     if (n0 >= V) return;
@@ -182,7 +182,7 @@ struct EpiDlogit {
   int64_t c0;
 
   __device__ __forceinline__ void operator()(f32x16_t (&acc)[kTM][kTN], int m0, int n0, int lane,
-                                             char*) const {
+                                             char*, int) const {
     const int col = lane & 31;
     const float scale = grad[0] / fmaxf(n_valid[0], 1.0f);
     float bj[kTN];
@@ -284,10 +284,10 @@ int fwd_impl(const bf16* hidden, int64_t ldh, const bf16* weight, int64_t ldw, c
 
   Segment seg{{hidden, ldh}, {weight, ldw}, H};
   Problem pb;
-  int rc = make_problem(pb, M, V, 1, &seg, kKMajor, kKMajor, 0);
+  int rc = make_problem<BigCfg>(pb, M, V, 1, &seg, kKMajor, kKMajor, 0);
   if (rc) return rc;
   EpiLse<TB> epi{bias, labels, w.pmax, w.psum, w.zy, M, V, nblk};
-  gemm_kernel<kKMajor, kKMajor, EpiLse<TB>><<<dim3(grid_blocks(pb)), kThreads, 0, st>>>(pb, epi);
+  gemm_kernel<BigCfg, kKMajor, kKMajor, EpiLse<TB>><<<dim3(grid_blocks(pb)), kThreads, 0, st>>>(pb, epi);
   ML_LAUNCH_CHECK();
   lse_reduce_kernel<<<dim3((M + 3) / 4), 256, 0, st>>>(w.pmax, w.psum, nblk, w.zy, labels, ignore,
                                                        M, V, lse, w.loss_row, w.valid_row);
@@ -311,18 +311,18 @@ int bwd_impl(const bf16* hidden, int64_t ldh, const bf16* weight, int64_t ldw, c
     {  // 1. dlogits of this chunk
       Segment seg{{hidden, ldh}, {wc, ldw}, H};
       Problem pb;
-      int rc = make_problem(pb, M, C, 1, &seg, kKMajor, kKMajor, 0);
+      int rc = make_problem<BigCfg>(pb, M, C, 1, &seg, kKMajor, kKMajor, 0);
       if (rc) return rc;
       EpiDlogit<TB> epi{bias ? bias + c0 : nullptr, labels, ignore, lse, grad, n_valid, D,
                         (int64_t)chunk, M, C, (int64_t)c0};
-      gemm_kernel<kKMajor, kKMajor, EpiDlogit<TB>>
+      gemm_kernel<BigCfg, kKMajor, kKMajor, EpiDlogit<TB>>
           <<<dim3(grid_blocks(pb)), kThreads, 0, st>>>(pb, epi);
       ML_LAUNCH_CHECK();
     }
     if (dh32) {  // 2. dH (+)= D W_c
       Segment seg{{D, (int64_t)chunk}, {wc, ldw}, C};
       Problem pb;
-      int rc = make_problem(pb, M, H, 1, &seg, kKMajor, kMNMajor, 0);
+      int rc = make_problem<BigCfg>(pb, M, H, 1, &seg, kKMajor, kMNMajor, 0);
       if (rc) return rc;
       rc = launch_store<float>(pb, kKMajor, kMNMajor, dh32, H, 1.0f, c0 > 0 ? 1.0f : 0.0f, st);
       if (rc) return rc;
@@ -330,7 +330,7 @@ int bwd_impl(const bf16* hidden, int64_t ldh, const bf16* weight, int64_t ldw, c
     if (d_weight) {  // 3. dW_c = D^T H
       Segment seg{{D, (int64_t)chunk}, {hidden, ldh}, M};
       Problem pb;
-      int rc = make_problem(pb, C, H, 1, &seg, kMNMajor, kMNMajor, 0);
+      int rc = make_problem<BigCfg>(pb, C, H, 1, &seg, kMNMajor, kMNMajor, 0);
       if (rc) return rc;
       rc = launch_store<bf16>(pb, kMNMajor, kMNMajor, d_weight + (int64_t)c0 * H, H, 1.0f, 0.0f,
                               st);

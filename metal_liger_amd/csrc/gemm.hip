@@ -16,11 +16,39 @@ int run(int64_t M, int64_t N, int nseg, const Segment* segs, int la, int lb, voi
   ML_CHECK(C != nullptr && ldc >= N, "gemm: bad C (ldc %lld < N %lld)", (long long)ldc,
            (long long)N);
   Problem pb;
-  int rc = make_problem(pb, (int)M, (int)N, nseg, segs, la, lb, 0);
+  int rc = make_problem<BigCfg>(pb, (int)M, (int)N, nseg, segs, la, lb, 0);
   if (rc) return rc;
   hipStream_t st = (hipStream_t)stream;
   if (c_dtype == ML_F32) return launch_store<float>(pb, la, lb, C, ldc, alpha, beta, st);
   if (c_dtype == ML_BF16) return launch_store<bf16>(pb, la, lb, C, ldc, alpha, beta, st);
+  set_error("gemm: C dtype %d not supported (fp32 or bf16)", c_dtype);
+  return ML_ERR_INVALID;
+}
+
+// Split-K / tile-shape variant (cfg 0: 256x256, 1: 256x32, 2: 64x256).
+template <class C, typename TC>
+int run_splitk_cfg(const Problem& pb, int la, int lb, float* ws, TC* out, int64_t ldo, float alpha,
+                   float beta, hipStream_t st) {
+  if (la == kKMajor && lb == kKMajor) return launch_splitk<C, kKMajor, kKMajor, TC>(pb, ws, out, ldo, alpha, beta, st);
+  if (la == kKMajor && lb == kMNMajor) return launch_splitk<C, kKMajor, kMNMajor, TC>(pb, ws, out, ldo, alpha, beta, st);
+  if (la == kMNMajor && lb == kKMajor) return launch_splitk<C, kMNMajor, kKMajor, TC>(pb, ws, out, ldo, alpha, beta, st);
+  return launch_splitk<C, kMNMajor, kMNMajor, TC>(pb, ws, out, ldo, alpha, beta, st);
+}
+
+template <class C>
+int run_splitk(int64_t M, int64_t N, const Segment& seg, int la, int lb, int ksplit, void* C_,
+               int64_t ldc, int c_dtype, float alpha, float beta, void* ws, size_t ws_bytes,
+               hipStream_t st) {
+  Problem pb;
+  int rc = make_problem<C>(pb, (int)M, (int)N, 1, &seg, la, lb, 0, ksplit);
+  if (rc) return rc;
+  ML_CHECK(ws && ws_bytes >= splitk_ws_bytes(pb), "gemm: split-K workspace too small (%zu < %zu)",
+           ws_bytes, splitk_ws_bytes(pb));
+  float* w = static_cast<float*>(ws);
+  if (c_dtype == ML_F32)
+    return run_splitk_cfg<C, float>(pb, la, lb, w, static_cast<float*>(C_), ldc, alpha, beta, st);
+  if (c_dtype == ML_BF16)
+    return run_splitk_cfg<C, bf16>(pb, la, lb, w, static_cast<bf16*>(C_), ldc, alpha, beta, st);
   set_error("gemm: C dtype %d not supported (fp32 or bf16)", c_dtype);
   return ML_ERR_INVALID;
 }
@@ -54,4 +82,35 @@ extern "C" int ml_gemm_bf16_segments(int64_t M, int64_t N, int nseg, const int64
                             {static_cast<const bf16*>(b_ptrs[s]), ldbs[s]}, (int)k_lens[s]};
   }
   return gemm::run(M, N, nseg, segs, a_layout, b_layout, C, ldc, c_dtype, alpha, beta, stream);
+}
+
+extern "C" size_t ml_gemm_splitk_workspace_bytes(int64_t M, int64_t N, int64_t K, int ksplit) {
+  if (M <= 0 || N <= 0 || K <= 0) return 0;
+  const int64_t total = (K + gemm::kBK - 1) / gemm::kBK;
+  const int64_t ks = ksplit < 1 ? 1 : ksplit;
+  const int64_t kps = (total + ks - 1) / ks;
+  const int64_t splits = (total + kps - 1) / kps;
+  return (size_t)(splits * M * N) * sizeof(float);
+}
+
+extern "C" int ml_gemm_bf16_splitk(int64_t M, int64_t N, int64_t K, const void* A, int64_t lda,
+                                   int a_layout, const void* B, int64_t ldb, int b_layout, void* C,
+                                   int64_t ldc, int c_dtype, float alpha, float beta, int tile_cfg,
+                                   int ksplit, void* workspace, size_t workspace_bytes,
+                                   void* stream) {
+  ML_CHECK(M > 0 && N > 0 && M < (1LL << 31) && N < (1LL << 31), "gemm: bad M=%lld N=%lld",
+           (long long)M, (long long)N);
+  ML_CHECK(K > 0 && K < (1LL << 31), "gemm: bad K=%lld", (long long)K);
+  ML_CHECK(a_layout == gemm::kKMajor || a_layout == gemm::kMNMajor, "gemm: bad A layout");
+  ML_CHECK(b_layout == gemm::kKMajor || b_layout == gemm::kMNMajor, "gemm: bad B layout");
+  ML_CHECK(C != nullptr && ldc >= N, "gemm: bad C");
+  ML_CHECK(ksplit >= 1, "gemm: ksplit must be >= 1");
+  gemm::Segment s{{static_cast<const bf16*>(A), lda}, {static_cast<const bf16*>(B), ldb}, (int)K};
+  hipStream_t st = (hipStream_t)stream;
+  switch (tile_cfg) {
+    case 0: return gemm::run_splitk<gemm::BigCfg>(M, N, s, a_layout, b_layout, ksplit, C, ldc, c_dtype, alpha, beta, workspace, workspace_bytes, st);
+    case 1: return gemm::run_splitk<gemm::TallCfg>(M, N, s, a_layout, b_layout, ksplit, C, ldc, c_dtype, alpha, beta, workspace, workspace_bytes, st);
+    case 2: return gemm::run_splitk<gemm::WideCfg>(M, N, s, a_layout, b_layout, ksplit, C, ldc, c_dtype, alpha, beta, workspace, workspace_bytes, st);
+    default: set_error("gemm: tile_cfg must be 0 (256x256), 1 (256x32) or 2 (64x256)"); return ML_ERR_INVALID;
+  }
 }

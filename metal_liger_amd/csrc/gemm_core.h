@@ -1,10 +1,13 @@
 // bf16 MFMA GEMM core for gfx950 (CDNA4): C[M,N] = sum_k A[m,k] * B[k,n],
 // fp32 accumulation, pluggable epilogue.
 //
-// Tiling
-//   block tile 256 x 256 x 64, 256 threads = 4 wave64s in a 2 x 2 grid, each
-//   wave owns a 128 x 128 sub-tile = 4 x 4 v_mfma_f32_32x32x16_bf16 tiles
-//   (256 fp32 accumulators per lane, held in AGPRs).
+// Tiling (compile-time tile shape Cfg<BM, BN, WAVES_M>)
+//   256 threads = 4 wave64s in a WAVES_M x (4 / WAVES_M) grid; a wave owns a
+//   (BM / WAVES_M) x (BN / WAVES_N) sub-tile made of 32 x 32 tiles of
+//   v_mfma_f32_32x32x16_bf16 (accumulators in AGPRs). BK = 64.
+//   The big-GEMM shape is 256 x 256 (2 x 2 waves of 128 x 128); narrow shapes
+//   (256 x 32, 64 x 256) serve the rank-r LoRA products without wasting MFMA
+//   work on padding.
 // Operand layouts (per operand, "rows" = M for A, N for B)
 //   K-major : element (r, k) at p[r * ld + k]   (A row-major, F.linear weight)
 //   MN-major: element (r, k) at p[k * ld + r]   (A^T stored, B row-major)
@@ -15,18 +18,22 @@
 //   transposed in registers (8 x 8 bf16 blocks, v_perm_b32) on their way
 //   into LDS, so the MFMA inner loop is the same for every layout.
 // Pipeline
-//   two LDS stages (2 x 64 KiB): the global loads of k-tile t+1 are in
-//   flight while the MFMAs of k-tile t run; one barrier per k-tile.
+//   two LDS stages: the global loads of k-tile t+1 are in flight while the
+//   MFMAs of k-tile t run; one barrier per k-tile. Global addresses are a
+//   uniform tile base (scalar registers) plus 32-bit per-thread offsets.
 // K segments
 //   K may be a concatenation of up to kMaxSeg segments with their own A/B
 //   pointers and leading dimensions (e.g. [dQ | dK | dV | lora] against
 //   [Wq; Wk; Wv; A]); a segment's last k-tile is zero-filled past its end.
+// Split-K
+//   with ksplit > 1 (single segment), split s accumulates k-tiles
+//   [s * kps, (s + 1) * kps) and the epilogue receives s; EpiPartial writes
+//   fp32 partial tiles that reduce_partials_kernel sums in fixed order.
 // Tile order
 //   workgroups are dispatched round-robin over the 8 XCDs, so block b is
-//   remapped to logical tile (b % 8) * ceil(T/8) + b / 8: each XCD walks a
-//   contiguous range of logical tiles, ordered m-fastest within groups of
-//   group_m m-tiles, so concurrently running tiles of one XCD share B (and
-//   A within a group) in that XCD's L2.
+//   remapped to logical work item (b % 8) * ceil(W/8) + b / 8: each XCD walks
+//   a contiguous range, ordered m-fastest within groups of group_m m-tiles,
+//   so concurrently running tiles of one XCD share operands in its L2.
 #pragma once
 
 #include "common.h"
@@ -38,15 +45,35 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kBM = 256, kBN = 256, kBK = 64;
+constexpr int kBK = 64;
 constexpr int kThreads = 256;
-constexpr int kWM = 128, kWN = 128;
-constexpr int kTM = kWM / 32, kTN = kWN / 32;
-constexpr int kMaxSeg = 4;
-constexpr int kRowBytes = kBK * 2;                 // 128
-constexpr int kTileBytes = kBM * kRowBytes;        // 32 KiB (A and B tiles alike)
-constexpr int kLdsBytes = 4 * kTileBytes;          // A + B, two stages: 128 KiB
+constexpr int kMaxSeg = 8;
+constexpr int kRowBytes = kBK * 2;  // 128
 constexpr int kXcds = 8;
+
+template <int BM_, int BN_, int WAVES_M_>
+struct Cfg {
+  static constexpr int BM = BM_, BN = BN_;
+  static constexpr int WAVES_M = WAVES_M_, WAVES_N = 4 / WAVES_M_;
+  static constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
+  static constexpr int TM = WM / 32, TN = WN / 32;
+  static constexpr int A_BYTES = BM * kRowBytes, B_BYTES = BN * kRowBytes;
+  static constexpr int STAGE_BYTES = A_BYTES + B_BYTES;
+  static constexpr int LDS_BYTES = 2 * STAGE_BYTES;
+  static_assert(WAVES_M * WAVES_N == 4, "4 waves per block");
+  static_assert(TM >= 1 && TN >= 1 && WM % 32 == 0 && WN % 32 == 0, "wave tile of 32x32 MFMAs");
+  static_assert(BM <= 256 && BN <= 256, "at most one 16-byte chunk set per thread");
+  static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
+};
+
+using BigCfg = Cfg<256, 256, 2>;   // 2 x 2 waves of 128 x 128
+using TallCfg = Cfg<256, 32, 4>;   // 4 x 1 waves of 64 x 32  (rank-r wide outputs)
+using WideCfg = Cfg<64, 256, 1>;   // 1 x 4 waves of 64 x 64  (few-row outputs)
+
+// Names for the big tile
+constexpr int kBM = BigCfg::BM, kBN = BigCfg::BN;
+constexpr int kWM = BigCfg::WM, kWN = BigCfg::WN;
+constexpr int kTM = BigCfg::TM, kTN = BigCfg::TN;
 
 enum : int { kKMajor = 0, kMNMajor = 1 };
 
@@ -57,7 +84,7 @@ struct Operand {
 
 struct Segment {
   Operand a, b;
-  int k_len;  // multiple of 8
+  int k_len;
 };
 
 struct Problem {
@@ -66,6 +93,8 @@ struct Problem {
   Segment seg[kMaxSeg];
   int tiles_m, tiles_n;
   int group_m;
+  int ksplit;  // >= 1; > 1 only with one segment
+  int kps;     // k-tiles per split
 };
 
 // 16-byte chunk c of LDS row r lives at chunk c ^ swz(r).
@@ -74,9 +103,10 @@ __device__ __forceinline__ int swz(int r) { return ((r >> 1) & 7) ^ ((r & 1) << 
 __device__ __forceinline__ int lds_off(int r, int c) { return r * kRowBytes + ((c ^ swz(r)) << 4); }
 
 // ------------------------------------------------------------ tile loaders --
-// Each thread moves 8 x 16 bytes of a 256-row x 64-k tile per k-step. The
-// address of every load is a wave-uniform tile base (scalar registers) plus a
-// 32-bit per-thread byte offset computed once per tile and K segment.
+// A ROWS x 64 tile: K-major moves ROWS / 32 chunks of 16 bytes per thread
+// (chunk q = tid + 256 i -> row q / 8, k-chunk q % 8; a wave reads 8 rows x
+// 128 contiguous bytes per instruction); MN-major moves one 8 (k) x 8 (r)
+// block per thread (kb = tid % 8, rb = tid / 8) for the first ROWS threads.
 struct TileRegs {
   u32x4 v[8];
 };
@@ -84,19 +114,21 @@ struct TileRegs {
 struct TileIter {
   const char* base;   // uniform: operand origin of this tile at k = 0 of the segment
   uint32_t off[8];    // per-thread byte offsets (k = 0)
-  int64_t kstride;    // bytes per k step of 1 (K-major: 2, MN-major: 2 * ld)
+  int64_t kstride;    // bytes per unit of k
 };
 
-// K-major: chunk q = tid + 256 i -> row q / 8, k-chunk q % 8 (a wave reads 8
-// rows x 128 contiguous bytes per instruction). Rows past the operand end
-// re-read its last row (those outputs are never stored).
+template <int ROWS>
+constexpr int kmajor_chunks() { return ROWS / 32; }
+
+// Rows past the operand end re-read its last row (those outputs are never stored).
+template <int ROWS>
 __device__ __forceinline__ void setup_kmajor(TileIter& it, const Operand& op, int row0, int rows,
                                              int tid) {
   it.base = reinterpret_cast<const char*>(op.ptr + (int64_t)row0 * op.ld);
   it.kstride = 2;
   const int last = rows - 1 - row0;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
+  for (int i = 0; i < kmajor_chunks<ROWS>(); ++i) {
     const int q = tid + kThreads * i;
     int r = q >> 3;
     r = r < last ? r : last;
@@ -104,50 +136,52 @@ __device__ __forceinline__ void setup_kmajor(TileIter& it, const Operand& op, in
   }
 }
 
-// MN-major: thread owns the 8 (k) x 8 (r) block kb = tid % 8, rb = tid / 8 and
-// loads its 8 k-rows of 16 bytes (8 consecutive r). rows % 8 == 0 is required.
+// rows % 8 == 0 is required (16-byte loads of 8 consecutive r).
+template <int ROWS>
 __device__ __forceinline__ void setup_mnmajor(TileIter& it, const Operand& op, int row0, int rows,
                                               int tid) {
   it.base = reinterpret_cast<const char*>(op.ptr + row0);
   it.kstride = 2 * op.ld;
   const int kb = tid & 7;
   int r = (tid >> 3) << 3;
+  r = r < ROWS ? r : 0;  // threads past the tile's rows do not load
   r = r < rows - row0 - 8 ? r : rows - row0 - 8;
 #pragma unroll
   for (int j = 0; j < 8; ++j)
     it.off[j] = (uint32_t)((((int64_t)((kb << 3) + j)) * op.ld + r) * 2);
 }
 
-template <int LAYOUT>
+template <int LAYOUT, int ROWS>
 __device__ __forceinline__ void setup_tile(TileIter& it, const Operand& op, int row0, int rows,
                                            int tid) {
   if constexpr (LAYOUT == kKMajor)
-    setup_kmajor(it, op, row0, rows, tid);
+    setup_kmajor<ROWS>(it, op, row0, rows, tid);
   else
-    setup_mnmajor(it, op, row0, rows, tid);
+    setup_mnmajor<ROWS>(it, op, row0, rows, tid);
 }
 
 // Loads the k-tile starting at k0 of a segment of length klen; k past klen
-// reads as zero.
-template <int LAYOUT>
+// reads as zero (from an always-valid address: the tile origin).
+template <int LAYOUT, int ROWS>
 __device__ __forceinline__ void load_tile(TileRegs& t, const TileIter& it, int k0, int klen,
                                           int tid) {
   const char* b = it.base + (int64_t)k0 * it.kstride;
   const int kb8 = (tid & 7) << 3;
+  constexpr int NL = (LAYOUT == kKMajor) ? kmajor_chunks<ROWS>() : 8;
+  const bool active = (LAYOUT == kKMajor) || ((tid >> 3) << 3) < ROWS;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
+  for (int i = 0; i < NL; ++i) {
     const int kk = (LAYOUT == kKMajor) ? k0 + kb8 : k0 + kb8 + i;
-    const bool kin = kk < klen;
-    // k past the segment end re-reads the tile origin (row row0, k 0 of the
-    // segment: always in bounds) and is replaced by zeros
+    const bool kin = kk < klen && active;
     const u32x4 val = *reinterpret_cast<const u32x4*>(kin ? b + it.off[i] : it.base);
     t.v[i] = kin ? val : u32x4{0u, 0u, 0u, 0u};
   }
 }
 
+template <int ROWS>
 __device__ __forceinline__ void store_kmajor(const TileRegs& t, char* lds, int tid) {
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
+  for (int i = 0; i < kmajor_chunks<ROWS>(); ++i) {
     const int q = tid + kThreads * i;
     *reinterpret_cast<u32x4*>(lds + lds_off(q >> 3, q & 7)) = t.v[i];
   }
@@ -155,9 +189,11 @@ __device__ __forceinline__ void store_kmajor(const TileRegs& t, char* lds, int t
 
 // Transposes the 8 x 8 block (t.v[j] holds r = 0..7 at k = j) into 8 rows of
 // 8 consecutive k and stores them at chunk kb of rows 8 rb .. 8 rb + 7.
+template <int ROWS>
 __device__ __forceinline__ void store_mnmajor(const TileRegs& t, char* lds, int tid) {
   const int kb = tid & 7;
   const int rb = tid >> 3;
+  if ((rb << 3) >= ROWS) return;
 #pragma unroll
   for (int rr = 0; rr < 8; ++rr) {
     const unsigned sel = (rr & 1) ? 0x07060302u : 0x05040100u;
@@ -169,57 +205,60 @@ __device__ __forceinline__ void store_mnmajor(const TileRegs& t, char* lds, int 
   }
 }
 
-template <int LAYOUT>
+template <int LAYOUT, int ROWS>
 __device__ __forceinline__ void store_tile(const TileRegs& t, char* lds, int tid) {
   if constexpr (LAYOUT == kKMajor)
-    store_kmajor(t, lds, tid);
+    store_kmajor<ROWS>(t, lds, tid);
   else
-    store_mnmajor(t, lds, tid);
+    store_mnmajor<ROWS>(t, lds, tid);
 }
 
 // ----------------------------------------------------------------- compute --
-__device__ __forceinline__ void mma_tile(f32x16_t (&acc)[kTM][kTN], const char* As, const char* Bs,
-                                         int wm, int wn, int lane) {
+template <class C>
+__device__ __forceinline__ void mma_tile(f32x16_t (&acc)[C::TM][C::TN], const char* As,
+                                         const char* Bs, int wm, int wn, int lane) {
   const int lr = lane & 31;
   const int hk = lane >> 5;
 #pragma unroll
   for (int s = 0; s < kBK / 16; ++s) {
     const int c = 2 * s + hk;
-    bf16x8_t af[kTM], bfr[kTN];
+    bf16x8_t af[C::TM], bfr[C::TN];
 #pragma unroll
-    for (int i = 0; i < kTM; ++i)
+    for (int i = 0; i < C::TM; ++i)
       af[i] = *reinterpret_cast<const bf16x8_t*>(As + lds_off(wm + 32 * i + lr, c));
 #pragma unroll
-    for (int j = 0; j < kTN; ++j)
+    for (int j = 0; j < C::TN; ++j)
       bfr[j] = *reinterpret_cast<const bf16x8_t*>(Bs + lds_off(wn + 32 * j + lr, c));
 #pragma unroll
-    for (int i = 0; i < kTM; ++i)
+    for (int i = 0; i < C::TM; ++i)
 #pragma unroll
-      for (int j = 0; j < kTN; ++j)
+      for (int j = 0; j < C::TN; ++j)
         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
   }
 }
 
-// Logical tile of this workgroup (XCD-aware, grouped); false if none.
-__device__ __forceinline__ bool tile_coords(const Problem& pb, int& tm, int& tn) {
-  const int T = pb.tiles_m * pb.tiles_n;
-  const int T8 = (T + kXcds - 1) / kXcds;
+// Work item of this workgroup (XCD-aware, grouped); false if none.
+__device__ __forceinline__ bool tile_coords(const Problem& pb, int& tm, int& tn, int& split) {
+  const int W = pb.tiles_m * pb.tiles_n * pb.ksplit;
+  const int W8 = (W + kXcds - 1) / kXcds;
   const int bid = blockIdx.x;
-  const int logical = (bid % kXcds) * T8 + bid / kXcds;
-  if (logical >= T) return false;
+  const int logical = (bid % kXcds) * W8 + bid / kXcds;
+  if (logical >= W) return false;
+  split = logical % pb.ksplit;
+  const int t = logical / pb.ksplit;
   const int gsize = pb.group_m * pb.tiles_n;
-  const int g = logical / gsize;
+  const int g = t / gsize;
   const int first_m = g * pb.group_m;
   const int gm = min(pb.tiles_m - first_m, pb.group_m);
-  const int within = logical - g * gsize;
+  const int within = t - g * gsize;
   tm = first_m + within % gm;
   tn = within / gm;
   return true;
 }
 
 inline int grid_blocks(const Problem& pb) {
-  const int T = pb.tiles_m * pb.tiles_n;
-  return ((T + kXcds - 1) / kXcds) * kXcds;
+  const int W = pb.tiles_m * pb.tiles_n * pb.ksplit;
+  return ((W + kXcds - 1) / kXcds) * kXcds;
 }
 
 // Geometry of one lane's accumulators: element v of MFMA tile (i, j) sits at
@@ -228,38 +267,46 @@ __device__ __forceinline__ int acc_row(int v, int lane) {
   return 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
 }
 
-// Main loop: accumulates the tile (tm, tn) into acc. smem is the kernel's
-// __shared__ array (stage s of A at s * kTileBytes, of B at (2 + s) * kTileBytes).
-template <int LA, int LB>
-__device__ __forceinline__ void mainloop(const Problem& pb, int tm, int tn, char* smem,
-                                         f32x16_t (&acc)[kTM][kTN]) {
+// Main loop: accumulates work item (tm, tn, split) into acc.
+template <class C, int LA, int LB>
+__device__ __forceinline__ void mainloop(const Problem& pb, int tm, int tn, int split, char* smem,
+                                         f32x16_t (&acc)[C::TM][C::TN]) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int wm = (wave >> 1) * kWM;
-  const int wn = (wave & 1) * kWN;
-  const int m0 = tm * kBM;
-  const int n0 = tn * kBN;
+  const int wm = (wave / C::WAVES_N) * C::WM;
+  const int wn = (wave % C::WAVES_N) * C::WN;
+  const int m0 = tm * C::BM;
+  const int n0 = tn * C::BN;
 #pragma unroll
-  for (int i = 0; i < kTM; ++i)
+  for (int i = 0; i < C::TM; ++i)
 #pragma unroll
-    for (int j = 0; j < kTN; ++j)
+    for (int j = 0; j < C::TN; ++j)
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
 
-  int nk = 0;
-  for (int s = 0; s < pb.nseg; ++s) nk += (pb.seg[s].k_len + kBK - 1) / kBK;
-  if (nk == 0) return;
+  int nk, seg = 0, k0 = 0;
+  if (pb.ksplit > 1) {
+    // single segment: k-tiles [split * kps, min(total, (split + 1) * kps))
+    const int total = (pb.seg[0].k_len + kBK - 1) / kBK;
+    const int first = split * pb.kps;
+    nk = total - first < pb.kps ? total - first : pb.kps;
+    k0 = first * kBK;
+  } else {
+    nk = 0;
+    for (int s = 0; s < pb.nseg; ++s) nk += (pb.seg[s].k_len + kBK - 1) / kBK;
+  }
+  if (nk <= 0) return;
+  int klen = pb.seg[0].k_len;
 
   TileIter ia, ib;
   TileRegs ra, rb;
-  int seg = 0, k0 = 0, klen = pb.seg[0].k_len;
-  setup_tile<LA>(ia, pb.seg[0].a, m0, pb.M, tid);
-  setup_tile<LB>(ib, pb.seg[0].b, n0, pb.N, tid);
-  load_tile<LA>(ra, ia, 0, klen, tid);
-  load_tile<LB>(rb, ib, 0, klen, tid);
-  store_tile<LA>(ra, smem, tid);
-  store_tile<LB>(rb, smem + 2 * kTileBytes, tid);
+  setup_tile<LA, C::BM>(ia, pb.seg[0].a, m0, pb.M, tid);
+  setup_tile<LB, C::BN>(ib, pb.seg[0].b, n0, pb.N, tid);
+  load_tile<LA, C::BM>(ra, ia, k0, klen, tid);
+  load_tile<LB, C::BN>(rb, ib, k0, klen, tid);
+  store_tile<LA, C::BM>(ra, smem, tid);
+  store_tile<LB, C::BN>(rb, smem + C::A_BYTES, tid);
   __syncthreads();
 
   for (int kt = 0; kt < nk; ++kt) {
@@ -271,35 +318,40 @@ __device__ __forceinline__ void mainloop(const Problem& pb, int tm, int tn, char
         ++seg;
         k0 = 0;
         klen = pb.seg[seg].k_len;
-        setup_tile<LA>(ia, pb.seg[seg].a, m0, pb.M, tid);
-        setup_tile<LB>(ib, pb.seg[seg].b, n0, pb.N, tid);
+        setup_tile<LA, C::BM>(ia, pb.seg[seg].a, m0, pb.M, tid);
+        setup_tile<LB, C::BN>(ib, pb.seg[seg].b, n0, pb.N, tid);
       }
-      load_tile<LA>(ra, ia, k0, klen, tid);
-      load_tile<LB>(rb, ib, k0, klen, tid);
+      load_tile<LA, C::BM>(ra, ia, k0, klen, tid);
+      load_tile<LB, C::BN>(rb, ib, k0, klen, tid);
     }
-    mma_tile(acc, smem + cur * kTileBytes, smem + (2 + cur) * kTileBytes, wm, wn, lane);
+    mma_tile<C>(acc, smem + cur * C::STAGE_BYTES, smem + cur * C::STAGE_BYTES + C::A_BYTES, wm,
+                wn, lane);
     if (more) {
-      store_tile<LA>(ra, smem + (cur ^ 1) * kTileBytes, tid);
-      store_tile<LB>(rb, smem + (2 + (cur ^ 1)) * kTileBytes, tid);
+      char* nxt = smem + (cur ^ 1) * C::STAGE_BYTES;
+      store_tile<LA, C::BM>(ra, nxt, tid);
+      store_tile<LB, C::BN>(rb, nxt + C::A_BYTES, tid);
     }
     __syncthreads();
   }
 }
 
 // The GEMM kernel: mainloop + epilogue functor
-//   epi(acc, m_base, n_base, lane, smem) with m_base / n_base the origin of
-//   this wave's 128 x 128 sub-tile. smem may be reused by the epilogue.
-template <int LA, int LB, class Epi>
+//   epi(acc, m_base, n_base, lane, smem, split) with m_base / n_base the
+//   origin of this wave's sub-tile. smem may be reused by the epilogue.
+template <class C, int LA, int LB, class Epi>
 __global__ __launch_bounds__(kThreads) void gemm_kernel(const Problem pb, const Epi epi) {
-  __shared__ __attribute__((aligned(16))) char smem[kLdsBytes];
-  int tm, tn;
-  if (!tile_coords(pb, tm, tn)) return;
-  f32x16_t acc[kTM][kTN];
-  mainloop<LA, LB>(pb, tm, tn, smem, acc);
+  __shared__ __attribute__((aligned(16))) char smem[C::LDS_BYTES];
+  int tm, tn, split;
+  if (!tile_coords(pb, tm, tn, split)) return;
+  f32x16_t acc[C::TM][C::TN];
+  mainloop<C, LA, LB>(pb, tm, tn, split, smem, acc);
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
-  epi(acc, tm * kBM + (wave >> 1) * kWM, tn * kBN + (wave & 1) * kWN, tid & 63, smem);
+  epi(acc, tm * C::BM + (wave / C::WAVES_N) * C::WM, tn * C::BN + (wave % C::WAVES_N) * C::WN,
+      tid & 63, smem, split);
 }
+
+// --------------------------------------------------------------- epilogues --
 
 // C = alpha * acc + beta * C (C of type TC, row-major with ldc).
 template <typename TC>
@@ -309,15 +361,16 @@ struct EpiStore {
   int M, N;
   float alpha, beta;
 
-  __device__ __forceinline__ void operator()(f32x16_t (&acc)[kTM][kTN], int m0, int n0, int lane,
-                                             char*) const {
+  template <int TM, int TN>
+  __device__ __forceinline__ void operator()(f32x16_t (&acc)[TM][TN], int m0, int n0, int lane,
+                                             char*, int) const {
     const int col = lane & 31;
 #pragma unroll
-    for (int j = 0; j < kTN; ++j) {
+    for (int j = 0; j < TN; ++j) {
       const int n = n0 + 32 * j + col;
       if (n >= N) continue;
 #pragma unroll
-      for (int i = 0; i < kTM; ++i) {
+      for (int i = 0; i < TM; ++i) {
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
           const int m = m0 + 32 * i + acc_row(v, lane);
@@ -332,6 +385,50 @@ struct EpiStore {
     }
   }
 };
+
+// fp32 partial tile of split s at P[s][m][n] (dense M x N per split).
+struct EpiPartial {
+  float* P;
+  int M, N;
+
+  template <int TM, int TN>
+  __device__ __forceinline__ void operator()(f32x16_t (&acc)[TM][TN], int m0, int n0, int lane,
+                                             char*, int split) const {
+    const int col = lane & 31;
+    float* base = P + (int64_t)split * M * N;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int n = n0 + 32 * j + col;
+      if (n >= N) continue;
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int m = m0 + 32 * i + acc_row(v, lane);
+          if (m < M) base[(int64_t)m * N + n] = acc[i][j][v];
+        }
+    }
+  }
+};
+
+// out[m, n] = alpha * sum_s P[s][m][n] + beta * out[m, n]  (fixed order)
+template <typename TC>
+__global__ __launch_bounds__(256) void reduce_partials_kernel(const float* __restrict__ P,
+                                                              int ksplit, int M, int N,
+                                                              TC* __restrict__ out, int64_t ldo,
+                                                              float alpha, float beta) {
+  const int64_t total = (int64_t)M * N;
+  for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < total;
+       e += (int64_t)gridDim.x * 256) {
+    float s = 0.f;
+    for (int k = 0; k < ksplit; ++k) s += P[(int64_t)k * total + e];
+    const int64_t m = e / N, n = e - m * N;
+    TC* p = out + m * ldo + n;
+    float r = alpha * s;
+    if (beta != 0.f) r += beta * to_f32(*p);
+    *p = from_f32<TC>(r);
+  }
+}
 
 // ---------------------------------------------------------------- host side --
 
@@ -353,8 +450,9 @@ inline int check_operand(const Operand& op, int layout, int rows_dim, int k_len,
   return ML_OK;
 }
 
+template <class C>
 inline int make_problem(Problem& pb, int M, int N, int nseg, const Segment* segs, int la, int lb,
-                        int group_m) {
+                        int group_m, int ksplit = 1) {
   ML_CHECK(M > 0 && N > 0, "gemm: empty output (M=%d, N=%d)", M, N);
   ML_CHECK(nseg >= 1 && nseg <= kMaxSeg, "gemm: 1..%d K segments supported (got %d)", kMaxSeg,
            nseg);
@@ -375,23 +473,31 @@ inline int make_problem(Problem& pb, int M, int N, int nseg, const Segment* segs
       if (rc) return rc;
     }
   }
-  // drop empty segments
   int w = 0;
   for (int s = 0; s < pb.nseg; ++s)
     if (pb.seg[s].k_len > 0) pb.seg[w++] = pb.seg[s];
   pb.nseg = w;
-  pb.tiles_m = (M + kBM - 1) / kBM;
-  pb.tiles_n = (N + kBN - 1) / kBN;
+  pb.tiles_m = (M + C::BM - 1) / C::BM;
+  pb.tiles_n = (N + C::BN - 1) / C::BN;
   pb.group_m = group_m > 0 ? min(group_m, pb.tiles_m) : pb.tiles_m;
+  pb.ksplit = 1;
+  pb.kps = 0;
+  if (ksplit > 1 && pb.nseg == 1) {
+    const int total = (pb.seg[0].k_len + kBK - 1) / kBK;
+    const int kps = (total + ksplit - 1) / ksplit;
+    pb.kps = kps;
+    pb.ksplit = (total + kps - 1) / kps;  // no empty splits
+  }
   return ML_OK;
 }
 
+// Big-tile launch with the store epilogue.
 template <typename TC>
-inline int launch_store(const Problem& pb, int la, int lb, void* C, int64_t ldc, float alpha, float beta,
-                 hipStream_t st) {
+inline int launch_store(const Problem& pb, int la, int lb, void* C, int64_t ldc, float alpha,
+                        float beta, hipStream_t st) {
   EpiStore<TC> epi{static_cast<TC*>(C), ldc, pb.M, pb.N, alpha, beta};
   const dim3 grid(grid_blocks(pb));
-#define ML_G(LA, LB) gemm_kernel<LA, LB, EpiStore<TC>><<<grid, kThreads, 0, st>>>(pb, epi)
+#define ML_G(LA, LB) gemm_kernel<BigCfg, LA, LB, EpiStore<TC>><<<grid, kThreads, 0, st>>>(pb, epi)
   if (la == kKMajor && lb == kKMajor) ML_G(kKMajor, kKMajor);
   else if (la == kKMajor && lb == kMNMajor) ML_G(kKMajor, kMNMajor);
   else if (la == kMNMajor && lb == kKMajor) ML_G(kMNMajor, kKMajor);
@@ -399,6 +505,27 @@ inline int launch_store(const Problem& pb, int la, int lb, void* C, int64_t ldc,
 #undef ML_G
   ML_LAUNCH_CHECK();
   return ML_OK;
+}
+
+// Split-K product of shape C into fp32 partials ws (ksplit * M * N floats),
+// then out = alpha * sum + beta * out.
+template <class C, int LA, int LB, typename TC>
+inline int launch_splitk(const Problem& pb, float* ws, TC* out, int64_t ldo, float alpha, float beta,
+                         hipStream_t st) {
+  EpiPartial epi{ws, pb.M, pb.N};
+  gemm_kernel<C, LA, LB, EpiPartial><<<dim3(grid_blocks(pb)), kThreads, 0, st>>>(pb, epi);
+  ML_LAUNCH_CHECK();
+  const int64_t total = (int64_t)pb.M * pb.N;
+  int64_t blocks = (total + 255) / 256;
+  blocks = blocks < 2048 ? blocks : 2048;
+  reduce_partials_kernel<TC><<<dim3((unsigned)blocks), 256, 0, st>>>(ws, pb.ksplit, pb.M, pb.N,
+                                                                     out, ldo, alpha, beta);
+  ML_LAUNCH_CHECK();
+  return ML_OK;
+}
+
+inline size_t splitk_ws_bytes(const Problem& pb) {
+  return (size_t)pb.ksplit * (size_t)pb.M * (size_t)pb.N * sizeof(float);
 }
 
 }  // namespace gemm

@@ -280,7 +280,8 @@ def _gemm_operand(t: torch.Tensor, what: str) -> torch.Tensor:
 
 def matmul(a: torch.Tensor, b: torch.Tensor, *, a_t: bool = False, b_t: bool = False,
            out: torch.Tensor | None = None, out_dtype: torch.dtype = torch.float32,
-           alpha: float = 1.0, beta: float = 0.0) -> torch.Tensor:
+           alpha: float = 1.0, beta: float = 0.0, tile_cfg: int = 0,
+           ksplit: int = 1) -> torch.Tensor:
     """op(a) @ op(b) on the MFMA engine, op(x) = x.T when the flag is set.
 
     a: [M, K] (or [K, M] with a_t); b: [K, N] (or [N, K] with b_t, an
@@ -299,11 +300,21 @@ def matmul(a: torch.Tensor, b: torch.Tensor, *, a_t: bool = False, b_t: bool = F
         beta = 0.0
     elif out.shape != (M, N) or out.stride(1) != 1:
         raise ValueError("gemm: out must be a row-major [M, N] tensor")
-    call(
-        "ml_gemm_bf16", M, N, K, ptr(a), a.stride(0), 1 if a_t else 0, ptr(b), b.stride(0),
-        0 if b_t else 1, ptr(out), out.stride(0), dtype_tag(out, "out"), float(alpha), float(beta),
-        stream_of(a),
-    )
+    if tile_cfg == 0 and ksplit == 1:
+        call(
+            "ml_gemm_bf16", M, N, K, ptr(a), a.stride(0), 1 if a_t else 0, ptr(b), b.stride(0),
+            0 if b_t else 1, ptr(out), out.stride(0), dtype_tag(out, "out"), float(alpha),
+            float(beta), stream_of(a),
+        )
+    else:
+        wsb = _hip.query("ml_gemm_splitk_workspace_bytes", M, N, K, ksplit)
+        ws = torch.empty(max(wsb // 4, 1), dtype=torch.float32, device=a.device)
+        call(
+            "ml_gemm_bf16_splitk", M, N, K, ptr(a), a.stride(0), 1 if a_t else 0, ptr(b),
+            b.stride(0), 0 if b_t else 1, ptr(out), out.stride(0), dtype_tag(out, "out"),
+            float(alpha), float(beta), int(tile_cfg), int(ksplit), ptr(ws), ws.numel() * 4,
+            stream_of(a),
+        )
     return out
 
 
@@ -379,3 +390,90 @@ def flce_bwd(hidden, weight, labels, bias, ignore_index, lse, n_valid, grad_loss
         ws.numel(), stream_of(weight),
     )
     return dh, dw
+
+
+# -------------------------------------------------------------------- LoRA --
+
+
+def _bf16_rows(t: torch.Tensor) -> torch.Tensor:
+    """bf16, row-major, 16-byte aligned rows (a copy only when needed)."""
+    if t.dtype != torch.bfloat16:
+        t = t.to(torch.bfloat16)
+    if t.dim() != 2 or t.stride(1) != 1 or t.stride(0) % 8 != 0 or t.data_ptr() % 16 != 0:
+        t = t.contiguous()
+    return t
+
+
+def _ksplit_for(tiles: int, k: int) -> int:
+    ktiles = (k + 63) // 64
+    return max(1, min(ktiles, (512 + tiles - 1) // max(tiles, 1)))
+
+
+def lora_xa(x2: torch.Tensor, a_stack: torch.Tensor) -> torch.Tensor:
+    """X A^T for stacked LoRA A matrices: [N, in] x [R, in]^T -> [N, R] bf16
+    (256x32 tiles, split-K over in)."""
+    N, K = x2.shape
+    R = a_stack.shape[0]
+    tiles = ((N + 255) // 256) * ((R + 31) // 32)
+    return matmul(x2, a_stack, b_t=True, out_dtype=torch.bfloat16, tile_cfg=1,
+                  ksplit=_ksplit_for(tiles, K))
+
+
+def lora_linear_out(x2: torch.Tensor, w: torch.Tensor, xa: torch.Tensor,
+                    sb: torch.Tensor) -> torch.Tensor:
+    """X W^T + XA (s B)^T as ONE K-concatenated GEMM -> [N, out] bf16."""
+    N, K = x2.shape
+    out_f = w.shape[0]
+    r = xa.shape[1]
+    out = torch.empty(N, out_f, dtype=torch.bfloat16, device=x2.device)
+    call(
+        "ml_gemm_bf16_segments", N, out_f, 2, geom([K, r]), _hip.ptrs([x2.data_ptr(), xa.data_ptr()]),
+        geom([x2.stride(0), xa.stride(0)]), _hip.ptrs([w.data_ptr(), sb.data_ptr()]),
+        geom([w.stride(0), sb.stride(0)]), 0, 0, ptr(out), out.stride(0), dtype_tag(out, "out"),
+        1.0, 0.0, stream_of(x2),
+    )
+    return out
+
+
+def lora_qkv_bwd(x2, dys, ws_, a_stack, bs, scales, xa, rank):
+    """Returns (dX bf16 [N, in], dA fp32 [3r, in], [dB_i fp32 [out_i, r]])."""
+    ensure_rocm_device(x2, *dys, *ws_, a_stack, *bs, xa)
+    N, IN = x2.shape
+    outs = [int(d.shape[1]) for d in dys]
+    dev = x2.device
+    dX = torch.empty(N, IN, dtype=torch.bfloat16, device=dev)
+    dA = torch.empty(3 * rank, IN, dtype=torch.float32, device=dev)
+    dBs = [torch.empty(o, rank, dtype=torch.float32, device=dev) for o in outs]
+    wsb = _hip.query("ml_lora_qkv_bwd_workspace_bytes", N, IN, geom(outs), rank)
+    ws = torch.empty(max(wsb, 16), dtype=torch.uint8, device=dev)
+    call(
+        "ml_lora_qkv_bwd", ptr(x2), N, IN, _hip.ptrs([d.data_ptr() for d in dys]), geom(outs),
+        _hip.ptrs([w.data_ptr() for w in ws_]), ptr(a_stack), _hip.ptrs([b.data_ptr() for b in bs]),
+        _hip.floats(scales), ptr(xa), rank, ptr(dX), ptr(dA),
+        _hip.ptrs([b.data_ptr() for b in dBs]), ptr(ws), ws.numel(), stream_of(x2),
+    )
+    return dX, dA, dBs
+
+
+def lora_mlp_bwd(x2, gate, up, h, dy, wg, wu, wd, a_gu, a_d, bg, bu, bd, scales, xa_gu, ha_d, rank):
+    """Returns (dX, dA_GU [2r, H], dA_D [r, I], dB_G [I, r], dB_U [I, r], dB_D [H, r])."""
+    ensure_rocm_device(x2, gate, up, h, dy, wg, wu, wd, a_gu, a_d, bg, bu, bd, xa_gu, ha_d)
+    N, H = x2.shape
+    I = gate.shape[1]
+    dev = x2.device
+    f32 = torch.float32
+    dX = torch.empty(N, H, dtype=torch.bfloat16, device=dev)
+    dA_GU = torch.empty(2 * rank, H, dtype=f32, device=dev)
+    dA_D = torch.empty(rank, I, dtype=f32, device=dev)
+    dB_G = torch.empty(I, rank, dtype=f32, device=dev)
+    dB_U = torch.empty(I, rank, dtype=f32, device=dev)
+    dB_D = torch.empty(H, rank, dtype=f32, device=dev)
+    wsb = _hip.query("ml_lora_mlp_bwd_workspace_bytes", N, H, I, rank)
+    ws = torch.empty(max(wsb, 16), dtype=torch.uint8, device=dev)
+    call(
+        "ml_lora_mlp_bwd", ptr(x2), N, H, I, ptr(gate), ptr(up), ptr(h), ptr(dy), ptr(wg), ptr(wu),
+        ptr(wd), ptr(a_gu), ptr(a_d), ptr(bg), ptr(bu), ptr(bd), _hip.floats(scales), ptr(xa_gu),
+        ptr(ha_d), rank, ptr(dX), ptr(dA_GU), ptr(dA_D), ptr(dB_G), ptr(dB_U), ptr(dB_D), ptr(ws),
+        ws.numel(), stream_of(x2),
+    )
+    return dX, dA_GU, dA_D, dB_G, dB_U, dB_D

@@ -1,0 +1,319 @@
+"""Fused LoRA QKV + MLP on MI355X (drop-in for the reference's ops/fused_lora.py).
+
+X is saved once per fused block (as in the reference), and the backward of
+each block is a single call into the HIP library:
+
+* QKV (`_LoRA_QKV`): the rank-r products P_i = s_i dY_i B_i, dA = P^T X and
+  dB_i = s_i dY_i^T (X A_i^T) run on narrow MFMA tiles with split-K; the
+  shared dX is ONE MFMA GEMM over the K-concatenation
+  [dQ | dK | dV | P] x [Wq; Wk; Wv; A_q; A_k; A_v].
+* MLP (`_LoRA_MLP`): dH = dY W_D + s (dY B_D) A_D comes from one MFMA GEMM
+  whose epilogue applies the SwiGLU backward (sigmoid recomputed), writing
+  d_gate / d_up; then the gate / up adapters as above, and dX as one GEMM
+  over [d_gate | d_up | P] x [W_G; W_U; A_G; A_U].
+
+The forward passes also run on the MFMA engine: X A^T for the stacked A
+matrices (saved for the backward, where the reference recomputed it) and
+each output as one GEMM over [X | X A^T] x [W; s B]^T.
+
+Semantics kept from the reference (ops/fused_lora.py:43-421): PEFT parameter
+layout (first adapter only, dropout ignored), A/B cast to the activation
+dtype, dA/dB returned in fp32, no gradient for the frozen base weights, and
+the patcher shadows q/k/v_proj without replacing modules (state_dict keys
+unchanged). The HIP path computes in bf16 (MI355X's training dtype); other
+activation dtypes raise.
+"""
+
+import logging
+import types
+from typing import Any, Optional, Tuple  # noqa: F401
+
+import torch
+import torch.nn as nn
+
+from metal_liger_amd import hip_ops
+
+logger = logging.getLogger(__name__)
+
+
+def _get_lora_params(linear):
+    """(W, A, B, scaling) of a PEFT LoRA Linear, else (None,)*4
+    (ops/fused_lora.py:43-66): first adapter, base weight from base_layer."""
+    if not hasattr(linear, 'lora_A'):
+        return None, None, None, None
+    adapters = list(linear.lora_A.keys())
+    if not adapters:
+        return None, None, None, None
+    adapter = adapters[0]
+    W = linear.base_layer.weight if hasattr(linear, 'base_layer') else linear.weight
+    A = linear.lora_A[adapter].weight   # [r, in_features]
+    B = linear.lora_B[adapter].weight   # [out_features, r]
+    scaling = linear.scaling[adapter]
+    return W, A, B, scaling
+
+
+def _check_bf16(X: torch.Tensor, what: str):
+    if X.dtype != torch.bfloat16:
+        raise TypeError(
+            f"metal_liger_amd {what}: the fused LoRA path runs bf16 MFMA GEMMs; got activations "
+            f"of dtype {X.dtype} (cast the model to bfloat16)"
+        )
+
+
+def _pad_rank(r: int) -> int:
+    return (r + 7) // 8 * 8
+
+
+def _stack_a(As, rp: int) -> torch.Tensor:
+    """[A_1; A_2; ...] in bf16, each padded with zero rows to rp."""
+    parts = []
+    for A in As:
+        a = A.detach().to(torch.bfloat16)
+        if a.shape[0] != rp:
+            a = torch.cat([a, a.new_zeros(rp - a.shape[0], a.shape[1])], 0)
+        parts.append(a)
+    return torch.cat(parts, 0).contiguous()
+
+
+def _pad_b(B: torch.Tensor, rp: int, scale: float = 1.0) -> torch.Tensor:
+    """B (optionally times the LoRA scale) in bf16, padded with zero columns to rp."""
+    b = B.detach().to(torch.bfloat16)
+    if scale != 1.0:
+        b = b * scale
+    if b.shape[1] != rp:
+        b = torch.cat([b, b.new_zeros(b.shape[0], rp - b.shape[1])], 1)
+    return b.contiguous()
+
+
+def _lora_linear(X: torch.Tensor, W: torch.Tensor,
+                 A: torch.Tensor, B: torch.Tensor, scaling: float) -> torch.Tensor:
+    """X W^T + s (X A^T) B^T (ops/fused_lora.py:69-82) on the MFMA engine."""
+    _check_bf16(X, "_lora_linear")
+    shape = X.shape
+    X2 = hip_ops._bf16_rows(X.reshape(-1, shape[-1]))
+    W2 = hip_ops._bf16_rows(W.detach())
+    if A is None or B is None:
+        out = hip_ops.matmul(X2, W2, b_t=True, out_dtype=torch.bfloat16)
+    else:
+        rp = _pad_rank(A.shape[0])
+        xa = hip_ops.lora_xa(X2, _stack_a([A], rp))
+        out = hip_ops.lora_linear_out(X2, W2, xa, _pad_b(B, rp, float(scaling)))
+    return out.view(*shape[:-1], -1)
+
+
+class _LoRA_QKV(torch.autograd.Function):
+    """Fused Q+K+V LoRA projections — X saved once for all three backward
+    passes (ops/fused_lora.py:85-171)."""
+
+    @staticmethod
+    def forward(ctx,
+                X,
+                QW, QA, QB, QS,
+                KW, KA, KB, KS,
+                VW, VA, VB, VS):
+        _check_bf16(X, "LoRA QKV")
+        shape = X.shape
+        Xf = hip_ops._bf16_rows(X.reshape(-1, shape[-1]))
+        ranks = {QA.shape[0], KA.shape[0], VA.shape[0]}
+        if len(ranks) != 1:
+            raise ValueError(f"LoRA QKV: q/k/v adapters must share the rank (got {sorted(ranks)})")
+        r = QA.shape[0]
+        rp = _pad_rank(r)
+        a_stack = _stack_a([QA, KA, VA], rp)
+        xa = hip_ops.lora_xa(Xf, a_stack)                      # [N, 3 rp], saved
+        Ws = [hip_ops._bf16_rows(W.detach()) for W in (QW, KW, VW)]
+        Bs = [_pad_b(B, rp) for B in (QB, KB, VB)]
+        scales = [float(QS), float(KS), float(VS)]
+        outs = []
+        for i in range(3):
+            sb = Bs[i] * scales[i] if scales[i] != 1.0 else Bs[i]
+            outs.append(hip_ops.lora_linear_out(Xf, Ws[i], xa[:, i * rp:(i + 1) * rp], sb))
+        ctx.save_for_backward(Xf, xa, a_stack, *Ws, *Bs)
+        ctx.scales = scales
+        ctx.rank, ctx.rank_p = r, rp
+        ctx.orig_shape = shape
+        ctx.param_dtypes = [(A.dtype, B.dtype) for A, B in ((QA, QB), (KA, KB), (VA, VB))]
+        return tuple(o.view(*shape[:-1], -1) for o in outs)
+
+    @staticmethod
+    def backward(ctx, dQ, dK, dV):
+        Xf, xa, a_stack, QW, KW, VW, QB, KB, VB = ctx.saved_tensors
+        r, rp = ctx.rank, ctx.rank_p
+        shape = ctx.orig_shape
+        dys = [hip_ops._bf16_rows(d.reshape(-1, d.shape[-1])) for d in (dQ, dK, dV)]
+        dX, dA, dBs = hip_ops.lora_qkv_bwd(Xf, dys, [QW, KW, VW], a_stack, [QB, KB, VB],
+                                           ctx.scales, xa, rp)
+        grads = []
+        for i in range(3):
+            dAi = dA[i * rp:i * rp + r]
+            dBi = dBs[i][:, :r]
+            grads.append((dAi, dBi))
+        dX = dX.view(*shape)
+        return (dX,
+                None, grads[0][0], grads[0][1], None,   # QW, QA, QB, QS
+                None, grads[1][0], grads[1][1], None,   # KW, KA, KB, KS
+                None, grads[2][0], grads[2][1], None)   # VW, VA, VB, VS
+
+
+class _LoRA_MLP(torch.autograd.Function):
+    """Fused gate+up+down LoRA MLP with SwiGLU (ops/fused_lora.py:174-266)."""
+
+    @staticmethod
+    def forward(ctx,
+                X,
+                GW, GA, GB, GS,   # gate projection
+                UW, UA, UB, US,   # up projection
+                DW, DA, DB, DS):  # down projection
+        _check_bf16(X, "LoRA MLP")
+        shape = X.shape
+        Xf = hip_ops._bf16_rows(X.reshape(-1, shape[-1]))
+        ranks = {GA.shape[0], UA.shape[0], DA.shape[0]}
+        if len(ranks) != 1:
+            raise ValueError(f"LoRA MLP: gate/up/down adapters must share the rank (got {sorted(ranks)})")
+        r = GA.shape[0]
+        rp = _pad_rank(r)
+        scales = [float(GS), float(US), float(DS)]
+        a_gu = _stack_a([GA, UA], rp)                            # [2 rp, hidden]
+        a_d = _stack_a([DA], rp)                                 # [rp, inter]
+        GWc, UWc, DWc = (hip_ops._bf16_rows(W.detach()) for W in (GW, UW, DW))
+        BG, BU, BD = (_pad_b(B, rp) for B in (GB, UB, DB))
+        xa_gu = hip_ops.lora_xa(Xf, a_gu)                         # [N, 2 rp]
+        gate = hip_ops.lora_linear_out(Xf, GWc, xa_gu[:, :rp], BG * scales[0])
+        up = hip_ops.lora_linear_out(Xf, UWc, xa_gu[:, rp:], BU * scales[1])
+        h = hip_ops.swiglu_fwd(gate, up)                          # silu(gate) * up, bf16
+        ha_d = hip_ops.lora_xa(h, a_d)                            # [N, rp]
+        out = hip_ops.lora_linear_out(h, DWc, ha_d, BD * scales[2])
+        ctx.save_for_backward(Xf, gate, up, h, xa_gu, ha_d, a_gu, a_d, GWc, UWc, DWc, BG, BU, BD)
+        ctx.scales = scales
+        ctx.rank, ctx.rank_p = r, rp
+        ctx.orig_shape = shape
+        return out.view(*shape)
+
+    @staticmethod
+    def backward(ctx, dY):
+        (Xf, gate, up, h, xa_gu, ha_d, a_gu, a_d, GW, UW, DW, BG, BU, BD) = ctx.saved_tensors
+        r, rp = ctx.rank, ctx.rank_p
+        shape = ctx.orig_shape
+        dy = hip_ops._bf16_rows(dY.reshape(-1, dY.shape[-1]))
+        dX, dA_GU, dA_D, dB_G, dB_U, dB_D = hip_ops.lora_mlp_bwd(
+            Xf, gate, up, h, dy, GW, UW, DW, a_gu, a_d, BG, BU, BD, ctx.scales, xa_gu, ha_d, rp)
+        dX = dX.view(*shape)
+        return (dX,
+                None, dA_GU[:r], dB_G[:, :r], None,        # GW, GA, GB, GS
+                None, dA_GU[rp:rp + r], dB_U[:, :r], None,  # UW, UA, UB, US
+                None, dA_D[:r], dB_D[:, :r], None)          # DW, DA, DB, DS
+
+
+def apply_fused_lora_qkv(attn_module, X: torch.Tensor):
+    """Fused Q+K+V LoRA projections of an attention module
+    (ops/fused_lora.py:269-295); plain module calls when any projection has
+    no LoRA adapter."""
+    QW, QA, QB, QS = _get_lora_params(attn_module.q_proj)
+    KW, KA, KB, KS = _get_lora_params(attn_module.k_proj)
+    VW, VA, VB, VS = _get_lora_params(attn_module.v_proj)
+
+    if QA is None or KA is None or VA is None:
+        Q = attn_module.q_proj(X)
+        K = attn_module.k_proj(X)
+        V = attn_module.v_proj(X)
+        return Q, K, V
+
+    return _LoRA_QKV.apply(
+        X,
+        QW, QA, QB, QS,
+        KW, KA, KB, KS,
+        VW, VA, VB, VS,
+    )
+
+
+def apply_fused_lora_mlp(mlp_module, X: torch.Tensor) -> torch.Tensor:
+    """Fused gate+up+down LoRA MLP (ops/fused_lora.py:298-320); the module's
+    own forward when any projection has no LoRA adapter."""
+    GW, GA, GB, GS = _get_lora_params(mlp_module.gate_proj)
+    UW, UA, UB, US = _get_lora_params(mlp_module.up_proj)
+    DW, DA, DB, DS = _get_lora_params(mlp_module.down_proj)
+
+    if GA is None or UA is None or DA is None:
+        return mlp_module(X)
+
+    return _LoRA_MLP.apply(
+        X,
+        GW, GA, GB, GS,
+        UW, UA, UB, US,
+        DW, DA, DB, DS,
+    )
+
+
+def patch_fused_lora(model: nn.Module) -> int:
+    """Routes every attention / MLP with LoRA on all three projections through
+    the fused functions (ops/fused_lora.py:323-421). Modules are not
+    replaced: attention forwards shadow q/k/v_proj in the instance __dict__
+    with the precomputed fused results for the duration of the call, so
+    state_dict keys stay unchanged. Returns the number of patched modules."""
+    base = model.base_model.model if hasattr(model, 'base_model') else model
+
+    def _find_layers_list(m, depth=0):
+        if depth > 6:
+            return None
+        for name, child in m.named_children():
+            if name == 'layers' and len(list(child.children())) > 0:
+                return child
+            result = _find_layers_list(child, depth + 1)
+            if result is not None:
+                return result
+        return None
+
+    layers = _find_layers_list(base)
+    if layers is None:
+        logger.warning("MetalLiger fused LoRA: could not find transformer layers")
+        return 0
+
+    patched = 0
+    for layer in layers:
+        attn = getattr(layer, 'self_attn', None)
+        mlp = getattr(layer, 'mlp', None)
+
+        if attn is not None:
+            has_q = hasattr(attn, 'q_proj') and _get_lora_params(attn.q_proj)[1] is not None
+            has_k = hasattr(attn, 'k_proj') and _get_lora_params(attn.k_proj)[1] is not None
+            has_v = hasattr(attn, 'v_proj') and _get_lora_params(attn.v_proj)[1] is not None
+
+            if has_q and has_k and has_v:
+                orig_fwd = attn.forward
+
+                def _make_fused_forward(orig_fwd):
+                    def _fused_forward(self_attn, hidden_states, *args, **kwargs):
+                        Q, K, V = apply_fused_lora_qkv(self_attn, hidden_states)
+                        self_attn.__dict__['q_proj'] = lambda x: Q
+                        self_attn.__dict__['k_proj'] = lambda x: K
+                        self_attn.__dict__['v_proj'] = lambda x: V
+                        try:
+                            return orig_fwd(hidden_states, *args, **kwargs)
+                        finally:
+                            self_attn.__dict__.pop('q_proj', None)
+                            self_attn.__dict__.pop('k_proj', None)
+                            self_attn.__dict__.pop('v_proj', None)
+
+                    return _fused_forward
+
+                attn.forward = types.MethodType(_make_fused_forward(orig_fwd), attn)
+                attn._metal_liger_fused_lora = True
+                patched += 1
+
+        if mlp is not None:
+            has_gate = hasattr(mlp, 'gate_proj') and _get_lora_params(mlp.gate_proj)[1] is not None
+            has_up = hasattr(mlp, 'up_proj') and _get_lora_params(mlp.up_proj)[1] is not None
+            has_down = hasattr(mlp, 'down_proj') and _get_lora_params(mlp.down_proj)[1] is not None
+
+            if has_gate and has_up and has_down:
+                def _make_fused_mlp_forward(mlp_instance):
+                    def _fused_mlp_forward(self, x):
+                        return apply_fused_lora_mlp(self, x)
+                    return _fused_mlp_forward.__get__(mlp_instance, type(mlp_instance))
+
+                mlp.forward = _make_fused_mlp_forward(mlp)
+                mlp._metal_liger_fused_lora = True
+                patched += 1
+
+    logger.info(f"MetalLiger fused LoRA: activated on {patched} modules.")
+    return patched

@@ -69,3 +69,25 @@ def test_gemm_rejects_bad_shapes(dev):
     b = torch.zeros(12, 64, dtype=torch.bfloat16, device=dev)
     with pytest.raises(RuntimeError, match="multiple of 8"):
         hip_ops.matmul(a, b)
+
+
+@pytest.mark.parametrize("cfg", [0, 1, 2])
+@pytest.mark.parametrize("ksplit", [1, 3, 8])
+@pytest.mark.parametrize("a_t,b_t,mnk", [(False, True, (520, 48, 2048)), (True, False, (48, 264, 1000)),
+                                         (True, False, (2048, 16, 777)), (False, False, (300, 32, 512))])
+def test_gemm_splitk_shapes(dev, cfg, ksplit, a_t, b_t, mnk):
+    """Tile shapes 256x256 / 256x32 / 64x256 with split-K (fixed-order partial sums)."""
+    from metal_liger_amd import hip_ops
+    M, N, K = mnk
+    a_kmajor, b_kmajor = not a_t, b_t
+    if (a_kmajor or b_kmajor) and K % 8:
+        pytest.skip("K-major operands need K % 8 == 0")
+    a = seeded((K, M) if a_t else (M, K), 31, torch.bfloat16)
+    b = seeded((N, K) if b_t else (K, N), 32, torch.bfloat16)
+    out = hip_ops.matmul(a.to(dev), b.to(dev), a_t=a_t, b_t=b_t, tile_cfg=cfg, ksplit=ksplit)
+    assert_close(out, ref_mm(a, b, a_t, b_t), f"splitk cfg={cfg} ks={ksplit} {mnk}")
+    c0 = seeded((M, N), 33).to(dev)
+    c = c0.clone()
+    hip_ops.matmul(a.to(dev), b.to(dev), a_t=a_t, b_t=b_t, out=c, alpha=2.0, beta=0.5,
+                   tile_cfg=cfg, ksplit=ksplit)
+    assert_close(c, 2.0 * ref_mm(a, b, a_t, b_t) + 0.5 * c0.cpu(), "splitk alpha/beta")

@@ -1,0 +1,246 @@
+"""GPU parity: fused LoRA QKV / MLP (HIP path) against the oracle.
+
+The oracle restates the reference's torch ops (ops/fused_lora.py) op for
+op; small cases run it on the CPU, the Qwen3-2B-layer config runs the same
+restatement on the GPU. Every output and gradient must satisfy both
+  * against the oracle evaluated in fp32 on the same bf16 inputs ("exact"),
+    with ref the oracle in bf16 (the reference's rounding sequence):
+    rms(ours - exact) <= 1.5 rms(ref - exact), and elementwise
+    |ours - exact| <= 2e-2 |exact| + 1e-2 + 6 rms(ref - exact) - the bf16
+    bar (rtol 2e-2 / atol 1e-2) widened by the size of the reference's own
+    rounding error (6 sigma: the config tensors hold 10^7 entries), and
+  * relative Frobenius error <= 2e-2 against the oracle in bf16.
+The widening is needed because the reference rounds every intermediate
+(dY B, (dY B) A, each partial sum) to bf16, and on entries where large
+rank-r terms cancel that rounding alone exceeds atol 1e-2; the kernels round
+the rank-r intermediate P = s dY B to bf16 at the same point.
+"""
+
+import pytest
+import torch
+
+from oracle import reference_ops as ref
+from tests.parity import assert_close, rel_fro, seeded
+
+pytestmark = pytest.mark.gpu
+BF = torch.bfloat16
+
+
+def adapter(out_f, in_f, r, seed, w_std=0.02, a_std=0.25, b_std=0.02):
+    W = seeded((out_f, in_f), seed, BF, scale=w_std)
+    A = seeded((r, in_f), seed + 1, BF, scale=a_std)
+    B = seeded((out_f, r), seed + 2, BF, scale=b_std)
+    return W, A, B
+
+
+def check(out, ref32, refbf, what):
+    """rms(ours - exact) <= 1.5 rms(reference_bf16 - exact); elementwise
+    |ours - exact| <= 2e-2 |exact| + 1e-2 + 6 rms(reference_bf16 - exact), i.e.
+    the bf16 bar widened by the size of the reference's own rounding error;
+    relative Frobenius <= 2e-2 against the bf16 reference."""
+    o = out.detach().float().cpu()
+    e = ref32.detach().float().cpu()
+    b = refbf.detach().float().cpu()
+    assert o.shape == e.shape, f"{what}: shape {tuple(o.shape)} != {tuple(e.shape)}"
+    ref_rms = (b - e).pow(2).mean().sqrt()
+    ours_rms = (o - e).pow(2).mean().sqrt()
+    # aggregate: no less accurate than the reference's own bf16 evaluation
+    assert ours_rms <= 1.5 * ref_rms + 1e-6 * e.abs().max(), (
+        f"{what}: rms error {ours_rms.item():.3e} vs reference {ref_rms.item():.3e}")
+    band = 6.0 * ref_rms
+    tol = 2e-2 * e.abs() + 1e-2 + band
+    err = (o - e).abs()
+    bad = err > tol
+    if bad.any():
+        idx = bad.nonzero()[:6].tolist()
+        ex = "; ".join(f"{tuple(i)}: ours {o[tuple(i)].item():.4f} exact {e[tuple(i)].item():.4f} "
+                       f"ref {b[tuple(i)].item():.4f}" for i in idx)
+        raise AssertionError(f"{what}: {int(bad.sum())}/{o.numel()} beyond the bar; max excess "
+                             f"{(err - tol).max().item():.3e}; band {band.item():.3e}; {ex}")
+    assert rel_fro(out, refbf) <= 2e-2, f"{what}: rel Frobenius {rel_fro(out, refbf):.3e}"
+
+
+def f32(ts):
+    return [t.float() if torch.is_tensor(t) else t for t in ts]
+
+
+def run_qkv(dev, X, params, dys):
+    from metal_liger_amd.ops.fused_lora import _LoRA_QKV
+    Xd = X.to(dev).requires_grad_(True)
+    leaves = []
+    args = []
+    for (W, A, B, s) in params:
+        Ad = A.to(dev).requires_grad_(True)
+        Bd = B.to(dev).requires_grad_(True)
+        leaves.append((Ad, Bd))
+        args += [W.to(dev), Ad, Bd, s]
+    outs = _LoRA_QKV.apply(Xd, *args)
+    torch.autograd.backward(outs, [d.to(dev) for d in dys])
+    return outs, Xd.grad, leaves
+
+
+@pytest.mark.parametrize("N,IN,OUTS,r", [(32, 128, (128, 128, 128), 8), (300, 256, (256, 128, 128), 16),
+                                         (64, 64, (64, 32, 32), 4)])
+def test_lora_qkv_small(dev, N, IN, OUTS, r):
+    X = seeded((N, IN), 1, BF)
+    params = [(*adapter(o, IN, r, 10 * i + 2, b_std=0.05), 2.0) for i, o in enumerate(OUTS)]
+    dys = [seeded((N, o), 50 + i, BF) for i, o in enumerate(OUTS)]
+    outs, dX, leaves = run_qkv(dev, X, params, dys)
+    flat = [t for p in params for t in p]
+    rQ, rK, rV = ref.lora_qkv_forward(X, *flat)
+    rdX, *rdAB = ref.lora_qkv_backward(X, *dys, *flat)
+    fQ, fK, fV = ref.lora_qkv_forward(X.float(), *f32(flat))
+    fdX, *fdAB = ref.lora_qkv_backward(X.float(), *f32(dys), *f32(flat))
+    for o, fo, ro, n in zip(outs, (fQ, fK, fV), (rQ, rK, rV), "QKV"):
+        check(o, fo, ro, f"{n} fwd")
+    check(dX, fdX, rdX, "dX")
+    for i, (Ad, Bd) in enumerate(leaves):
+        assert Ad.grad.dtype == BF  # autograd casts the fp32 grads to the parameter dtype
+        check(Ad.grad.float(), fdAB[2 * i], rdAB[2 * i], f"dA[{i}]")
+        check(Bd.grad.float(), fdAB[2 * i + 1], rdAB[2 * i + 1], f"dB[{i}]")
+
+
+def test_lora_qkv_reference_test_case(dev):
+    """reference tests/test_fused_ops.py:198-242 in bf16: X [2,16,128], W/A/B
+    ~N(0,1) (r=8, s=2), loss = sum(Q)+sum(K)+sum(V), against autograd of
+    X W^T + (X A^T) B^T s in fp32 on the same bf16 values. QW gets no gradient."""
+    from metal_liger_amd.ops.fused_lora import _LoRA_QKV
+    g = torch.Generator().manual_seed(42)
+    X = torch.randn(2, 16, 128, generator=g).to(BF)
+    P = [(torch.randn(128, 128, generator=g).to(BF), torch.randn(8, 128, generator=g).to(BF),
+          torch.randn(128, 8, generator=g).to(BF), 2.0) for _ in range(3)]
+    Xd = X.to(dev).requires_grad_(True)
+    args, leaves = [], []
+    for W, A, B, s in P:
+        Wd = W.to(dev).requires_grad_(True)
+        Ad = A.to(dev).requires_grad_(True)
+        Bd = B.to(dev).requires_grad_(True)
+        leaves.append((Wd, Ad, Bd))
+        args += [Wd, Ad, Bd, s]
+    Q, K, V = _LoRA_QKV.apply(Xd, *args)
+    (Q.sum() + K.sum() + V.sum()).backward()
+    Xr = X.float().requires_grad_(True)
+    refs = []
+    for W, A, B, s in P:
+        Ar = A.float().requires_grad_(True)
+        Br = B.float().requires_grad_(True)
+        refs.append((Ar, Br, Xr @ W.float().t() + (Xr @ Ar.t()) @ Br.t() * s))
+    sum(o.sum() for _, _, o in refs).backward()
+    for o, (_, _, ro) in zip((Q, K, V), refs):
+        assert rel_fro(o, ro) <= 2e-2
+    assert rel_fro(Xd.grad, Xr.grad) <= 2e-2
+    for (Wd, Ad, Bd), (Ar, Br, _) in zip(leaves, refs):
+        assert Wd.grad is None
+        assert rel_fro(Ad.grad, Ar.grad) <= 2e-2
+        assert rel_fro(Bd.grad, Br.grad) <= 2e-2
+
+
+def test_lora_special_cases(dev):
+    from metal_liger_amd.ops.fused_lora import _LoRA_QKV
+    N, IN = 64, 128
+    X = seeded((N, IN), 3, BF)
+    base = [adapter(128, IN, 16, 60 + i) for i in range(3)]
+    dys = [seeded((N, 128), 70 + i, BF) for i in range(3)]
+    # B = 0 -> dA = 0 exactly; A = 0 -> dB = 0 exactly
+    p0 = [(W, A, torch.zeros_like(B), 2.0) for W, A, B in base]
+    _, _, leaves = run_qkv(dev, X, p0, dys)
+    assert all(a.grad.abs().max().item() == 0 for a, _ in leaves)
+    p1 = [(W, torch.zeros_like(A), B, 2.0) for W, A, B in base]
+    _, _, leaves = run_qkv(dev, X, p1, dys)
+    assert all(b.grad.abs().max().item() == 0 for _, b in leaves)
+    # s = 0 -> dX is the base contribution only
+    p2 = [(W, A, B, 0.0) for W, A, B in base]
+    _, dX, _ = run_qkv(dev, X, p2, dys)
+    expect = sum(d.float() @ W.float() for d, (W, _, _) in zip(dys, base))
+    assert rel_fro(dX, expect) <= 1e-2
+
+
+def run_mlp(dev, X, params, dY):
+    from metal_liger_amd.ops.fused_lora import _LoRA_MLP
+    Xd = X.to(dev).requires_grad_(True)
+    args, leaves = [], []
+    for (W, A, B, s) in params:
+        Ad = A.to(dev).requires_grad_(True)
+        Bd = B.to(dev).requires_grad_(True)
+        leaves.append((Ad, Bd))
+        args += [W.to(dev), Ad, Bd, s]
+    out = _LoRA_MLP.apply(Xd, *args)
+    out.backward(dY.to(dev))
+    return out, Xd.grad, leaves
+
+
+@pytest.mark.parametrize("N,H,I,r", [(48, 128, 256, 8), (200, 256, 768, 16)])
+def test_lora_mlp_small(dev, N, H, I, r):
+    X = seeded((N, H), 5, BF)
+    G = adapter(I, H, r, 80, w_std=0.1, b_std=0.05)
+    U = adapter(I, H, r, 83, w_std=0.1, b_std=0.05)
+    Dn = adapter(H, I, r, 86, w_std=0.1, b_std=0.05)
+    params = [(*G, 2.0), (*U, 2.0), (*Dn, 2.0)]
+    dY = seeded((N, H), 90, BF)
+    out, dX, leaves = run_mlp(dev, X, params, dY)
+    flat = [t for p in params for t in p]
+    rout, gate, up, h = ref.lora_mlp_forward(X, *flat)
+    rdX, *rdAB = ref.lora_mlp_backward(X, gate, up, h, dY, *flat)
+    fout, fg, fu, fh = ref.lora_mlp_forward(X.float(), *f32(flat))
+    fdX, *fdAB = ref.lora_mlp_backward(X.float(), fg, fu, fh, dY.float(), *f32(flat))
+    check(out, fout, rout, "mlp out")
+    check(dX, fdX, rdX, "mlp dX")
+    for i, (Ad, Bd) in enumerate(leaves):
+        check(Ad.grad.float(), fdAB[2 * i], rdAB[2 * i], f"mlp dA[{i}]")
+        check(Bd.grad.float(), fdAB[2 * i + 1], rdAB[2 * i + 1], f"mlp dB[{i}]")
+
+
+def _qwen3_layer(seed):
+    H, Iq, Ik, I, r = 2048, 2048, 1024, 6144, 16
+    X = seeded((8192, H), seed, BF)
+    qkv = [adapter(o, H, r, seed + 10 * (i + 1)) for i, o in enumerate((Iq, Ik, Ik))]
+    mlp = [adapter(I, H, r, seed + 40), adapter(I, H, r, seed + 50), adapter(H, I, r, seed + 60)]
+    return X, qkv, mlp
+
+
+def test_lora_qkv_config(dev):
+    """Qwen3-style 2B layer: X [8192, 2048], Wq [2048,2048], Wk/Wv [1024,2048],
+    r 16, alpha 32 (s = 2), A ~N(0,1/16), B ~N(0,0.02), dQ/dK/dV ~N(0,1)."""
+    X, qkv, _ = _qwen3_layer(0)
+    params = [(W, A, B, 2.0) for W, A, B in qkv]
+    dys = [seeded((8192, W.shape[0]), 100 + i, BF) for i, (W, _, _) in enumerate(qkv)]
+    outs, dX, leaves = run_qkv(dev, X, params, dys)
+    flat = [t.to(dev) if torch.is_tensor(t) else t for p in params for t in p]
+    Xg = X.to(dev)
+    dyg = [d.to(dev) for d in dys]
+    rdX, *rdAB = ref.lora_qkv_backward(Xg, *dyg, *flat)
+    fdX, *fdAB = ref.lora_qkv_backward(Xg.float(), *f32(dyg), *f32(flat))
+    check(dX, fdX, rdX, "dX config")
+    for i, (Ad, Bd) in enumerate(leaves):
+        check(Ad.grad.float(), fdAB[2 * i], rdAB[2 * i], f"dA[{i}] config")
+        check(Bd.grad.float(), fdAB[2 * i + 1], rdAB[2 * i + 1], f"dB[{i}] config")
+
+
+def test_lora_mlp_config(dev):
+    X, _, mlp = _qwen3_layer(1)
+    params = [(W, A, B, 2.0) for W, A, B in mlp]
+    dY = seeded((8192, 2048), 120, BF)
+    out, dX, leaves = run_mlp(dev, X, params, dY)
+    flat = [t.to(dev) if torch.is_tensor(t) else t for p in params for t in p]
+    Xg = X.to(dev)
+    dYg = dY.to(dev)
+    rout, gate, up, h = ref.lora_mlp_forward(Xg, *flat)
+    rdX, *rdAB = ref.lora_mlp_backward(Xg, gate, up, h, dYg, *flat)
+    del gate, up, h
+    fout, fg, fu, fh = ref.lora_mlp_forward(Xg.float(), *f32(flat))
+    fdX, *fdAB = ref.lora_mlp_backward(Xg.float(), fg, fu, fh, dYg.float(), *f32(flat))
+    check(out, fout, rout, "mlp out config")
+    check(dX, fdX, rdX, "mlp dX config")
+    for i, (Ad, Bd) in enumerate(leaves):
+        check(Ad.grad.float(), fdAB[2 * i], rdAB[2 * i], f"mlp dA[{i}] config")
+        check(Bd.grad.float(), fdAB[2 * i + 1], rdAB[2 * i + 1], f"mlp dB[{i}] config")
+
+
+def test_lora_rejects_fp32(dev):
+    from metal_liger_amd.ops.fused_lora import _LoRA_QKV
+    X = torch.randn(4, 64, device=dev)
+    W = torch.randn(64, 64, device=dev)
+    A = torch.randn(8, 64, device=dev)
+    B = torch.randn(64, 8, device=dev)
+    with pytest.raises(TypeError, match="bf16"):
+        _LoRA_QKV.apply(X, W, A, B, 2.0, W, A, B, 2.0, W, A, B, 2.0)
