@@ -249,8 +249,13 @@ def patch_fused_lora(model: nn.Module) -> int:
     the fused functions (ops/fused_lora.py:323-421). Modules are not
     replaced: attention forwards shadow q/k/v_proj in the instance __dict__
     with the precomputed fused results for the duration of the call, so
-    state_dict keys stay unchanged. Returns the number of patched modules."""
-    base = model.base_model.model if hasattr(model, 'base_model') else model
+    state_dict keys stay unchanged. Returns the number of patched modules.
+
+    The layer search starts at PEFT's ``base_model.model``; a bare HF model's
+    ``base_model`` (its decoder, which has no ``.model``) is searched as is,
+    where the reference raises AttributeError."""
+    base = getattr(model, 'base_model', model)
+    base = getattr(base, 'model', base)
 
     def _find_layers_list(m, depth=0):
         if depth > 6:

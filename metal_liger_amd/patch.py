@@ -1,0 +1,152 @@
+"""Model patcher: swaps a HuggingFace Qwen3 / Qwen3-VL model's RMSNorms, SwiGLU
+MLPs and (with LoRA) attention / MLP projections onto the fused ops.
+
+Same entry point and behaviour as the reference's patch.py:181-240
+(``apply_metal_liger_to_qwen3vl``): decoder layers and the final norm are
+located through the same wrapping layouts (bare HF, PEFT, Qwen3-VL's nested
+language_model, accelerate), RMSNorm modules are replaced by
+MetalLigerRMSNorm sharing the original weight storage (state_dict keys
+unchanged), MLPs by MetalLigerSwiGLU, and LoRA projections are routed through
+the fused LoRA functions without replacing modules.
+"""
+
+import logging
+
+import torch.nn as nn
+
+from metal_liger_amd.ops.fused_lora import patch_fused_lora
+from metal_liger_amd.ops.fused_rms_norm import MetalLigerRMSNorm
+from metal_liger_amd.ops.fused_swiglu import MetalLigerSwiGLU
+
+logger = logging.getLogger(__name__)
+
+# Attribute paths to the decoder-layer list, most specific first
+# (patch.py:36-54 of the reference).
+_LAYER_PATHS = (
+    ("base_model", "model", "model", "language_model", "layers"),  # PEFT + Qwen3-VL
+    ("base_model", "model", "model", "layers"),                    # PEFT
+    ("model", "language_model", "layers"),                         # Qwen3-VL
+    ("model", "layers"),                                           # HF causal LM
+    ("layers",),                                                   # bare decoder
+    ("module", "model", "layers"),                                 # accelerate wrapper
+)
+
+# Attribute paths to the final norm's parent (patch.py:69-81).
+_NORM_PARENT_PATHS = (
+    ("base_model", "model", "model", "language_model"),
+    ("model", "language_model"),
+    ("base_model", "model", "model"),
+    ("model",),
+)
+
+
+def _resolve(obj, path):
+    for name in path:
+        obj = getattr(obj, name, None)
+        if obj is None:
+            return None
+    return obj
+
+
+def _find_layers(model: nn.Module):
+    """First non-empty decoder-layer list along _LAYER_PATHS, else None."""
+    for path in _LAYER_PATHS:
+        try:
+            layers = _resolve(model, path)
+            if layers is not None and len(layers) > 0:
+                return layers
+        except (AttributeError, TypeError):
+            continue
+    return None
+
+
+def _find_final_norm(model: nn.Module):
+    """(norm module, parent) of the final norm, or (None, None)."""
+    for path in _NORM_PARENT_PATHS:
+        parent = _resolve(model, path)
+        norm = getattr(parent, "norm", None) if parent is not None else None
+        if norm is not None and hasattr(norm, "weight"):
+            return norm, parent
+    return None, None
+
+
+def _fused_norm_like(old: nn.Module) -> MetalLigerRMSNorm:
+    eps = getattr(old, "variance_epsilon", getattr(old, "eps", 1e-6))
+    return MetalLigerRMSNorm(hidden_size=old.weight.shape[0], eps=eps, weight=old.weight.data)
+
+
+def _replace_rms_norms(model: nn.Module) -> int:
+    """Replaces each layer's input / post-attention norm and the final norm;
+    returns the number replaced (patch.py:92-159)."""
+    layers = _find_layers(model)
+    if layers is None:
+        logger.warning("MetalLiger: could not find transformer layers for RMSNorm patching")
+        return 0
+    count = 0
+    for layer in layers:
+        for name in ("input_layernorm", "post_attention_layernorm"):
+            if hasattr(layer, name):
+                setattr(layer, name, _fused_norm_like(getattr(layer, name)))
+                count += 1
+    old, parent = _find_final_norm(model)
+    if old is not None:
+        parent.norm = _fused_norm_like(old)
+        count += 1
+    return count
+
+
+def _replace_mlps(model: nn.Module) -> int:
+    """Wraps every layer MLP that has gate_proj in MetalLigerSwiGLU (patch.py:162-178)."""
+    layers = _find_layers(model)
+    if layers is None:
+        return 0
+    count = 0
+    for layer in layers:
+        if hasattr(layer, "mlp") and hasattr(layer.mlp, "gate_proj"):
+            layer.mlp = MetalLigerSwiGLU(layer.mlp)
+            count += 1
+    return count
+
+
+def apply_metal_liger_to_qwen3vl(
+    model: nn.Module,
+    fuse_rms_norm: bool = True,
+    fuse_swiglu: bool = True,
+    fuse_rope: bool = False,
+    fuse_cross_entropy: bool = False,
+    fuse_lora: bool = True,
+    use_optimized_generator: bool = False,
+) -> nn.Module:
+    """Apply the fused operations to a Qwen3 / Qwen3-VL model in place and
+    return it (patch.py:181-240).
+
+    fuse_rope / fuse_cross_entropy only log, as in the reference: RoPE is
+    applied with apply_fused_rotary / apply_fused_rotary_inline and the loss
+    with MetalLigerFusedLinearCrossEntropy by the caller.
+    use_optimized_generator is not part of this build (inference path).
+    """
+    stats = {}
+    if fuse_rms_norm:
+        n = _replace_rms_norms(model)
+        stats["rms_norm"] = n
+        logger.info(f"MetalLiger: replaced {n} RMSNorm layers with fused versions")
+    if fuse_swiglu:
+        n = _replace_mlps(model)
+        stats["swiglu"] = n
+        logger.info(f"MetalLiger: replaced {n} MLP layers with fused SwiGLU")
+    if fuse_lora:
+        n = patch_fused_lora(model)
+        stats["fused_lora"] = n
+        logger.info(f"MetalLiger: fused LoRA QKV+MLP marked {n} modules")
+    if use_optimized_generator:
+        logger.warning("MetalLiger: the optimized generator is not part of this build; skipped")
+        stats["generator"] = "unavailable"
+    if fuse_rope:
+        logger.info("MetalLiger: fused RoPE — use apply_fused_rotary() / apply_fused_rotary_inline()")
+        stats["rope"] = "available"
+    if fuse_cross_entropy:
+        logger.info("MetalLiger: fused CE — use MetalLigerFusedLinearCrossEntropy in trainer")
+        stats["cross_entropy"] = "available"
+    total = sum(v for v in stats.values() if isinstance(v, int))
+    logger.info(f"MetalLiger: {total} total layers patched. Details: {stats}")
+    return model

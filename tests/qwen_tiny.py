@@ -1,0 +1,65 @@
+"""A tiny Qwen3 causal LM (HF transformers) with PEFT-layout LoRA adapters,
+for patcher and end-to-end tests."""
+
+import torch
+import torch.nn as nn
+
+from tests.peft_shim import LoraLinear, init_lora, wrap_lora
+
+
+def tiny_config(**kw):
+    from transformers import Qwen3Config
+    cfg = dict(vocab_size=512, hidden_size=128, intermediate_size=256, num_hidden_layers=2,
+               num_attention_heads=4, num_key_value_heads=2, head_dim=32, rms_norm_eps=1e-6,
+               rope_theta=1e6, max_position_embeddings=256, tie_word_embeddings=False)
+    cfg.update(kw)
+    return Qwen3Config(**cfg)
+
+
+class PeftLike(nn.Module):
+    """PeftModel -> LoraModel -> causal LM nesting (base_model.model)."""
+
+    def __init__(self, lm: nn.Module):
+        super().__init__()
+        self.base_model = nn.Module()
+        self.base_model.model = lm
+
+    def forward(self, *a, **k):
+        return self.base_model.model(*a, **k)
+
+
+def build(seed=0, lora=True, peft_wrap=True, attn="eager", dtype=torch.float32):
+    from transformers import Qwen3ForCausalLM
+    torch.manual_seed(seed)
+    cfg = tiny_config()
+    cfg._attn_implementation = attn
+    lm = Qwen3ForCausalLM(cfg).to(dtype)
+    if lora:
+        for i, layer in enumerate(lm.model.layers):
+            wrap_lora(layer.self_attn, ["q_proj", "k_proj", "v_proj", "o_proj"], r=16, alpha=32)
+            wrap_lora(layer.mlp, ["gate_proj", "up_proj", "down_proj"], r=16, alpha=32)
+            for j, m in enumerate(list(layer.self_attn.children()) + list(layer.mlp.children())):
+                if isinstance(m, LoraLinear):
+                    init_lora(m, 1000 * seed + 10 * i + j)
+        lm.to(dtype)
+    return PeftLike(lm) if peft_wrap else lm
+
+
+def register_fp32_attention(name="ml_fp32_eager"):
+    """Eager attention evaluated in fp32 with contiguous operands (the bf16
+    batched products with transposed right operands are avoided on ROCm)."""
+    from transformers import AttentionInterface
+    from transformers.models.qwen3.modeling_qwen3 import repeat_kv
+
+    def attn(module, query, key, value, attention_mask, scaling, dropout=0.0, **kwargs):
+        k = repeat_kv(key, module.num_key_value_groups).float()
+        v = repeat_kv(value, module.num_key_value_groups).float().contiguous()
+        w = torch.matmul(query.float().contiguous(), k.transpose(2, 3).contiguous()) * scaling
+        if attention_mask is not None:
+            w = w + attention_mask.float()
+        w = torch.softmax(w, dim=-1)
+        out = torch.matmul(w, v).to(query.dtype)
+        return out.transpose(1, 2).contiguous(), None
+
+    AttentionInterface.register(name, attn)
+    return name
