@@ -15,8 +15,12 @@ its average launch duration from HIP events on its stream around 20
 back-to-back launches, against 8 TB/s.
 cpu_baseline: the oracle (a CPU restatement of the reference's torch ops)
 on a bounded sample of the same workload, on the host's cores.
+breakdown: each op's average launch time; plus, outside the step, chunked
+FLCE fwd+bwd (hidden [8192, 2048], lm_head [151936, 2048], chunk 8192:
+15.29 TFLOP) and the fused LoRA backward of a Qwen3-style 2B layer (QKV +
+MLP, rank 16: 774.2 GFLOP), as TFLOP/s against the 2.5 PFLOP/s bf16 peak.
 
-Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline]
+Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline] [--no-mfma-ops] [--pmc-probe]
 """
 
 from __future__ import annotations
@@ -46,6 +50,138 @@ def seeded(shape, seed, dtype):
     import torch
     g = torch.Generator().manual_seed(seed)
     return torch.randn(*shape, generator=g, dtype=torch.float32).to(dtype)
+
+
+FLCE_N, FLCE_H, FLCE_V, FLCE_CHUNK = 8192, 2048, 151936, 8192
+FLCE_FLOP = 3 * 2 * FLCE_N * FLCE_V * FLCE_H                 # logits, dH, dW
+LORA_N, LORA_H, LORA_KV, LORA_I, LORA_R = 8192, 2048, 1024, 6144, 16
+LORA_BWD_FLOP = 774_167_855_104                             # QKV + MLP backward, necessary FLOPs
+MFMA_PEAK_TFLOPS = 2500.0
+
+
+def gpu_randn(shape, seed, dev, scale=1.0, dtype=None):
+    import torch
+    g = torch.Generator(device=dev).manual_seed(seed)
+    t = torch.randn(*shape, generator=g, device=dev, dtype=torch.float32)
+    if scale != 1.0:
+        t.mul_(scale)
+    return t.to(dtype or torch.bfloat16)
+
+
+def time_launches(fn, stream, reps):
+    """Average milliseconds per call over `reps` back-to-back calls (events on
+    the stream the kernels are launched on)."""
+    import torch
+    fn()
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
+    a.record(stream)
+    for _ in range(reps):
+        fn()
+    b.record(stream)
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / reps
+
+
+def bench_flce(dev, stream, reps):
+    """Chunked fused linear cross-entropy fwd + bwd: hidden [8192, 2048],
+    lm_head [151936, 2048] ~N(0, 0.02), no bias, 10% of labels ignored,
+    chunk 8192; 15.29 TFLOP per fwd+bwd."""
+    import torch
+
+    from metal_liger_amd import hip_ops
+    h = gpu_randn((FLCE_N, FLCE_H), 10, dev)
+    w = gpu_randn((FLCE_V, FLCE_H), 11, dev, 0.02)
+    g = torch.Generator(device=dev).manual_seed(12)
+    lab = torch.randint(0, FLCE_V, (FLCE_N,), generator=g, device=dev)
+    lab[torch.rand(FLCE_N, generator=g, device=dev) < 0.1] = -100
+    one = torch.ones((), device=dev)
+    state = {}
+
+    def fwd():
+        state["f"] = hip_ops.flce_fwd(h, w, lab)
+
+    def bwd():
+        _, lse, nv = state["f"]
+        hip_ops.flce_bwd(h, w, lab, None, -100, lse, nv, one, FLCE_CHUNK)
+
+    f_ms = time_launches(fwd, stream, reps)
+    b_ms = time_launches(bwd, stream, reps)
+    tot = f_ms + b_ms
+    tf = FLCE_FLOP / (tot * 1e-3) / 1e12
+    del h, w, lab, state
+    torch.cuda.empty_cache()
+    return {"fwd_ms": round(f_ms, 3), "bwd_ms": round(b_ms, 3), "TFLOP/s": round(tf, 1),
+            "mfma_frac": round(tf / MFMA_PEAK_TFLOPS, 4), "flop": FLCE_FLOP}
+
+
+def bench_lora_bwd(dev, stream, reps):
+    """Fused LoRA backward of a Qwen3-style 2B layer (QKV + MLP): X [8192, 2048],
+    Wq [2048, 2048], Wk/Wv [1024, 2048], Wgate/Wup [6144, 2048], Wdown
+    [2048, 6144] ~N(0, 0.02), rank 16, alpha 32, A ~N(0, 1/16), B ~N(0, 0.02);
+    forward intermediates made by the library's forward ops beforehand."""
+    import torch
+
+    from metal_liger_amd import hip_ops
+    N, H, KV, I, r = LORA_N, LORA_H, LORA_KV, LORA_I, LORA_R
+    s = 2.0
+    x = gpu_randn((N, H), 20, dev)
+    outs = (H, KV, KV)
+    Wqkv = [gpu_randn((o, H), 21 + i, dev, 0.02) for i, o in enumerate(outs)]
+    a_qkv = gpu_randn((3 * r, H), 24, dev, 0.25)
+    Bqkv = [gpu_randn((o, r), 25 + i, dev, 0.02) for i, o in enumerate(outs)]
+    dqkv = [gpu_randn((N, o), 28 + i, dev) for i, o in enumerate(outs)]
+    xa = hip_ops.lora_xa(x, a_qkv)
+    WG, WU = gpu_randn((I, H), 31, dev, 0.02), gpu_randn((I, H), 32, dev, 0.02)
+    WD = gpu_randn((H, I), 33, dev, 0.02)
+    a_gu = gpu_randn((2 * r, H), 34, dev, 0.25)
+    a_d = gpu_randn((r, I), 35, dev, 0.25)
+    BG, BU = gpu_randn((I, r), 36, dev, 0.02), gpu_randn((I, r), 37, dev, 0.02)
+    BD = gpu_randn((H, r), 38, dev, 0.02)
+    dy = gpu_randn((N, H), 39, dev)
+    xa_gu = hip_ops.lora_xa(x, a_gu)
+    gate = hip_ops.lora_linear_out(x, WG, xa_gu[:, :r], BG * s)
+    up = hip_ops.lora_linear_out(x, WU, xa_gu[:, r:], BU * s)
+    hmid = hip_ops.swiglu_fwd(gate, up)
+    ha_d = hip_ops.lora_xa(hmid, a_d)
+
+    def qkv():
+        hip_ops.lora_qkv_bwd(x, dqkv, Wqkv, a_qkv, Bqkv, [s, s, s], xa, r)
+
+    def mlp():
+        hip_ops.lora_mlp_bwd(x, gate, up, hmid, dy, WG, WU, WD, a_gu, a_d, BG, BU, BD,
+                             [s, s, s], xa_gu, ha_d, r)
+
+    q_ms = time_launches(qkv, stream, reps)
+    m_ms = time_launches(mlp, stream, reps)
+    tot = q_ms + m_ms
+    tf = LORA_BWD_FLOP / (tot * 1e-3) / 1e12
+    return {"qkv_ms": round(q_ms, 3), "mlp_ms": round(m_ms, 3), "TFLOP/s": round(tf, 1),
+            "mfma_frac": round(tf / MFMA_PEAK_TFLOPS, 4), "flop": LORA_BWD_FLOP,
+            "tokens_per_s": round(N / (tot * 1e-3), 1)}
+
+
+def pmc_probe(dev):
+    """Launch sequence for rocprofv3 --pmc traffic counting: 3 copies of a
+    1 GiB buffer (the calibration: a plain copy reads and writes exactly
+    1 GiB each), then 5 launches of the SwiGLU backward on gate, up, dy
+    [8192, 6144] bf16 (503,316,480 algorithmic bytes per launch)."""
+    import torch
+
+    from metal_liger_amd import hip_ops
+    src = torch.empty(1 << 30, dtype=torch.uint8, device=dev).fill_(1)
+    dst = torch.empty_like(src)
+    gate = gpu_randn((N_TOK, INTER), 0, dev)
+    up = gpu_randn((N_TOK, INTER), 1, dev)
+    dy = gpu_randn((N_TOK, INTER), 2, dev)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    for _ in range(5):
+        hip_ops.swiglu_bwd(gate, up, dy)
+    torch.cuda.synchronize()
+    print("pmc probe: 3 x 1 GiB copy, 5 x swiglu_bwd [8192, 6144] bf16", flush=True)
 
 
 def load_traffic():
@@ -117,6 +253,10 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--pmc-probe", action="store_true",
+                    help="only the launch sequence used for rocprofv3 --pmc traffic counting")
+    ap.add_argument("--no-mfma-ops", action="store_true",
+                    help="skip the FLCE / LoRA-backward lines of the breakdown")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -129,6 +269,9 @@ def main():
 
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
+    if args.pmc_probe:
+        pmc_probe(dev)
+        return
     bf = torch.bfloat16
     gate = seeded((N_TOK, INTER), 0, bf).to(dev)
     up = seeded((N_TOK, INTER), 1, bf).to(dev)
@@ -192,6 +335,9 @@ def main():
                      "GB/s": round(op_bytes[n] / (per_op[n] * 1e-3) / 1e9, 1)}
                  for n in per_op}
     breakdown["gpu_ms_per_step"] = round(gpu_ms_step, 4)
+    if not args.no_mfma_ops:
+        breakdown["flce_fwd_bwd"] = bench_flce(dev, stream, 5)
+        breakdown["lora_bwd_layer"] = bench_lora_bwd(dev, stream, 10)
     dom_ms = per_op["swiglu_bwd"]
     achieved = SWIGLU_BWD_BYTES / (dom_ms * 1e-3) / 1e9
     roofline = {
