@@ -83,6 +83,27 @@ def time_launches(fn, stream, reps):
     return a.elapsed_time(b) / reps
 
 
+RMS_N, RMS_H = 8192, 2048
+RMS_FWD_BYTES = 2 * RMS_N * RMS_H * 4 + RMS_H * 4 + RMS_N * 4          # x, w in; y, rrms out
+RMS_BWD_BYTES = 3 * RMS_N * RMS_H * 4 + 2 * RMS_H * 4 + RMS_N * 4      # x, dy, w, rrms in; dx, dw out
+
+
+def bench_rmsnorm(dev, stream, reps):
+    """RMSNorm fwd and bwd, fp32 x [8192, 2048], weight 1 + 0.1 N(0, 1),
+    eps 1e-6 (rrms saved by the forward, as the autograd Function does)."""
+    import torch
+
+    from metal_liger_amd import hip_ops
+    x = gpu_randn((RMS_N, RMS_H), 40, dev, dtype=torch.float32)
+    w = (1.0 + 0.1 * gpu_randn((RMS_H,), 41, dev, dtype=torch.float32))
+    dy = gpu_randn((RMS_N, RMS_H), 42, dev, dtype=torch.float32)
+    _, rrms = hip_ops.rms_norm_fwd(x, w, 1e-6)
+    f_ms = time_launches(lambda: hip_ops.rms_norm_fwd(x, w, 1e-6), stream, reps)
+    b_ms = time_launches(lambda: hip_ops.rms_norm_bwd(x, w, dy, rrms, 1e-6), stream, reps)
+    return {"fwd_us": round(f_ms * 1e3, 2), "fwd_GB/s": round(RMS_FWD_BYTES / (f_ms * 1e-3) / 1e9, 1),
+            "bwd_us": round(b_ms * 1e3, 2), "bwd_GB/s": round(RMS_BWD_BYTES / (b_ms * 1e-3) / 1e9, 1)}
+
+
 def bench_flce(dev, stream, reps):
     """Chunked fused linear cross-entropy fwd + bwd: hidden [8192, 2048],
     lm_head [151936, 2048] ~N(0, 0.02), no bias, 10% of labels ignored,
@@ -335,6 +356,7 @@ def main():
                      "GB/s": round(op_bytes[n] / (per_op[n] * 1e-3) / 1e9, 1)}
                  for n in per_op}
     breakdown["gpu_ms_per_step"] = round(gpu_ms_step, 4)
+    breakdown["rmsnorm_fp32"] = bench_rmsnorm(dev, stream, reps)
     if not args.no_mfma_ops:
         breakdown["flce_fwd_bwd"] = bench_flce(dev, stream, 5)
         breakdown["lora_bwd_layer"] = bench_lora_bwd(dev, stream, 10)
