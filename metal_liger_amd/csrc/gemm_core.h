@@ -160,21 +160,43 @@ __device__ __forceinline__ void setup_tile(TileIter& it, const Operand& op, int 
     setup_mnmajor<ROWS>(it, op, row0, rows, tid);
 }
 
-// Loads the k-tile starting at k0 of a segment of length klen; k past klen
-// reads as zero (from an always-valid address: the tile origin).
+// Loads the k-tile starting at k0 (< klen) of a segment of length klen.
+// Interior tiles (k0 + 64 <= klen, a uniform test) load unpredicated from a
+// uniform base plus 32-bit per-thread offsets. In a segment's last, partial
+// tile the lanes whose k lies past klen read the tile origin instead (always
+// in bounds); store_tile zeroes their data. Nothing consumes the loaded
+// registers before the LDS store, so the load latency overlaps the MFMAs.
 template <int LAYOUT, int ROWS>
 __device__ __forceinline__ void load_tile(TileRegs& t, const TileIter& it, int k0, int klen,
                                           int tid) {
+  // MN-major tiles narrower than the block: only the first ROWS / 8 x 8
+  // threads hold a block (store_mnmajor skips the others too).
+  if (LAYOUT == kMNMajor && ROWS < kThreads && ((tid >> 3) << 3) >= ROWS) return;
   const char* b = it.base + (int64_t)k0 * it.kstride;
+  constexpr int NL = (LAYOUT == kKMajor) ? kmajor_chunks<ROWS>() : 8;
+  if (k0 + kBK <= klen) {
+#pragma unroll
+    for (int i = 0; i < NL; ++i) t.v[i] = *reinterpret_cast<const u32x4*>(b + it.off[i]);
+  } else {
+    const int kb8 = (tid & 7) << 3;
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+      const int kk = (LAYOUT == kKMajor) ? k0 + kb8 : k0 + kb8 + i;
+      t.v[i] = *reinterpret_cast<const u32x4*>(b + (kk < klen ? it.off[i] : 0u));
+    }
+  }
+}
+
+// Zeroes the chunks of a partial tile whose k lies past klen (uniform test).
+template <int LAYOUT, int ROWS>
+__device__ __forceinline__ void zero_tail(TileRegs& t, int k0, int klen, int tid) {
+  if (k0 + kBK <= klen) return;
   const int kb8 = (tid & 7) << 3;
   constexpr int NL = (LAYOUT == kKMajor) ? kmajor_chunks<ROWS>() : 8;
-  const bool active = (LAYOUT == kKMajor) || ((tid >> 3) << 3) < ROWS;
 #pragma unroll
   for (int i = 0; i < NL; ++i) {
     const int kk = (LAYOUT == kKMajor) ? k0 + kb8 : k0 + kb8 + i;
-    const bool kin = kk < klen && active;
-    const u32x4 val = *reinterpret_cast<const u32x4*>(kin ? b + it.off[i] : it.base);
-    t.v[i] = kin ? val : u32x4{0u, 0u, 0u, 0u};
+    if (kk >= klen) t.v[i] = u32x4{0u, 0u, 0u, 0u};
   }
 }
 
@@ -206,7 +228,8 @@ __device__ __forceinline__ void store_mnmajor(const TileRegs& t, char* lds, int 
 }
 
 template <int LAYOUT, int ROWS>
-__device__ __forceinline__ void store_tile(const TileRegs& t, char* lds, int tid) {
+__device__ __forceinline__ void store_tile(TileRegs& t, char* lds, int tid, int k0, int klen) {
+  zero_tail<LAYOUT, ROWS>(t, k0, klen, tid);
   if constexpr (LAYOUT == kKMajor)
     store_kmajor<ROWS>(t, lds, tid);
   else
@@ -214,27 +237,82 @@ __device__ __forceinline__ void store_tile(const TileRegs& t, char* lds, int tid
 }
 
 // ----------------------------------------------------------------- compute --
+// Scheduling-group masks of __builtin_amdgcn_sched_group_barrier.
+constexpr int kSchedMfma = 0x008;
+constexpr int kSchedDsRead = 0x100;
+constexpr int kSchedDsWrite = 0x200;
+
+// Fragments of one 16-wide k-step for a wave: TM A fragments, TN B fragments.
+template <class C>
+struct Frags {
+  bf16x8_t a[C::TM], b[C::TN];
+};
+
+template <class C>
+__device__ __forceinline__ void load_frags(Frags<C>& f, const char* As, const char* Bs, int wm,
+                                           int wn, int lane, int s) {
+  const int lr = lane & 31;
+  const int c = 2 * s + (lane >> 5);
+  // B first: the first TN MFMAs of a step use every B fragment and A[0].
+#pragma unroll
+  for (int j = 0; j < C::TN; ++j)
+    f.b[j] = *reinterpret_cast<const bf16x8_t*>(Bs + lds_off(wn + 32 * j + lr, c));
+#pragma unroll
+  for (int i = 0; i < C::TM; ++i)
+    f.a[i] = *reinterpret_cast<const bf16x8_t*>(As + lds_off(wm + 32 * i + lr, c));
+}
+
+template <class C>
+__device__ __forceinline__ void mfma_step(f32x16_t (&acc)[C::TM][C::TN], const Frags<C>& f) {
+#pragma unroll
+  for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+    for (int j = 0; j < C::TN; ++j)
+      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[i], f.b[j], acc[i][j], 0, 0, 0);
+}
+
+// Interleaves the next k-step's LDS reads with this k-step's MFMAs: the
+// compiler otherwise serialises each fragment read against the MFMAs that
+// consume it and exposes the LDS latency every few MFMAs.
+template <class C>
+__device__ __forceinline__ void sched_reads_between_mfmas() {
+  constexpr int kReads = C::TM + C::TN;
+  constexpr int kMfma = C::TM * C::TN;
+  constexpr int kPer = kMfma / kReads > 0 ? kMfma / kReads : 1;
+#pragma unroll
+  for (int q = 0; q < kReads; ++q) {
+    __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(kSchedMfma, kPer, 0);
+  }
+  if constexpr (kMfma > kPer * kReads)
+    __builtin_amdgcn_sched_group_barrier(kSchedMfma, kMfma - kPer * kReads, 0);
+}
+
+// One 64-wide k-tile from LDS stage (As, Bs): 4 k-steps with the fragments
+// of step s + 1 read while the MFMAs of step s run.
+// sched_barrier(0) fences each block so that the scheduler can only
+// interleave step s + 1's reads with step s's MFMAs, which keeps both
+// fragment sets live in distinct registers.
 template <class C>
 __device__ __forceinline__ void mma_tile(f32x16_t (&acc)[C::TM][C::TN], const char* As,
                                          const char* Bs, int wm, int wn, int lane) {
-  const int lr = lane & 31;
-  const int hk = lane >> 5;
-#pragma unroll
-  for (int s = 0; s < kBK / 16; ++s) {
-    const int c = 2 * s + hk;
-    bf16x8_t af[C::TM], bfr[C::TN];
-#pragma unroll
-    for (int i = 0; i < C::TM; ++i)
-      af[i] = *reinterpret_cast<const bf16x8_t*>(As + lds_off(wm + 32 * i + lr, c));
-#pragma unroll
-    for (int j = 0; j < C::TN; ++j)
-      bfr[j] = *reinterpret_cast<const bf16x8_t*>(Bs + lds_off(wn + 32 * j + lr, c));
-#pragma unroll
-    for (int i = 0; i < C::TM; ++i)
-#pragma unroll
-      for (int j = 0; j < C::TN; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
-  }
+  Frags<C> f0, f1;
+  load_frags<C>(f0, As, Bs, wm, wn, lane, 0);
+  __builtin_amdgcn_sched_barrier(0);
+  load_frags<C>(f1, As, Bs, wm, wn, lane, 1);
+  mfma_step<C>(acc, f0);
+  sched_reads_between_mfmas<C>();
+  __builtin_amdgcn_sched_barrier(0);
+  load_frags<C>(f0, As, Bs, wm, wn, lane, 2);
+  mfma_step<C>(acc, f1);
+  sched_reads_between_mfmas<C>();
+  __builtin_amdgcn_sched_barrier(0);
+  load_frags<C>(f1, As, Bs, wm, wn, lane, 3);
+  mfma_step<C>(acc, f0);
+  sched_reads_between_mfmas<C>();
+  __builtin_amdgcn_sched_barrier(0);
+  mfma_step<C>(acc, f1);
+  __builtin_amdgcn_sched_barrier(0);
 }
 
 // Work item of this workgroup (XCD-aware, grouped); false if none.
@@ -305,34 +383,35 @@ __device__ __forceinline__ void mainloop(const Problem& pb, int tm, int tn, int 
   setup_tile<LB, C::BN>(ib, pb.seg[0].b, n0, pb.N, tid);
   load_tile<LA, C::BM>(ra, ia, k0, klen, tid);
   load_tile<LB, C::BN>(rb, ib, k0, klen, tid);
-  store_tile<LA, C::BM>(ra, smem, tid);
-  store_tile<LB, C::BN>(rb, smem + C::A_BYTES, tid);
+  store_tile<LA, C::BM>(ra, smem, tid, k0, klen);
+  store_tile<LB, C::BN>(rb, smem + C::A_BYTES, tid, k0, klen);
   __syncthreads();
 
-  for (int kt = 0; kt < nk; ++kt) {
+  // k-tile kt + 1 is loaded into registers while k-tile kt is multiplied
+  // from LDS stage kt % 2, then stored into the other stage.
+  for (int kt = 0; kt + 1 < nk; ++kt) {
     const int cur = kt & 1;
-    const bool more = kt + 1 < nk;
-    if (more) {
-      k0 += kBK;
-      if (k0 >= klen) {
-        ++seg;
-        k0 = 0;
-        klen = pb.seg[seg].k_len;
-        setup_tile<LA, C::BM>(ia, pb.seg[seg].a, m0, pb.M, tid);
-        setup_tile<LB, C::BN>(ib, pb.seg[seg].b, n0, pb.N, tid);
-      }
-      load_tile<LA, C::BM>(ra, ia, k0, klen, tid);
-      load_tile<LB, C::BN>(rb, ib, k0, klen, tid);
+    k0 += kBK;
+    if (k0 >= klen) {
+      ++seg;
+      k0 = 0;
+      klen = pb.seg[seg].k_len;
+      setup_tile<LA, C::BM>(ia, pb.seg[seg].a, m0, pb.M, tid);
+      setup_tile<LB, C::BN>(ib, pb.seg[seg].b, n0, pb.N, tid);
     }
+    load_tile<LA, C::BM>(ra, ia, k0, klen, tid);
+    load_tile<LB, C::BN>(rb, ib, k0, klen, tid);
     mma_tile<C>(acc, smem + cur * C::STAGE_BYTES, smem + cur * C::STAGE_BYTES + C::A_BYTES, wm,
                 wn, lane);
-    if (more) {
-      char* nxt = smem + (cur ^ 1) * C::STAGE_BYTES;
-      store_tile<LA, C::BM>(ra, nxt, tid);
-      store_tile<LB, C::BN>(rb, nxt + C::A_BYTES, tid);
-    }
+    char* nxt = smem + (cur ^ 1) * C::STAGE_BYTES;
+    store_tile<LA, C::BM>(ra, nxt, tid, k0, klen);
+    store_tile<LB, C::BN>(rb, nxt + C::A_BYTES, tid, k0, klen);
     __syncthreads();
   }
+  const int last = (nk - 1) & 1;
+  mma_tile<C>(acc, smem + last * C::STAGE_BYTES, smem + last * C::STAGE_BYTES + C::A_BYTES, wm, wn,
+              lane);
+  __syncthreads();  // the epilogue may reuse the LDS
 }
 
 // The GEMM kernel: mainloop + epilogue functor
