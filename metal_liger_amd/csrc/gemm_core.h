@@ -36,6 +36,8 @@
 //   so concurrently running tiles of one XCD share operands in its L2.
 #pragma once
 
+#include <utility>
+
 #include "common.h"
 
 namespace mla {
@@ -50,6 +52,12 @@ constexpr int kThreads = 256;
 constexpr int kMaxSeg = 8;
 constexpr int kRowBytes = kBK * 2;  // 128
 constexpr int kXcds = 8;
+
+// Default m-tiles per tile-order group (group_m = 0): with 32 blocks
+// resident per XCD, groups of 8 give each XCD an 8 x 4 patch of tiles.
+#ifndef ML_GEMM_GROUP_M
+#define ML_GEMM_GROUP_M 8
+#endif
 
 template <int BM_, int BN_, int WAVES_M_>
 struct Cfg {
@@ -236,11 +244,36 @@ __device__ __forceinline__ void store_tile(TileRegs& t, char* lds, int tid, int 
     store_mnmajor<ROWS>(t, lds, tid);
 }
 
+// Software-pipelined staging: a tile held in registers is written to LDS in
+// four parts, one per MFMA k-step, and each register is reloaded with the
+// following tile as soon as its part is written (K-major: the chunks just
+// stored; MN-major: all eight after the last part, since every row of the
+// 8 x 8 transpose reads all eight registers).
+template <int LAYOUT, int ROWS>
+constexpr int store_count(int part) {
+  if constexpr (LAYOUT == kKMajor) {
+    int n = 0;
+    for (int i = 0; i < kmajor_chunks<ROWS>(); ++i) n += (i * 4 / kmajor_chunks<ROWS>() == part);
+    return n;
+  } else {
+    return 2;
+  }
+}
+
+template <int LAYOUT, int ROWS>
+constexpr int reload_count(int part) {
+  if constexpr (LAYOUT == kKMajor)
+    return store_count<LAYOUT, ROWS>(part);
+  else
+    return part == 3 ? 8 : 0;
+}
+
 // ----------------------------------------------------------------- compute --
 // Scheduling-group masks of __builtin_amdgcn_sched_group_barrier.
 constexpr int kSchedMfma = 0x008;
 constexpr int kSchedDsRead = 0x100;
 constexpr int kSchedDsWrite = 0x200;
+constexpr int kSchedVmemRead = 0x020;
 
 // Fragments of one 16-wide k-step for a wave: TM A fragments, TN B fragments.
 template <class C>
@@ -315,6 +348,139 @@ __device__ __forceinline__ void mma_tile(f32x16_t (&acc)[C::TM][C::TN], const ch
   __builtin_amdgcn_sched_barrier(0);
 }
 
+// Compile-time loop: f(std::integral_constant<int, q>) for q = 0 .. N-1.
+template <class F, int... Q>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, Q...>) {
+  (f(std::integral_constant<int, Q>{}), ...);
+}
+template <int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+// Single operations of a k-step, addressed by compile-time index.
+// Fragment read q: B[q] for q < TN, then A[q - TN].
+template <class C, int Q>
+__device__ __forceinline__ void read_frag(Frags<C>& f, const char* As, const char* Bs, int wm,
+                                          int wn, int lane, int s) {
+  const int lr = lane & 31;
+  const int c = 2 * s + (lane >> 5);
+  if constexpr (Q < C::TN)
+    f.b[Q] = *reinterpret_cast<const bf16x8_t*>(Bs + lds_off(wn + 32 * Q + lr, c));
+  else
+    f.a[Q - C::TN] = *reinterpret_cast<const bf16x8_t*>(As + lds_off(wm + 32 * (Q - C::TN) + lr, c));
+}
+
+// First K-major chunk written in part P of a tile of NL chunks per thread.
+constexpr int part_first(int nl, int part) { return (part * nl + 3) / 4; }
+
+// The I-th LDS store of part P (K-major: chunk part_first + I; MN-major:
+// row 2P + I of the 8 x 8 block).
+template <int LAYOUT, int ROWS, int P, int I>
+__device__ __forceinline__ void store_one(const TileRegs& t, char* lds, int tid) {
+  if constexpr (LAYOUT == kKMajor) {
+    constexpr int i = part_first(kmajor_chunks<ROWS>(), P) + I;
+    const int q = tid + kThreads * i;
+    *reinterpret_cast<u32x4*>(lds + lds_off(q >> 3, q & 7)) = t.v[i];
+  } else {
+    const int kb = tid & 7;
+    const int rb = tid >> 3;
+    if (ROWS < kThreads && (rb << 3) >= ROWS) return;
+    constexpr int rr = 2 * P + I;
+    constexpr unsigned sel = (rr & 1) ? 0x07060302u : 0x05040100u;
+    u32x4 o;
+#pragma unroll
+    for (int pp = 0; pp < 4; ++pp)
+      o[pp] = __builtin_amdgcn_perm(t.v[2 * pp + 1][rr >> 1], t.v[2 * pp][rr >> 1], sel);
+    *reinterpret_cast<u32x4*>(lds + lds_off((rb << 3) + rr, kb)) = o;
+  }
+}
+
+// The I-th reload of part P (K-major: the chunk store_one<P, I> wrote;
+// MN-major, part 3 only: register I). Lanes whose k lies past klen read the
+// tile origin (in bounds); zero_tail clears them before the tile is stored.
+template <int LAYOUT, int ROWS, int P, int I>
+__device__ __forceinline__ void reload_one(TileRegs& t, const char* b, const TileIter& it, int k0,
+                                           int klen, int tid) {
+  if (LAYOUT == kMNMajor && ROWS < kThreads && ((tid >> 3) << 3) >= ROWS) return;
+  const int kb8 = (tid & 7) << 3;
+  if constexpr (LAYOUT == kKMajor) {
+    constexpr int i = part_first(kmajor_chunks<ROWS>(), P) + I;
+    t.v[i] = *reinterpret_cast<const u32x4*>(b + (k0 + kb8 < klen ? it.off[i] : 0u));
+  } else {
+    t.v[I] = *reinterpret_cast<const u32x4*>(b + (k0 + kb8 + I < klen ? it.off[I] : 0u));
+  }
+}
+
+// One k-step of the pipelined tile, in a fixed issue order: MFMA slot q
+// (q = 0 .. TM*TN-1) is preceded by the q-th fragment read of step S + 1,
+// the q-th LDS store of part S of the staged tile and the q-th reload;
+// sched_barrier(0) keeps the compiler from regrouping them.
+template <class C, int LA, int LB, bool RELOAD, int S>
+__device__ __forceinline__ void pipe_step(f32x16_t (&acc)[C::TM][C::TN], Frags<C>& fnext,
+                                          const Frags<C>& fcur, const char* As, const char* Bs,
+                                          int wm, int wn, int lane, TileRegs& ra, TileRegs& rb,
+                                          char* nxt, const char* bA, const char* bB,
+                                          const TileIter& ia, const TileIter& ib, int k0,
+                                          int klen, int tid) {
+  constexpr int kReads = S < 3 ? C::TM + C::TN : 0;
+  constexpr int kWa = store_count<LA, C::BM>(S), kWb = store_count<LB, C::BN>(S);
+  constexpr int kLa = RELOAD ? reload_count<LA, C::BM>(S) : 0;
+  constexpr int kLb = RELOAD ? reload_count<LB, C::BN>(S) : 0;
+  constexpr int kMfma = C::TM * C::TN;
+  // Stores: A in slots [0, kWa), B in [kWa, kWa + kWb). A reload never
+  // precedes the store that reads its register: K-major chunk i is stored
+  // and reloaded in one slot (store first); an MN-major operand's reloads
+  // start after its last store, since each transposed row reads all eight
+  // registers.
+  constexpr int kA0 = LA == kMNMajor ? kWa : 0;
+  constexpr int kB0min = LB == kMNMajor ? kWa + kWb : kWa;
+  constexpr int kB0 = kA0 + kLa > kB0min ? kA0 + kLa : kB0min;
+  constexpr int kMax1 = kReads > kWa + kWb ? kReads : kWa + kWb;
+  constexpr int kMax2 = kMax1 > kB0 + kLb ? kMax1 : kB0 + kLb;
+  constexpr int kSlots = kMfma > kMax2 ? kMfma : kMax2;
+  char* nxtB = nxt + C::A_BYTES;
+  static_for<kSlots>([&](auto qc) {
+    constexpr int q = decltype(qc)::value;
+    if constexpr (q < kReads) read_frag<C, q>(fnext, As, Bs, wm, wn, lane, S + 1);
+    if constexpr (q < kWa) store_one<LA, C::BM, S, q>(ra, nxt, tid);
+    else if constexpr (q < kWa + kWb) store_one<LB, C::BN, S, q - kWa>(rb, nxtB, tid);
+    if constexpr (q >= kA0 && q < kA0 + kLa)
+      reload_one<LA, C::BM, S, q - kA0>(ra, bA, ia, k0, klen, tid);
+    if constexpr (q >= kB0 && q < kB0 + kLb)
+      reload_one<LB, C::BN, S, q - kB0>(rb, bB, ib, k0, klen, tid);
+    if constexpr (q < kMfma) {
+      constexpr int i = q / C::TN, j = q % C::TN;
+      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fcur.a[i], fcur.b[j], acc[i][j], 0, 0, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  });
+}
+
+// A k-tile from LDS stage (As, Bs) while the registers (ra, rb) holding the
+// next tile are written to stage nxt and, with RELOAD, refilled with the
+// k-tile at k0 of the iterators (ia, ib).
+template <class C, int LA, int LB, bool RELOAD>
+__device__ __forceinline__ void mma_tile_pipelined(f32x16_t (&acc)[C::TM][C::TN], const char* As,
+                                                   const char* Bs, int wm, int wn, int lane,
+                                                   TileRegs& ra, TileRegs& rb, char* nxt,
+                                                   const TileIter& ia, const TileIter& ib, int k0,
+                                                   int klen, int tid) {
+  Frags<C> f0, f1;
+  load_frags<C>(f0, As, Bs, wm, wn, lane, 0);
+  __builtin_amdgcn_sched_barrier(0);
+  const char* bA = ia.base + (int64_t)k0 * ia.kstride;
+  const char* bB = ib.base + (int64_t)k0 * ib.kstride;
+  pipe_step<C, LA, LB, RELOAD, 0>(acc, f1, f0, As, Bs, wm, wn, lane, ra, rb, nxt, bA, bB, ia, ib,
+                                  k0, klen, tid);
+  pipe_step<C, LA, LB, RELOAD, 1>(acc, f0, f1, As, Bs, wm, wn, lane, ra, rb, nxt, bA, bB, ia, ib,
+                                  k0, klen, tid);
+  pipe_step<C, LA, LB, RELOAD, 2>(acc, f1, f0, As, Bs, wm, wn, lane, ra, rb, nxt, bA, bB, ia, ib,
+                                  k0, klen, tid);
+  pipe_step<C, LA, LB, RELOAD, 3>(acc, f0, f1, As, Bs, wm, wn, lane, ra, rb, nxt, bA, bB, ia, ib,
+                                  k0, klen, tid);
+}
+
 // Work item of this workgroup (XCD-aware, grouped); false if none.
 __device__ __forceinline__ bool tile_coords(const Problem& pb, int& tm, int& tn, int& split) {
   const int W = pb.tiles_m * pb.tiles_n * pb.ksplit;
@@ -387,10 +553,10 @@ __device__ __forceinline__ void mainloop(const Problem& pb, int tm, int tn, int 
   store_tile<LB, C::BN>(rb, smem + C::A_BYTES, tid, k0, klen);
   __syncthreads();
 
-  // k-tile kt + 1 is loaded into registers while k-tile kt is multiplied
-  // from LDS stage kt % 2, then stored into the other stage.
-  for (int kt = 0; kt + 1 < nk; ++kt) {
-    const int cur = kt & 1;
+  // Pipeline: while k-tile kt is multiplied from LDS stage kt % 2, the
+  // registers holding k-tile kt + 1 are written to the other stage, part by
+  // part, and refilled with k-tile kt + 2.
+  auto advance = [&]() {
     k0 += kBK;
     if (k0 >= klen) {
       ++seg;
@@ -399,16 +565,35 @@ __device__ __forceinline__ void mainloop(const Problem& pb, int tm, int tn, int 
       setup_tile<LA, C::BM>(ia, pb.seg[seg].a, m0, pb.M, tid);
       setup_tile<LB, C::BN>(ib, pb.seg[seg].b, n0, pb.N, tid);
     }
+  };
+  if (nk > 1) {
+    advance();
     load_tile<LA, C::BM>(ra, ia, k0, klen, tid);
     load_tile<LB, C::BN>(rb, ib, k0, klen, tid);
-    mma_tile<C>(acc, smem + cur * C::STAGE_BYTES, smem + cur * C::STAGE_BYTES + C::A_BYTES, wm,
-                wn, lane);
-    char* nxt = smem + (cur ^ 1) * C::STAGE_BYTES;
-    store_tile<LA, C::BM>(ra, nxt, tid, k0, klen);
-    store_tile<LB, C::BN>(rb, nxt + C::A_BYTES, tid, k0, klen);
+  }
+  int kt = 0;
+  for (; kt + 2 < nk; ++kt) {
+    const int cur = kt & 1;
+    const int k0s = k0, klens = klen;  // the tile in registers
+    advance();                         // the tile to load
+    zero_tail<LA, C::BM>(ra, k0s, klens, tid);
+    zero_tail<LB, C::BN>(rb, k0s, klens, tid);
+    char* st = smem + cur * C::STAGE_BYTES;
+    mma_tile_pipelined<C, LA, LB, true>(acc, st, st + C::A_BYTES, wm, wn, lane, ra, rb,
+                                        smem + (cur ^ 1) * C::STAGE_BYTES, ia, ib, k0, klen, tid);
     __syncthreads();
   }
-  const int last = (nk - 1) & 1;
+  if (kt + 1 < nk) {
+    const int cur = kt & 1;
+    zero_tail<LA, C::BM>(ra, k0, klen, tid);
+    zero_tail<LB, C::BN>(rb, k0, klen, tid);
+    char* st = smem + cur * C::STAGE_BYTES;
+    mma_tile_pipelined<C, LA, LB, false>(acc, st, st + C::A_BYTES, wm, wn, lane, ra, rb,
+                                         smem + (cur ^ 1) * C::STAGE_BYTES, ia, ib, k0, klen, tid);
+    __syncthreads();
+    ++kt;
+  }
+  const int last = kt & 1;
   mma_tile<C>(acc, smem + last * C::STAGE_BYTES, smem + last * C::STAGE_BYTES + C::A_BYTES, wm, wn,
               lane);
   __syncthreads();  // the epilogue may reuse the LDS
@@ -558,7 +743,7 @@ inline int make_problem(Problem& pb, int M, int N, int nseg, const Segment* segs
   pb.nseg = w;
   pb.tiles_m = (M + C::BM - 1) / C::BM;
   pb.tiles_n = (N + C::BN - 1) / C::BN;
-  pb.group_m = group_m > 0 ? min(group_m, pb.tiles_m) : pb.tiles_m;
+  pb.group_m = min(group_m > 0 ? group_m : ML_GEMM_GROUP_M, pb.tiles_m);
   pb.ksplit = 1;
   pb.kps = 0;
   if (ksplit > 1 && pb.nseg == 1) {
