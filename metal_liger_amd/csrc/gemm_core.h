@@ -513,7 +513,8 @@ __device__ __forceinline__ int acc_row(int v, int lane) {
 
 // Main loop: accumulates work item (tm, tn, split) into acc.
 template <class C, int LA, int LB>
-__device__ __forceinline__ void mainloop(const Problem& pb, int tm, int tn, int split, char* smem,
+__device__ __forceinline__ void mainloop(const Problem& pb, int tm, int tn, int split,
+                                         char* stage0, char* stage1,
                                          f32x16_t (&acc)[C::TM][C::TN]) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -549,8 +550,8 @@ __device__ __forceinline__ void mainloop(const Problem& pb, int tm, int tn, int 
   setup_tile<LB, C::BN>(ib, pb.seg[0].b, n0, pb.N, tid);
   load_tile<LA, C::BM>(ra, ia, k0, klen, tid);
   load_tile<LB, C::BN>(rb, ib, k0, klen, tid);
-  store_tile<LA, C::BM>(ra, smem, tid, k0, klen);
-  store_tile<LB, C::BN>(rb, smem + C::A_BYTES, tid, k0, klen);
+  store_tile<LA, C::BM>(ra, stage0, tid, k0, klen);
+  store_tile<LB, C::BN>(rb, stage0 + C::A_BYTES, tid, k0, klen);
   __syncthreads();
 
   // Pipeline: while k-tile kt is multiplied from LDS stage kt % 2, the
@@ -573,30 +574,271 @@ __device__ __forceinline__ void mainloop(const Problem& pb, int tm, int tn, int 
   }
   int kt = 0;
   for (; kt + 2 < nk; ++kt) {
-    const int cur = kt & 1;
+    char* st = (kt & 1) ? stage1 : stage0;
+    char* nx = (kt & 1) ? stage0 : stage1;
     const int k0s = k0, klens = klen;  // the tile in registers
     advance();                         // the tile to load
     zero_tail<LA, C::BM>(ra, k0s, klens, tid);
     zero_tail<LB, C::BN>(rb, k0s, klens, tid);
-    char* st = smem + cur * C::STAGE_BYTES;
-    mma_tile_pipelined<C, LA, LB, true>(acc, st, st + C::A_BYTES, wm, wn, lane, ra, rb,
-                                        smem + (cur ^ 1) * C::STAGE_BYTES, ia, ib, k0, klen, tid);
+    mma_tile_pipelined<C, LA, LB, true>(acc, st, st + C::A_BYTES, wm, wn, lane, ra, rb, nx, ia, ib,
+                                        k0, klen, tid);
     __syncthreads();
   }
   if (kt + 1 < nk) {
-    const int cur = kt & 1;
+    char* st = (kt & 1) ? stage1 : stage0;
+    char* nx = (kt & 1) ? stage0 : stage1;
     zero_tail<LA, C::BM>(ra, k0, klen, tid);
     zero_tail<LB, C::BN>(rb, k0, klen, tid);
-    char* st = smem + cur * C::STAGE_BYTES;
-    mma_tile_pipelined<C, LA, LB, false>(acc, st, st + C::A_BYTES, wm, wn, lane, ra, rb,
-                                         smem + (cur ^ 1) * C::STAGE_BYTES, ia, ib, k0, klen, tid);
+    mma_tile_pipelined<C, LA, LB, false>(acc, st, st + C::A_BYTES, wm, wn, lane, ra, rb, nx, ia,
+                                         ib, k0, klen, tid);
     __syncthreads();
     ++kt;
   }
-  const int last = kt & 1;
-  mma_tile<C>(acc, smem + last * C::STAGE_BYTES, smem + last * C::STAGE_BYTES + C::A_BYTES, wm, wn,
-              lane);
+  char* st = (kt & 1) ? stage1 : stage0;
+  mma_tile<C>(acc, st, st + C::A_BYTES, wm, wn, lane);
   __syncthreads();  // the epilogue may reuse the LDS
+}
+
+// ---------------------------------------------- direct-to-LDS main loop --
+// For the 256 x 256 tile with a K-major A operand. The LDS-staged loop is
+// bound by LDS traffic (stores through VGPRs plus fragment reads); here the
+// K-major operands go from global memory straight into LDS with
+// global_load_lds_dwordx4, which writes lane l's 16 bytes at LDS offset
+// 16 l of the instruction's base. One instruction fills an 8-row group
+// (1 KB) of the [rows][64 k] tile: lane l lands on row l / 8, physical
+// chunk l % 8, so it fetches logical chunk (l % 8) ^ swz(row) - the swizzle
+// is applied on the global side. Wave w fills groups w + 4 i. An MN-major B
+// keeps the register path (transposed on its way into LDS). The two LDS
+// stages are distinct __shared__ arrays and the loop is unrolled by two, so
+// the compiler sees that reads of one stage do not alias the loads into the
+// other and does not wait for them.
+// The lane id through an opaque move: values derived from it inside a rarely
+// taken branch (segment switch, partial tile) are computed there instead of
+// being hoisted out of the main loop and held in registers across it.
+__device__ __forceinline__ int opaque_lane() {
+  int l = threadIdx.x;
+  asm volatile("v_mov_b32 %0, %1" : "=v"(l) : "v"(l));
+  return l & 63;
+}
+
+template <int ROWS>
+struct DtlIter {
+  const char* base;            // uniform: tile origin at k = 0 of the segment
+  uint32_t off[ROWS / 32];     // group i: byte offset of this lane's row and chunk
+};
+
+template <int ROWS>
+__device__ __forceinline__ void setup_dtl(DtlIter<ROWS>& it, const Operand& op, int row0, int rows,
+                                          int wave) {
+  const int lane = opaque_lane();
+  it.base = reinterpret_cast<const char*>(op.ptr + (int64_t)row0 * op.ld);
+  const int last = rows - 1 - row0;
+#pragma unroll
+  for (int i = 0; i < ROWS / 32; ++i) {
+    const int r = 8 * (wave + 4 * i) + (lane >> 3);
+    const int c = (lane & 7) ^ swz(r);
+    const int rc = r < last ? r : last;
+    it.off[i] = (uint32_t)(((int64_t)rc * op.ld + 8 * c) * 2);
+  }
+}
+
+// Loads the k-tile at k0 (< klen) into the LDS tile `lds`. In a segment's
+// last, partial tile the lanes whose chunk lies past klen load the tile
+// origin instead (in bounds); dtl_zero_tail overwrites those chunks.
+template <int ROWS>
+__device__ __forceinline__ void dtl_load(const DtlIter<ROWS>& it, char* lds, int k0, int klen,
+                                         int wave) {
+  const char* b = it.base + (int64_t)k0 * 2;
+  if (k0 + kBK <= klen) {
+#pragma unroll
+    for (int i = 0; i < ROWS / 32; ++i) {
+      auto* dst = (__attribute__((address_space(3))) void*)(lds + (wave + 4 * i) * 1024);
+      const void* src = b + it.off[i];  // (a named pointer: the host pass rejects the inline form)
+      __builtin_amdgcn_global_load_lds(src, dst, 16, 0, 0);
+    }
+  } else {
+    const int l = opaque_lane();
+#pragma unroll
+    for (int i = 0; i < ROWS / 32; ++i) {
+      auto* dst = (__attribute__((address_space(3))) void*)(lds + (wave + 4 * i) * 1024);
+      const int r = 8 * (wave + 4 * i) + (l >> 3);
+      const uint32_t off = k0 + 8 * ((l & 7) ^ swz(r)) < klen ? it.off[i] : 0u;
+      const void* src = b + off;
+      __builtin_amdgcn_global_load_lds(src, dst, 16, 0, 0);
+    }
+  }
+}
+
+// For a partial k-tile: waits for this wave's direct loads, then zeroes the
+// chunks its lanes loaded past klen (each lane owns the 16 bytes its load
+// wrote). Call before the barrier that publishes the tile.
+template <int ROWS>
+__device__ __forceinline__ void dtl_zero_tail(char* lds, int k0, int klen, int wave) {
+  if (k0 + kBK <= klen) return;
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+  const int l = opaque_lane();
+#pragma unroll
+  for (int i = 0; i < ROWS / 32; ++i) {
+    const int r = 8 * (wave + 4 * i) + (l >> 3);
+    if (k0 + 8 * ((l & 7) ^ swz(r)) >= klen)
+      *reinterpret_cast<u32x4*>(lds + (wave + 4 * i) * 1024 + 16 * l) = u32x4{0u, 0u, 0u, 0u};
+  }
+}
+
+// One k-step: fragment reads of step S + 1, MFMAs of step S and, for a
+// register-staged B, part S of its LDS store (SB) and reload (RB).
+template <class C, int LB, bool SB, bool RB, int S>
+__device__ __forceinline__ void dtl_step(f32x16_t (&acc)[C::TM][C::TN], Frags<C>& fnext,
+                                         const Frags<C>& fcur, const char* As, const char* Bs,
+                                         int wm, int wn, int lane, TileRegs& rb, char* nxtB,
+                                         const char* bB, const TileIter& ib, int k0B, int klenB,
+                                         int tid) {
+  constexpr int kReads = S < 3 ? C::TM + C::TN : 0;
+  constexpr int kWb = SB ? store_count<LB, C::BN>(S) : 0;
+  constexpr int kLb = RB ? reload_count<LB, C::BN>(S) : 0;
+  constexpr int kB0 = LB == kMNMajor ? kWb : 0;
+  constexpr int kMfma = C::TM * C::TN;
+  constexpr int kMax1 = kReads > kWb ? kReads : kWb;
+  constexpr int kMax2 = kMax1 > kB0 + kLb ? kMax1 : kB0 + kLb;
+  constexpr int kSlots = kMfma > kMax2 ? kMfma : kMax2;
+  static_for<kSlots>([&](auto qc) {
+    constexpr int q = decltype(qc)::value;
+    if constexpr (q < kReads) read_frag<C, q>(fnext, As, Bs, wm, wn, lane, S + 1);
+    if constexpr (q < kWb) store_one<LB, C::BN, S, q>(rb, nxtB, tid);
+    if constexpr (q >= kB0 && q < kB0 + kLb)
+      reload_one<LB, C::BN, S, q - kB0>(rb, bB, ib, k0B, klenB, tid);
+    if constexpr (q < kMfma) {
+      constexpr int i = q / C::TN, j = q % C::TN;
+      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fcur.a[i], fcur.b[j], acc[i][j], 0, 0, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  });
+}
+
+template <class C, int LB, bool SB, bool RB>
+__device__ __forceinline__ void dtl_tile(f32x16_t (&acc)[C::TM][C::TN], const char* st, int wm,
+                                         int wn, int lane, TileRegs& rb, char* nxtB,
+                                         const TileIter& ib, int k0B, int klenB, int tid) {
+  const char* As = st;
+  const char* Bs = st + C::A_BYTES;
+  Frags<C> f0, f1;
+  load_frags<C>(f0, As, Bs, wm, wn, lane, 0);
+  __builtin_amdgcn_sched_barrier(0);
+  const char* bB = ib.base + (int64_t)k0B * ib.kstride;
+  dtl_step<C, LB, SB, RB, 0>(acc, f1, f0, As, Bs, wm, wn, lane, rb, nxtB, bB, ib, k0B, klenB, tid);
+  dtl_step<C, LB, SB, RB, 1>(acc, f0, f1, As, Bs, wm, wn, lane, rb, nxtB, bB, ib, k0B, klenB, tid);
+  dtl_step<C, LB, SB, RB, 2>(acc, f1, f0, As, Bs, wm, wn, lane, rb, nxtB, bB, ib, k0B, klenB, tid);
+  dtl_step<C, LB, SB, RB, 3>(acc, f0, f1, As, Bs, wm, wn, lane, rb, nxtB, bB, ib, k0B, klenB, tid);
+}
+
+template <class C, int LB>
+__device__ __forceinline__ void mainloop_dtl(const Problem& pb, int tm, int tn, int split,
+                                             char* stage0, char* stage1,
+                                             f32x16_t (&acc)[C::TM][C::TN]) {
+  static_assert(C::BM == 256 && C::BN == 256, "direct-to-LDS path: 256 x 256 tiles");
+  constexpr bool kBDtl = LB == kKMajor;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = (wave / C::WAVES_N) * C::WM;
+  const int wn = (wave % C::WAVES_N) * C::WN;
+  const int m0 = tm * C::BM;
+  const int n0 = tn * C::BN;
+#pragma unroll
+  for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+    for (int j = 0; j < C::TN; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+
+  int nk, k0 = 0;
+  if (pb.ksplit > 1) {
+    const int total = (pb.seg[0].k_len + kBK - 1) / kBK;
+    const int first = split * pb.kps;
+    nk = total - first < pb.kps ? total - first : pb.kps;
+    k0 = first * kBK;
+  } else {
+    nk = 0;
+    for (int s = 0; s < pb.nseg; ++s) nk += (pb.seg[s].k_len + kBK - 1) / kBK;
+  }
+  if (nk <= 0) return;
+
+  // Cursors over the K segments: the direct loads run one k-tile ahead of
+  // the tile being multiplied, a register-staged B two.
+  int segA = 0, k0A = k0, klenA = pb.seg[0].k_len;
+  int segB = 0, k0B = k0, klenB = pb.seg[0].k_len;
+  DtlIter<C::BM> ita;
+  DtlIter<C::BN> itb;
+  TileIter ib;
+  TileRegs rb;
+  setup_dtl<C::BM>(ita, pb.seg[0].a, m0, pb.M, wave);
+  if constexpr (kBDtl) setup_dtl<C::BN>(itb, pb.seg[0].b, n0, pb.N, wave);
+  else setup_tile<LB, C::BN>(ib, pb.seg[0].b, n0, pb.N, tid);
+
+  auto advanceA = [&]() __attribute__((always_inline)) {
+    k0A += kBK;
+    if (k0A >= klenA) {
+      ++segA;
+      k0A = 0;
+      klenA = pb.seg[segA].k_len;
+      setup_dtl<C::BM>(ita, pb.seg[segA].a, m0, pb.M, wave);
+      if constexpr (kBDtl) setup_dtl<C::BN>(itb, pb.seg[segA].b, n0, pb.N, wave);
+    }
+  };
+  auto advanceB = [&]() __attribute__((always_inline)) {  // register-staged B only
+    k0B += kBK;
+    if (k0B >= klenB) {
+      ++segB;
+      k0B = 0;
+      klenB = pb.seg[segB].k_len;
+      setup_tile<LB, C::BN>(ib, pb.seg[segB].b, n0, pb.N, tid);
+    }
+  };
+
+  // k-tile 0 -> stage 0; a register-staged B also takes k-tile 1 into registers
+  dtl_load<C::BM>(ita, stage0, k0A, klenA, wave);
+  if constexpr (kBDtl) dtl_load<C::BN>(itb, stage0 + C::A_BYTES, k0A, klenA, wave);
+  dtl_zero_tail<C::BM>(stage0, k0A, klenA, wave);
+  if constexpr (kBDtl) {
+    dtl_zero_tail<C::BN>(stage0 + C::A_BYTES, k0A, klenA, wave);
+  } else {
+    load_tile<LB, C::BN>(rb, ib, k0B, klenB, tid);
+    store_tile<LB, C::BN>(rb, stage0 + C::A_BYTES, tid, k0B, klenB);
+    if (nk > 1) {
+      advanceB();
+      load_tile<LB, C::BN>(rb, ib, k0B, klenB, tid);
+    }
+  }
+  __syncthreads();
+
+  // k-tile t: loads of k-tile t + 1 into stage nx, multiply from stage st.
+  // One code path for every t (no branch around the MFMAs, whose 256
+  // accumulators would otherwise be merged and copied): past the last
+  // k-tile the cursors stay put and the same tile is loaded again into the
+  // stage that is no longer read.
+  auto iteration = [&](int t, char* st, char* nx) __attribute__((always_inline)) {
+    if (t + 1 < nk) advanceA();
+    dtl_load<C::BM>(ita, nx, k0A, klenA, wave);
+    if constexpr (kBDtl) dtl_load<C::BN>(itb, nx + C::A_BYTES, k0A, klenA, wave);
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (kBDtl) {
+      dtl_tile<C, LB, false, false>(acc, st, wm, wn, lane, rb, nullptr, ib, 0, 0, tid);
+    } else {
+      const int k0s = k0B, klens = klenB;  // B in registers (k-tile t + 1)
+      if (t + 2 < nk) advanceB();          // B to load (k-tile t + 2)
+      zero_tail<LB, C::BN>(rb, k0s, klens, tid);
+      dtl_tile<C, LB, true, true>(acc, st, wm, wn, lane, rb, nx + C::A_BYTES, ib, k0B, klenB, tid);
+    }
+    dtl_zero_tail<C::BM>(nx, k0A, klenA, wave);
+    if constexpr (kBDtl) dtl_zero_tail<C::BN>(nx + C::A_BYTES, k0A, klenA, wave);
+    __syncthreads();
+  };
+  int t = 0;
+  for (; t + 1 < nk; t += 2) {
+    iteration(t, stage0, stage1);
+    iteration(t + 1, stage1, stage0);
+  }
+  if (t < nk) iteration(t, stage0, stage1);
 }
 
 // The GEMM kernel: mainloop + epilogue functor
@@ -604,11 +846,16 @@ __device__ __forceinline__ void mainloop(const Problem& pb, int tm, int tn, int 
 //   origin of this wave's sub-tile. smem may be reused by the epilogue.
 template <class C, int LA, int LB, class Epi>
 __global__ __launch_bounds__(kThreads) void gemm_kernel(const Problem pb, const Epi epi) {
-  __shared__ __attribute__((aligned(16))) char smem[C::LDS_BYTES];
+  __shared__ __attribute__((aligned(16))) char stage0[C::STAGE_BYTES];
+  __shared__ __attribute__((aligned(16))) char stage1[C::STAGE_BYTES];
+  char* smem = stage0;
   int tm, tn, split;
   if (!tile_coords(pb, tm, tn, split)) return;
   f32x16_t acc[C::TM][C::TN];
-  mainloop<C, LA, LB>(pb, tm, tn, split, smem, acc);
+  if constexpr (LA == kKMajor && C::BM == 256 && C::BN == 256)
+    mainloop_dtl<C, LB>(pb, tm, tn, split, stage0, stage1, acc);
+  else
+    mainloop<C, LA, LB>(pb, tm, tn, split, stage0, stage1, acc);
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   epi(acc, tm * C::BM + (wave / C::WAVES_N) * C::WM, tn * C::BN + (wave % C::WAVES_N) * C::WN,
