@@ -28,18 +28,20 @@ namespace {
 using namespace gemm;
 
 constexpr float kLog2e = 1.4426950408889634f;
-constexpr int kColBlock = kWN;  // columns per (max, sum) partial
+constexpr int kColBlock = big::WN;  // columns per (max, sum) partial: one wave's sub-tile
 
 __device__ __forceinline__ float exp_f(float x) { return __builtin_amdgcn_exp2f(x * kLog2e); }
 
-__device__ __forceinline__ float half_max(float v) {
+// Reductions over the 16 lanes of a group (the lanes that hold one row of a
+// 16 x 16 accumulator tile).
+__device__ __forceinline__ float grp16_max(float v) {
 #pragma unroll
-  for (int off = 16; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 32));
+  for (int off = 8; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 16));
   return v;
 }
-__device__ __forceinline__ float half_sum(float v) {
+__device__ __forceinline__ float grp16_sum(float v) {
 #pragma unroll
-  for (int off = 16; off > 0; off >>= 1) v += __shfl_xor(v, off, 32);
+  for (int off = 8; off > 0; off >>= 1) v += __shfl_xor(v, off, 16);
   return v;
 }
 
@@ -49,6 +51,8 @@ __device__ __forceinline__ float bias_at(const TB* b, int64_t n) {
 }
 
 // ------------------------------------------------------------ forward epi --
+// Each wave reduces its 128 logit columns to a (max, sum exp(z - max))
+// partial per row; the lane holding (row, label) writes the label logit.
 template <typename TB>
 struct EpiLse {
   const TB* bias;
@@ -58,47 +62,47 @@ struct EpiLse {
   float* zy;    // [M]
   int M, V, nblk;
 
-  __device__ __forceinline__ void operator()(f32x16_t (&acc)[kTM][kTN], int m0, int n0, int lane,
-                                             char*, int) const {
+  __device__ __forceinline__ void operator()(f32x4_t (&acc)[big::TM][big::TN], int m0, int n0,
+                                             int lane, char*, int) const {
     // a wave whose 128 columns all lie past the vocabulary (second half of
     // the last tile) owns no partial slot
     if (n0 >= V) return;
-    const int col = lane & 31;
-    float bj[kTN];
-    bool okj[kTN];
+    const int c = lane & 15;
+    float bj[big::TN];
+    bool okj[big::TN];
 #pragma unroll
-    for (int j = 0; j < kTN; ++j) {
-      const int n = n0 + 32 * j + col;
+    for (int j = 0; j < big::TN; ++j) {
+      const int n = n0 + 16 * j + c;
       okj[j] = n < V;
       bj[j] = okj[j] ? bias_at(bias, n) : 0.f;
     }
     const int nb = n0 / kColBlock;
 #pragma unroll
-    for (int i = 0; i < kTM; ++i) {
+    for (int i = 0; i < big::TM; ++i) {
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int m = m0 + 32 * i + acc_row(v, lane);
-        float z[kTN];
+      for (int v = 0; v < 4; ++v) {
+        const int m = m0 + 16 * i + 4 * (lane >> 4) + v;
+        float z[big::TN];
         float mx = -INFINITY;
 #pragma unroll
-        for (int j = 0; j < kTN; ++j) {
+        for (int j = 0; j < big::TN; ++j) {
           z[j] = okj[j] ? acc[i][j][v] + bj[j] : -INFINITY;
           mx = fmaxf(mx, z[j]);
         }
         if (m < M) {
           const int64_t lab = labels[m];
 #pragma unroll
-          for (int j = 0; j < kTN; ++j)
-            if (okj[j] && lab == (int64_t)(n0 + 32 * j + col)) zy[m] = z[j];
+          for (int j = 0; j < big::TN; ++j)
+            if (okj[j] && lab == (int64_t)(n0 + 16 * j + c)) zy[m] = z[j];
         }
-        mx = half_max(mx);
+        mx = grp16_max(mx);
         float s = 0.f;
         if (mx != -INFINITY) {
 #pragma unroll
-          for (int j = 0; j < kTN; ++j) s += exp_f(z[j] - mx);
+          for (int j = 0; j < big::TN; ++j) s += exp_f(z[j] - mx);
         }
-        s = half_sum(s);
-        if (col == 0 && m < M) {
+        s = grp16_sum(s);
+        if (c == 0 && m < M) {
           pmax[(int64_t)m * nblk + nb] = mx;
           psum[(int64_t)m * nblk + nb] = s;
         }
@@ -168,6 +172,7 @@ __global__ __launch_bounds__(1024) void loss_mean_kernel(const float* __restrict
 }
 
 // ----------------------------------------------------------- backward epi --
+// d = (exp(z - lse) - [col == label]) * mask * (grad / n_valid), to bf16.
 template <typename TB>
 struct EpiDlogit {
   const TB* bias;  // chunk-relative (bias + c0) or null
@@ -181,35 +186,35 @@ struct EpiDlogit {
   int M, C;
   int64_t c0;
 
-  __device__ __forceinline__ void operator()(f32x16_t (&acc)[kTM][kTN], int m0, int n0, int lane,
-                                             char*, int) const {
-    const int col = lane & 31;
+  __device__ __forceinline__ void operator()(f32x4_t (&acc)[big::TM][big::TN], int m0, int n0,
+                                             int lane, char*, int) const {
+    const int c = lane & 15;
     const float scale = grad[0] / fmaxf(n_valid[0], 1.0f);
-    float bj[kTN];
-    bool okj[kTN];
+    float bj[big::TN];
+    bool okj[big::TN];
 #pragma unroll
-    for (int j = 0; j < kTN; ++j) {
-      const int n = n0 + 32 * j + col;
+    for (int j = 0; j < big::TN; ++j) {
+      const int n = n0 + 16 * j + c;
       okj[j] = n < C;
       bj[j] = okj[j] ? bias_at(bias, n) : 0.f;
     }
 #pragma unroll
-    for (int i = 0; i < kTM; ++i) {
+    for (int i = 0; i < big::TM; ++i) {
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int m = m0 + 32 * i + acc_row(v, lane);
+      for (int v = 0; v < 4; ++v) {
+        const int m = m0 + 16 * i + 4 * (lane >> 4) + v;
         if (m >= M) continue;
         const int64_t lab = labels[m];
-        const bool valid = lab != ignore;
+        const float sc = lab != ignore ? scale : 0.f;
         const float L = lse[m];
         bf16* drow = D + (int64_t)m * ldd;
 #pragma unroll
-        for (int j = 0; j < kTN; ++j) {
+        for (int j = 0; j < big::TN; ++j) {
           if (!okj[j]) continue;
-          const int n = n0 + 32 * j + col;
+          const int n = n0 + 16 * j + c;
           float p = exp_f((acc[i][j][v] + bj[j]) - L);
           if (c0 + n == lab) p -= 1.0f;
-          drow[n] = from_f32<bf16>(valid ? p * scale : 0.f);
+          drow[n] = from_f32<bf16>(p * sc);
         }
       }
     }

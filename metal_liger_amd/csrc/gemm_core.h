@@ -1,34 +1,33 @@
 // bf16 MFMA GEMM core for gfx950 (CDNA4): C[M,N] = sum_k A[m,k] * B[k,n],
-// fp32 accumulation, pluggable epilogue.
+// fp32 accumulation, pluggable epilogue. Two engines share the problem
+// description, the tile order and the epilogues:
 //
-// Tiling (compile-time tile shape Cfg<BM, BN, WAVES_M>)
+// 256 x 256 tiles (every large product: FLCE logits / dH / dW, LoRA dX, the
+//   plain GEMM entry points) - see "256 x 256" below: v_mfma_f32_16x16x32_bf16,
+//   k-tiles of 32, four LDS stages filled by buffer_load ... lds straight
+//   from global memory in both operand layouts, transposing LDS reads
+//   (ds_read_b64_tr_b16) for MN-major operands.
+// Narrow tiles Cfg<BM, BN, WAVES_M> (256 x 32, 64 x 256: the rank-r LoRA
+//   products, which would waste most of a 256 x 256 tile on padding):
 //   256 threads = 4 wave64s in a WAVES_M x (4 / WAVES_M) grid; a wave owns a
-//   (BM / WAVES_M) x (BN / WAVES_N) sub-tile made of 32 x 32 tiles of
-//   v_mfma_f32_32x32x16_bf16 (accumulators in AGPRs). BK = 64.
-//   The big-GEMM shape is 256 x 256 (2 x 2 waves of 128 x 128); narrow shapes
-//   (256 x 32, 64 x 256) serve the rank-r LoRA products without wasting MFMA
-//   work on padding.
+//   (BM / WAVES_M) x (BN / WAVES_N) sub-tile of 32 x 32 tiles of
+//   v_mfma_f32_32x32x16_bf16. BK = 64; both operand layouts are staged
+//   through registers into LDS as [rows][64 k] bf16 (128-byte rows, 16-byte
+//   chunks XOR-swizzled for conflict-free ds_read_b128 fragment reads);
+//   MN-major tiles are transposed in registers (8 x 8 bf16 blocks,
+//   v_perm_b32) on their way in. Two LDS stages, one barrier per k-tile.
 // Operand layouts (per operand, "rows" = M for A, N for B)
 //   K-major : element (r, k) at p[r * ld + k]   (A row-major, F.linear weight)
 //   MN-major: element (r, k) at p[k * ld + r]   (A^T stored, B row-major)
-//   Both are staged into LDS as [rows][64 k] bf16, 128 bytes per row, with
-//   the 16-byte chunks of a row XOR-swizzled so that ds_read_b128 fragment
-//   reads (32 consecutive rows, same k chunk) and the stores are free of
-//   bank conflicts for both 8- and 16-lane bank groups. MN-major tiles are
-//   transposed in registers (8 x 8 bf16 blocks, v_perm_b32) on their way
-//   into LDS, so the MFMA inner loop is the same for every layout.
-// Pipeline
-//   two LDS stages: the global loads of k-tile t+1 are in flight while the
-//   MFMAs of k-tile t run; one barrier per k-tile. Global addresses are a
-//   uniform tile base (scalar registers) plus 32-bit per-thread offsets.
 // K segments
 //   K may be a concatenation of up to kMaxSeg segments with their own A/B
 //   pointers and leading dimensions (e.g. [dQ | dK | dV | lora] against
 //   [Wq; Wk; Wv; A]); a segment's last k-tile is zero-filled past its end.
 // Split-K
-//   with ksplit > 1 (single segment), split s accumulates k-tiles
-//   [s * kps, (s + 1) * kps) and the epilogue receives s; EpiPartial writes
-//   fp32 partial tiles that reduce_partials_kernel sums in fixed order.
+//   with ksplit > 1 (single segment), split s accumulates the 64-wide
+//   k-tiles [s * kps, (s + 1) * kps) and the epilogue receives s;
+//   EpiPartial writes fp32 partial tiles that reduce_partials_kernel sums in
+//   a fixed order.
 // Tile order
 //   workgroups are dispatched round-robin over the 8 XCDs, so block b is
 //   remapped to logical work item (b % 8) * ceil(W/8) + b / 8: each XCD walks
@@ -78,10 +77,6 @@ using BigCfg = Cfg<256, 256, 2>;   // 2 x 2 waves of 128 x 128
 using TallCfg = Cfg<256, 32, 4>;   // 4 x 1 waves of 64 x 32  (rank-r wide outputs)
 using WideCfg = Cfg<64, 256, 1>;   // 1 x 4 waves of 64 x 64  (few-row outputs)
 
-// Names for the big tile
-constexpr int kBM = BigCfg::BM, kBN = BigCfg::BN;
-constexpr int kWM = BigCfg::WM, kWN = BigCfg::WN;
-constexpr int kTM = BigCfg::TM, kTN = BigCfg::TN;
 
 enum : int { kKMajor = 0, kMNMajor = 1 };
 
@@ -272,8 +267,6 @@ constexpr int reload_count(int part) {
 // Scheduling-group masks of __builtin_amdgcn_sched_group_barrier.
 constexpr int kSchedMfma = 0x008;
 constexpr int kSchedDsRead = 0x100;
-constexpr int kSchedDsWrite = 0x200;
-constexpr int kSchedVmemRead = 0x020;
 
 // Fragments of one 16-wide k-step for a wave: TM A fragments, TN B fragments.
 template <class C>
@@ -505,11 +498,6 @@ inline int grid_blocks(const Problem& pb) {
   return ((W + kXcds - 1) / kXcds) * kXcds;
 }
 
-// Geometry of one lane's accumulators: element v of MFMA tile (i, j) sits at
-// row m0 + 32 i + acc_row(v, lane), column n0 + 32 j + (lane & 31).
-__device__ __forceinline__ int acc_row(int v, int lane) {
-  return 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
-}
 
 // Main loop: accumulates work item (tm, tn, split) into acc.
 template <class C, int LA, int LB>
@@ -599,272 +587,439 @@ __device__ __forceinline__ void mainloop(const Problem& pb, int tm, int tn, int 
   __syncthreads();  // the epilogue may reuse the LDS
 }
 
-// ---------------------------------------------- direct-to-LDS main loop --
-// For the 256 x 256 tile with a K-major A operand. The LDS-staged loop is
-// bound by LDS traffic (stores through VGPRs plus fragment reads); here the
-// K-major operands go from global memory straight into LDS with
-// global_load_lds_dwordx4, which writes lane l's 16 bytes at LDS offset
-// 16 l of the instruction's base. One instruction fills an 8-row group
-// (1 KB) of the [rows][64 k] tile: lane l lands on row l / 8, physical
-// chunk l % 8, so it fetches logical chunk (l % 8) ^ swz(row) - the swizzle
-// is applied on the global side. Wave w fills groups w + 4 i. An MN-major B
-// keeps the register path (transposed on its way into LDS). The two LDS
-// stages are distinct __shared__ arrays and the loop is unrolled by two, so
-// the compiler sees that reads of one stage do not alias the loads into the
-// other and does not wait for them.
 // The lane id through an opaque move: values derived from it inside a rarely
-// taken branch (segment switch, partial tile) are computed there instead of
-// being hoisted out of the main loop and held in registers across it.
+// taken branch (a K-segment switch) are computed there instead of being
+// hoisted out of the main loop and held in registers across it.
 __device__ __forceinline__ int opaque_lane() {
   int l = threadIdx.x;
   asm volatile("v_mov_b32 %0, %1" : "=v"(l) : "v"(l));
   return l & 63;
 }
 
-template <int ROWS>
-struct DtlIter {
-  const char* base;            // uniform: tile origin at k = 0 of the segment
-  uint32_t off[ROWS / 32];     // group i: byte offset of this lane's row and chunk
+// ============================================================ 256 x 256 ==
+// The big tile runs its own engine:
+//   v_mfma_f32_16x16x32_bf16 (on gfx950 it sustains a larger share of the
+//   matrix-core peak than the 32x32x16 form), a wave tile of 128 x 128 =
+//   8 x 8 MFMA tiles (256 fp32 accumulators, AGPRs), k-tiles of 32, and four
+//   LDS stages of 32 KB, so that loads run three k-tiles ahead of their use.
+// Both operands, in either layout, go global -> LDS with
+// buffer_load_dwordx4 ... lds (lane l's 16 bytes land at LDS offset 16 l of
+// the instruction's base; one instruction fills 1 KB), unconverted:
+//   K-major tile  [256 rows][32 k]   64-byte rows; the 16-byte chunk c of
+//                                    row r sits at chunk c ^ kswz(r),
+//                                    kswz(r) = ((r >> 1) ^ (r >> 2)) & 3
+//   MN-major tile [32 k][256 rows]   512-byte k-rows; the 32-byte unit u of
+//                                    k-row r sits at unit u ^ h(r),
+//                                    h(r) = (r & 3) | ((r >> 3) & 1) << 2
+// (the swizzles are applied on the global side: each lane fetches the data
+// its LDS slot holds). Fragments are read with ds_read_b128 (K-major) or
+// with two ds_read_b64_tr_b16 (MN-major). The transposing read returns, per
+// 16-lane group, lane i element j = element (i mod 4) of the 8 bytes
+// addressed by lane 4 j + i / 4; with lane 4 a + b addressing rows 4 b ..
+// 4 b + 3 of k-row a, lane i receives row i at 4 consecutive k, which is the
+// MFMA operand layout. Both swizzles keep every 8-lane group of a fragment
+// read within distinct 16-byte bank groups of a 128-byte window (and every
+// 16-lane group within a 256-byte one): the reads are free of bank conflicts.
+// A lane whose k lies past the end of its K segment loads from an offset past
+// the buffer resource's range; the hardware writes zeros for it.
+// Pipeline, per k-tile t (stage t % 4):
+//   wait for this wave's loads of k-tile t + 1, barrier (publishes t + 1;
+//   every wave has its fragments of t in registers, so stage t % 4 is free);
+//   the 64 MFMAs of k-tile t, with the fragment reads of k-tile t + 1 in the
+//   first 32 slots and the 8 loads of k-tile t + 4 into stage t % 4 in the
+//   last 32.
+
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef short i16x4_t __attribute__((ext_vector_type(4)));
+
+namespace big {
+constexpr int BK = 32;
+constexpr int TM = 8, TN = 8;  // 16 x 16 MFMA tiles per wave
+constexpr int WM = 128, WN = 128;
+constexpr int OP_BYTES = 256 * BK * 2;  // 16 KB per operand per stage
+constexpr int STAGE_BYTES = 2 * OP_BYTES;
+constexpr int STAGES = 4;
+constexpr int LOADS = 4;  // 1-KB loads per wave per operand per k-tile
+// vmcnt immediates (gfx9 encoding): 3 k-tiles (24 loads per wave) in flight
+// after the prologue, 2 k-tiles (16) in the loop.
+constexpr int kWaitVm24 = 0x4F78;
+constexpr int kWaitVm16 = 0x4F70;
+constexpr int kWaitVm0 = 0x0F70;
+constexpr uint32_t kOob = 0x80000000u;  // past every resource range used here
+constexpr uint32_t kRange = 0x7FFFFFFFu;
+constexpr uint32_t kDword3 = 0x00020000u;  // raw buffer, 32-bit data format
+}  // namespace big
+
+// Raw buffer resource (4 uniform dwords): base, stride 0, range, format.
+typedef unsigned int rsrc_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ rsrc_t make_rsrc(const char* base) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  rsrc_t r;
+  r[0] = __builtin_amdgcn_readfirstlane((uint32_t)a);
+  r[1] = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32) & 0xFFFFu);
+  r[2] = big::kRange;
+  r[3] = big::kDword3;
+  return r;
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const char* p) {
+  return (uint32_t)reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) char*)p);
+}
+
+// buffer_load_dwordx4 ... lds. Issued as inline assembly so that the
+// compiler inserts no waits of its own for it: the main loop keeps its own
+// vmcnt accounting (s_waitcnt with explicit counts before each barrier) and
+// has no other vector-memory operation in flight.
+// (m0 is a reserved register: the compiler keeps nothing in it across this
+// code - no other instruction of these kernels reads it - so its clobber is
+// declared and the warning about clobbering a reserved register is muted.)
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void buf_load_lds(rsrc_t r, uint32_t voff, char* lds) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
+               :
+               : "v"(voff), "s"(r), "s"(lds_addr(lds))
+               : "m0");
+}
+#pragma clang diagnostic pop
+
+// Chunk swizzle of the K-major tile (a function of the row's low 4 bits).
+__device__ __forceinline__ int kswz(int r) { return ((r >> 1) ^ (r >> 2)) & 3; }
+
+// Loads of one operand for one k-tile.
+template <int L>
+struct BigIter {
+  const char* base;  // uniform: operand at (first row of the tile, k = 0 of the segment)
+  int64_t kstep;     // bytes per unit of k
+  uint32_t off[big::LOADS];
+  int kr[big::LOADS];  // MN-major: the k-row of each load
 };
 
-template <int ROWS>
-__device__ __forceinline__ void setup_dtl(DtlIter<ROWS>& it, const Operand& op, int row0, int rows,
+// Wave w issues the 1-KB groups g = w + 4 i (i < 4): rows 16 g .. 16 g + 15
+// (K-major) or k-rows 2 g, 2 g + 1 (MN-major).
+template <int L>
+__device__ __forceinline__ void big_setup(BigIter<L>& it, const Operand& op, int row0, int rows,
                                           int wave) {
-  const int lane = opaque_lane();
-  it.base = reinterpret_cast<const char*>(op.ptr + (int64_t)row0 * op.ld);
-  const int last = rows - 1 - row0;
+  const int l = opaque_lane();
+  if constexpr (L == kKMajor) {
+    it.base = reinterpret_cast<const char*>(op.ptr + (int64_t)row0 * op.ld);
+    it.kstep = 2;
+    const int lc = (l & 3) ^ kswz(l >> 2);  // logical chunk of physical chunk l % 4 (row % 16 = l / 4)
+    const int last = rows - 1 - row0;
 #pragma unroll
-  for (int i = 0; i < ROWS / 32; ++i) {
-    const int r = 8 * (wave + 4 * i) + (lane >> 3);
-    const int c = (lane & 7) ^ swz(r);
-    const int rc = r < last ? r : last;
-    it.off[i] = (uint32_t)(((int64_t)rc * op.ld + 8 * c) * 2);
-  }
-}
-
-// Loads the k-tile at k0 (< klen) into the LDS tile `lds`. In a segment's
-// last, partial tile the lanes whose chunk lies past klen load the tile
-// origin instead (in bounds); dtl_zero_tail overwrites those chunks.
-template <int ROWS>
-__device__ __forceinline__ void dtl_load(const DtlIter<ROWS>& it, char* lds, int k0, int klen,
-                                         int wave) {
-  const char* b = it.base + (int64_t)k0 * 2;
-  if (k0 + kBK <= klen) {
-#pragma unroll
-    for (int i = 0; i < ROWS / 32; ++i) {
-      auto* dst = (__attribute__((address_space(3))) void*)(lds + (wave + 4 * i) * 1024);
-      const void* src = b + it.off[i];  // (a named pointer: the host pass rejects the inline form)
-      __builtin_amdgcn_global_load_lds(src, dst, 16, 0, 0);
+    for (int i = 0; i < big::LOADS; ++i) {
+      const int r = 16 * (wave + 4 * i) + (l >> 2);
+      const int rc = r < last ? r : last;  // rows past the end re-read the last row
+      it.off[i] = (uint32_t)(((int64_t)rc * op.ld + 8 * lc) * 2);
+      it.kr[i] = 0;
     }
   } else {
-    const int l = opaque_lane();
+    it.base = reinterpret_cast<const char*>(op.ptr + row0);
+    it.kstep = 2 * op.ld;
+    const int p = l & 31;  // physical 16-byte slot in the k-row
+    const int last8 = rows - row0 - 8;  // last 8-row group of the operand (rows % 8 == 0)
 #pragma unroll
-    for (int i = 0; i < ROWS / 32; ++i) {
-      auto* dst = (__attribute__((address_space(3))) void*)(lds + (wave + 4 * i) * 1024);
-      const int r = 8 * (wave + 4 * i) + (l >> 3);
-      const uint32_t off = k0 + 8 * ((l & 7) ^ swz(r)) < klen ? it.off[i] : 0u;
-      const void* src = b + off;
-      __builtin_amdgcn_global_load_lds(src, dst, 16, 0, 0);
+    for (int i = 0; i < big::LOADS; ++i) {
+      const int r = 2 * (wave + 4 * i) + (l >> 5);
+      const int h = (r & 3) | (((r >> 3) & 1) << 2);
+      int e = 8 * (2 * ((p >> 1) ^ h) + (p & 1));  // first row of the 8 this lane fetches
+      e = e < last8 ? e : last8;
+      it.off[i] = (uint32_t)(((int64_t)r * op.ld + e) * 2);
+      it.kr[i] = r;
     }
   }
 }
 
-// For a partial k-tile: waits for this wave's direct loads, then zeroes the
-// chunks its lanes loaded past klen (each lane owns the 16 bytes its load
-// wrote). Call before the barrier that publishes the tile.
-template <int ROWS>
-__device__ __forceinline__ void dtl_zero_tail(char* lds, int k0, int klen, int wave) {
-  if (k0 + kBK <= klen) return;
-  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-  const int l = opaque_lane();
+// Per-lane LDS byte offsets (within an operand tile) of the fragment reads
+// of a wave whose sub-tile starts at row wbase of the block tile.
+template <int L>
+struct FragAddr {
+  uint32_t a[L == kKMajor ? 1 : big::TM];
+};
+
+template <int L>
+__device__ __forceinline__ void frag_addr_setup(FragAddr<L>& fa, int wbase, int lane) {
+  if constexpr (L == kKMajor) {
+    // row wbase + 16 f + (lane & 15), chunk lane >> 4; the swizzle term
+    // kswz(row) only depends on row % 16 = lane & 15
+    fa.a[0] = (uint32_t)(wbase * 64 + (lane & 15) * 64 + (((lane >> 4) ^ kswz(lane & 15)) << 4));
+  } else {
+    // k-row 8 G + (i >> 2) (+ 4 for the second read), rows 4 (i & 3) .. of
+    // the fragment's 32-byte unit wbase / 16 + f, swizzled by h(k-row) =
+    // ((i >> 2) & 3) | (G & 1) << 2 (G = lane >> 4, i = lane & 15)
+    const int G = lane >> 4, i = lane & 15;
+    const int h = ((i >> 2) & 3) | ((G & 1) << 2);
+    const uint32_t b = (uint32_t)((8 * G + (i >> 2)) * 512 + 8 * (i & 3) + wbase * 2);
 #pragma unroll
-  for (int i = 0; i < ROWS / 32; ++i) {
-    const int r = 8 * (wave + 4 * i) + (l >> 3);
-    if (k0 + 8 * ((l & 7) ^ swz(r)) >= klen)
-      *reinterpret_cast<u32x4*>(lds + (wave + 4 * i) * 1024 + 16 * l) = u32x4{0u, 0u, 0u, 0u};
+    for (int f = 0; f < big::TM; ++f) fa.a[f] = b + (uint32_t)((f ^ h) << 5);
   }
 }
 
-// One k-step: fragment reads of step S + 1, MFMAs of step S and, for a
-// register-staged B, part S of its LDS store (SB) and reload (RB).
-template <class C, int LB, bool SB, bool RB, int S>
-__device__ __forceinline__ void dtl_step(f32x16_t (&acc)[C::TM][C::TN], Frags<C>& fnext,
-                                         const Frags<C>& fcur, const char* As, const char* Bs,
-                                         int wm, int wn, int lane, TileRegs& rb, char* nxtB,
-                                         const char* bB, const TileIter& ib, int k0B, int klenB,
-                                         int tid) {
-  constexpr int kReads = S < 3 ? C::TM + C::TN : 0;
-  constexpr int kWb = SB ? store_count<LB, C::BN>(S) : 0;
-  constexpr int kLb = RB ? reload_count<LB, C::BN>(S) : 0;
-  constexpr int kB0 = LB == kMNMajor ? kWb : 0;
-  constexpr int kMfma = C::TM * C::TN;
-  constexpr int kMax1 = kReads > kWb ? kReads : kWb;
-  constexpr int kMax2 = kMax1 > kB0 + kLb ? kMax1 : kB0 + kLb;
-  constexpr int kSlots = kMfma > kMax2 ? kMfma : kMax2;
-  static_for<kSlots>([&](auto qc) {
+struct BigFrags {
+  bf16x8_t a[big::TM], b[big::TN];
+};
+
+// Read q (compile time) of a k-tile's fragments: B first (the first MFMAs of
+// a k-tile use every B fragment), then A; an MN-major fragment takes two
+// transposing reads.
+template <int L>
+constexpr int reads_per_frag() { return L == kKMajor ? 1 : 2; }
+
+template <int L>
+__device__ __forceinline__ void read_big_frag(bf16x8_t& dst, const char* op, const FragAddr<L>& fa,
+                                              int f, int half) {
+  if constexpr (L == kKMajor) {
+    dst = *reinterpret_cast<const bf16x8_t*>(op + fa.a[0] + 1024 * f);
+  } else {
+    typedef __attribute__((address_space(3))) i16x4_t* lp;
+    const i16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (lp)(op + fa.a[f] + 2048 * half));
+    typedef short i16x8_t __attribute__((ext_vector_type(8)));
+    i16x8_t w = __builtin_bit_cast(i16x8_t, dst);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) w[4 * half + e] = v[e];
+    dst = __builtin_bit_cast(bf16x8_t, w);
+  }
+}
+
+template <int LA, int LB, int Q>
+__device__ __forceinline__ void big_read(BigFrags& f, const char* As, const char* Bs,
+                                         const FragAddr<LA>& fa, const FragAddr<LB>& fb) {
+  constexpr int RB = reads_per_frag<LB>(), RA = reads_per_frag<LA>();
+  if constexpr (Q < big::TN * RB) {
+    read_big_frag<LB>(f.b[Q / RB], Bs, fb, Q / RB, Q % RB);
+  } else {
+    constexpr int q = Q - big::TN * RB;
+    read_big_frag<LA>(f.a[q / RA], As, fa, q / RA, q % RA);
+  }
+}
+
+template <int L>
+__device__ __forceinline__ uint32_t big_oob(const BigIter<L>& it, int i, bool live, int kc, int kb,
+                                            int klen) {
+  const int k = kc + (L == kKMajor ? kb : it.kr[i]);
+  return (live && k < klen) ? 0u : big::kOob;
+}
+
+// One k-tile: 64 MFMAs on fc; reads of the next k-tile's fragments into fn
+// (from As_n, Bs_n) in the first slots; the 8 loads of a k-tile into
+// (ldA, ldB) in slots 32, 36, .., 60.
+template <int LA, int LB>
+__device__ __forceinline__ void big_tile(f32x4_t (&acc)[big::TM][big::TN], BigFrags& fn,
+                                         const BigFrags& fc, const char* As_n, const char* Bs_n,
+                                         const FragAddr<LA>& fa, const FragAddr<LB>& fb,
+                                         const BigIter<LA>& ia, const BigIter<LB>& ib, rsrc_t ra,
+                                         rsrc_t rb, const uint32_t (&oa)[big::LOADS],
+                                         const uint32_t (&ob)[big::LOADS], char* ldA, char* ldB,
+                                         int wave) {
+  constexpr int kReads = big::TN * reads_per_frag<LB>() + big::TM * reads_per_frag<LA>();
+  static_assert(kReads <= 32, "reads fit in the first half");
+  static_for<big::TM * big::TN>([&](auto qc) {
     constexpr int q = decltype(qc)::value;
-    if constexpr (q < kReads) read_frag<C, q>(fnext, As, Bs, wm, wn, lane, S + 1);
-    if constexpr (q < kWb) store_one<LB, C::BN, S, q>(rb, nxtB, tid);
-    if constexpr (q >= kB0 && q < kB0 + kLb)
-      reload_one<LB, C::BN, S, q - kB0>(rb, bB, ib, k0B, klenB, tid);
-    if constexpr (q < kMfma) {
-      constexpr int i = q / C::TN, j = q % C::TN;
-      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fcur.a[i], fcur.b[j], acc[i][j], 0, 0, 0);
+    if constexpr (q < kReads) big_read<LA, LB, q>(fn, As_n, Bs_n, fa, fb);
+    if constexpr (q >= 32 && (q - 32) % 4 == 0) {
+      constexpr int ld = (q - 32) / 4;  // 0..7: A loads 0..3, then B loads 0..3
+      if constexpr (ld < big::LOADS)
+        buf_load_lds(ra, ia.off[ld] | oa[ld], ldA + (wave + 4 * ld) * 1024);
+      else
+        buf_load_lds(rb, ib.off[ld - big::LOADS] | ob[ld - big::LOADS],
+                     ldB + (wave + 4 * (ld - big::LOADS)) * 1024);
     }
+    constexpr int i = q / big::TN, j = q % big::TN;
+    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fc.a[i], fc.b[j], acc[i][j], 0, 0, 0);
     __builtin_amdgcn_sched_barrier(0);
   });
 }
 
-template <class C, int LB, bool SB, bool RB>
-__device__ __forceinline__ void dtl_tile(f32x16_t (&acc)[C::TM][C::TN], const char* st, int wm,
-                                         int wn, int lane, TileRegs& rb, char* nxtB,
-                                         const TileIter& ib, int k0B, int klenB, int tid) {
-  const char* As = st;
-  const char* Bs = st + C::A_BYTES;
-  Frags<C> f0, f1;
-  load_frags<C>(f0, As, Bs, wm, wn, lane, 0);
-  __builtin_amdgcn_sched_barrier(0);
-  const char* bB = ib.base + (int64_t)k0B * ib.kstride;
-  dtl_step<C, LB, SB, RB, 0>(acc, f1, f0, As, Bs, wm, wn, lane, rb, nxtB, bB, ib, k0B, klenB, tid);
-  dtl_step<C, LB, SB, RB, 1>(acc, f0, f1, As, Bs, wm, wn, lane, rb, nxtB, bB, ib, k0B, klenB, tid);
-  dtl_step<C, LB, SB, RB, 2>(acc, f1, f0, As, Bs, wm, wn, lane, rb, nxtB, bB, ib, k0B, klenB, tid);
-  dtl_step<C, LB, SB, RB, 3>(acc, f0, f1, As, Bs, wm, wn, lane, rb, nxtB, bB, ib, k0B, klenB, tid);
-}
-
-template <class C, int LB>
-__device__ __forceinline__ void mainloop_dtl(const Problem& pb, int tm, int tn, int split,
-                                             char* stage0, char* stage1,
-                                             f32x16_t (&acc)[C::TM][C::TN]) {
-  static_assert(C::BM == 256 && C::BN == 256, "direct-to-LDS path: 256 x 256 tiles");
-  constexpr bool kBDtl = LB == kKMajor;
+// Main loop of the big tile; st[] are four distinct __shared__ arrays of
+// STAGE_BYTES (A tile, then B tile).
+template <int LA, int LB>
+__device__ __forceinline__ void big_mainloop(const Problem& pb, int tm, int tn, int split,
+                                             char* const (&st)[big::STAGES],
+                                             f32x4_t (&acc)[big::TM][big::TN]) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = (wave / C::WAVES_N) * C::WM;
-  const int wn = (wave % C::WAVES_N) * C::WN;
-  const int m0 = tm * C::BM;
-  const int n0 = tn * C::BN;
+  const int wm = (wave >> 1) * big::WM;
+  const int wn = (wave & 1) * big::WN;
+  const int m0 = tm * 256;
+  const int n0 = tn * 256;
 #pragma unroll
-  for (int i = 0; i < C::TM; ++i)
+  for (int i = 0; i < big::TM; ++i)
 #pragma unroll
-    for (int j = 0; j < C::TN; ++j)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+    for (int j = 0; j < big::TN; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
   int nk, k0 = 0;
-  if (pb.ksplit > 1) {
+  if (pb.ksplit > 1) {  // splits are counted in 64-wide k units
     const int total = (pb.seg[0].k_len + kBK - 1) / kBK;
     const int first = split * pb.kps;
-    nk = total - first < pb.kps ? total - first : pb.kps;
+    const int n64 = total - first < pb.kps ? total - first : pb.kps;
     k0 = first * kBK;
+    const int kend = k0 + n64 * kBK < pb.seg[0].k_len ? k0 + n64 * kBK : pb.seg[0].k_len;
+    nk = (kend - k0 + big::BK - 1) / big::BK;
   } else {
     nk = 0;
-    for (int s = 0; s < pb.nseg; ++s) nk += (pb.seg[s].k_len + kBK - 1) / kBK;
+    for (int s = 0; s < pb.nseg; ++s) nk += (pb.seg[s].k_len + big::BK - 1) / big::BK;
   }
   if (nk <= 0) return;
 
-  // Cursors over the K segments: the direct loads run one k-tile ahead of
-  // the tile being multiplied, a register-staged B two.
-  int segA = 0, k0A = k0, klenA = pb.seg[0].k_len;
-  int segB = 0, k0B = k0, klenB = pb.seg[0].k_len;
-  DtlIter<C::BM> ita;
-  DtlIter<C::BN> itb;
-  TileIter ib;
-  TileRegs rb;
-  setup_dtl<C::BM>(ita, pb.seg[0].a, m0, pb.M, wave);
-  if constexpr (kBDtl) setup_dtl<C::BN>(itb, pb.seg[0].b, n0, pb.N, wave);
-  else setup_tile<LB, C::BN>(ib, pb.seg[0].b, n0, pb.N, tid);
+  // Load cursor: the next k-tile to load (segment seg, offset kc, length
+  // klen); `loaded` k-tiles have been issued. Past the last k-tile the
+  // cursor stays and every lane's load is out of range (zeros, no traffic).
+  int seg = 0, kc = k0, klen = pb.seg[0].k_len, loaded = 0;
+  BigIter<LA> ia;
+  BigIter<LB> ib;
+  big_setup<LA>(ia, pb.seg[0].a, m0, pb.M, wave);
+  big_setup<LB>(ib, pb.seg[0].b, n0, pb.N, wave);
+  const int kb = 8 * ((lane & 3) ^ kswz(lane >> 2));  // K-major lanes: k offset in a k-tile
+  FragAddr<LA> fa;
+  FragAddr<LB> fb;
+  frag_addr_setup<LA>(fa, wm, lane);
+  frag_addr_setup<LB>(fb, wn, lane);
 
-  auto advanceA = [&]() __attribute__((always_inline)) {
-    k0A += kBK;
-    if (k0A >= klenA) {
-      ++segA;
-      k0A = 0;
-      klenA = pb.seg[segA].k_len;
-      setup_dtl<C::BM>(ita, pb.seg[segA].a, m0, pb.M, wave);
-      if constexpr (kBDtl) setup_dtl<C::BN>(itb, pb.seg[segA].b, n0, pb.N, wave);
+  auto cursor_loads = [&](rsrc_t& ra, rsrc_t& rb, uint32_t (&oa)[big::LOADS],
+                          uint32_t (&ob)[big::LOADS]) __attribute__((always_inline)) {
+    const bool live = loaded < nk;
+    ra = make_rsrc(ia.base + (int64_t)kc * ia.kstep);
+    rb = make_rsrc(ib.base + (int64_t)kc * ib.kstep);
+#pragma unroll
+    for (int i = 0; i < big::LOADS; ++i) {
+      oa[i] = big_oob<LA>(ia, i, live, kc, kb, klen);
+      ob[i] = big_oob<LB>(ib, i, live, kc, kb, klen);
     }
   };
-  auto advanceB = [&]() __attribute__((always_inline)) {  // register-staged B only
-    k0B += kBK;
-    if (k0B >= klenB) {
-      ++segB;
-      k0B = 0;
-      klenB = pb.seg[segB].k_len;
-      setup_tile<LB, C::BN>(ib, pb.seg[segB].b, n0, pb.N, tid);
+  auto advance = [&]() __attribute__((always_inline)) {
+    ++loaded;
+    if (loaded >= nk) return;
+    kc += big::BK;
+    if (kc >= klen) {
+      ++seg;
+      kc = 0;
+      klen = pb.seg[seg].k_len;
+      big_setup<LA>(ia, pb.seg[seg].a, m0, pb.M, wave);
+      big_setup<LB>(ib, pb.seg[seg].b, n0, pb.N, wave);
     }
   };
 
-  // k-tile 0 -> stage 0; a register-staged B also takes k-tile 1 into registers
-  dtl_load<C::BM>(ita, stage0, k0A, klenA, wave);
-  if constexpr (kBDtl) dtl_load<C::BN>(itb, stage0 + C::A_BYTES, k0A, klenA, wave);
-  dtl_zero_tail<C::BM>(stage0, k0A, klenA, wave);
-  if constexpr (kBDtl) {
-    dtl_zero_tail<C::BN>(stage0 + C::A_BYTES, k0A, klenA, wave);
-  } else {
-    load_tile<LB, C::BN>(rb, ib, k0B, klenB, tid);
-    store_tile<LB, C::BN>(rb, stage0 + C::A_BYTES, tid, k0B, klenB);
-    if (nk > 1) {
-      advanceB();
-      load_tile<LB, C::BN>(rb, ib, k0B, klenB, tid);
+  // Prologue: k-tiles 0..3 into the four stages; wait for k-tile 0.
+#pragma unroll
+  for (int j = 0; j < big::STAGES; ++j) {
+    rsrc_t ra, rb;
+    uint32_t oa[big::LOADS], ob[big::LOADS];
+    cursor_loads(ra, rb, oa, ob);
+#pragma unroll
+    for (int i = 0; i < big::LOADS; ++i) {
+      buf_load_lds(ra, ia.off[i] | oa[i], st[j] + (wave + 4 * i) * 1024);
+      buf_load_lds(rb, ib.off[i] | ob[i], st[j] + big::OP_BYTES + (wave + 4 * i) * 1024);
     }
+    advance();
   }
+  __builtin_amdgcn_s_waitcnt(big::kWaitVm24);
   __syncthreads();
+  BigFrags f0, f1;
+  static_for<big::TN * reads_per_frag<LB>() + big::TM * reads_per_frag<LA>()>([&](auto qc) {
+    big_read<LA, LB, decltype(qc)::value>(f0, st[0], st[0] + big::OP_BYTES, fa, fb);
+  });
 
-  // k-tile t: loads of k-tile t + 1 into stage nx, multiply from stage st.
-  // One code path for every t (no branch around the MFMAs, whose 256
-  // accumulators would otherwise be merged and copied): past the last
-  // k-tile the cursors stay put and the same tile is loaded again into the
-  // stage that is no longer read.
-  auto iteration = [&](int t, char* st, char* nx) __attribute__((always_inline)) {
-    if (t + 1 < nk) advanceA();
-    dtl_load<C::BM>(ita, nx, k0A, klenA, wave);
-    if constexpr (kBDtl) dtl_load<C::BN>(itb, nx + C::A_BYTES, k0A, klenA, wave);
-    __builtin_amdgcn_sched_barrier(0);
-    if constexpr (kBDtl) {
-      dtl_tile<C, LB, false, false>(acc, st, wm, wn, lane, rb, nullptr, ib, 0, 0, tid);
-    } else {
-      const int k0s = k0B, klens = klenB;  // B in registers (k-tile t + 1)
-      if (t + 2 < nk) advanceB();          // B to load (k-tile t + 2)
-      zero_tail<LB, C::BN>(rb, k0s, klens, tid);
-      dtl_tile<C, LB, true, true>(acc, st, wm, wn, lane, rb, nx + C::A_BYTES, ib, k0B, klenB, tid);
-    }
-    dtl_zero_tail<C::BM>(nx, k0A, klenA, wave);
-    if constexpr (kBDtl) dtl_zero_tail<C::BN>(nx + C::A_BYTES, k0A, klenA, wave);
+  // k-tile t in stage j = t % 4 (fragments in fc), k-tile t + 1 in stage j + 1.
+  auto iteration = [&](char* cur, char* nxt, BigFrags& fc, BigFrags& fn)
+      __attribute__((always_inline)) {
+    // This wave's loads of k-tile t + 1 have landed (the vmcnt wait is
+    // explicit: the compiler's fence does not cover loads into LDS) and its
+    // fragment reads of k-tile t are done (fence); the barrier publishes
+    // k-tile t + 1 and releases stage cur.
+    __builtin_amdgcn_s_waitcnt(big::kWaitVm16);
     __syncthreads();
+    rsrc_t ra, rb;
+    uint32_t oa[big::LOADS], ob[big::LOADS];
+    cursor_loads(ra, rb, oa, ob);
+    big_tile<LA, LB>(acc, fn, fc, nxt, nxt + big::OP_BYTES, fa, fb, ia, ib, ra, rb, oa, ob, cur,
+                     cur + big::OP_BYTES, wave);
+    advance();
   };
-  int t = 0;
-  for (; t + 1 < nk; t += 2) {
-    iteration(t, stage0, stage1);
-    iteration(t + 1, stage1, stage0);
+  // The body runs the four stages in turn; the k-tile count is rounded up to
+  // a multiple of four (the extra k-tiles are zeros and add nothing).
+  for (int t = 0; t < nk; t += big::STAGES) {
+    iteration(st[0], st[1], f0, f1);
+    iteration(st[1], st[2], f1, f0);
+    iteration(st[2], st[3], f0, f1);
+    iteration(st[3], st[0], f1, f0);
   }
-  if (t < nk) iteration(t, stage0, stage1);
+  __builtin_amdgcn_s_waitcnt(big::kWaitVm0);
+  __syncthreads();  // loads past the end have landed; the epilogue may reuse the LDS
+}
+
+// Per-element view of a wave's accumulators: f(m, n, value) for the
+// elements of MFMA-tile row i (for_each_acc_row) or of the whole wave
+// sub-tile at (m0, n0) (for_each_acc), in either MFMA layout:
+//   16 x 16 tiles (f32x4_t): element v of tile (i, j) is row 16 i + 4 (lane / 16) + v,
+//                            column 16 j + lane % 16
+//   32 x 32 tiles (f32x16_t): row 32 i + 8 (v / 4) + 4 (lane / 32) + v % 4,
+//                            column 32 j + lane % 32
+// The TN * (4 or 16) elements of a row are visited in the order (j, v).
+template <int TM, int TN, class F>
+__device__ __forceinline__ void for_each_acc_row(f32x4_t (&acc)[TM][TN], int i, int m0, int n0,
+                                                 int lane, F&& f) {
+  const int r0 = m0 + 16 * i + 4 * (lane >> 4), c0 = n0 + (lane & 15);
+#pragma unroll
+  for (int j = 0; j < TN; ++j)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) f(r0 + v, c0 + 16 * j, acc[i][j][v]);
+}
+
+template <int TM, int TN, class F>
+__device__ __forceinline__ void for_each_acc_row(f32x16_t (&acc)[TM][TN], int i, int m0, int n0,
+                                                 int lane, F&& f) {
+  const int r0 = m0 + 32 * i + 4 * (lane >> 5), c0 = n0 + (lane & 31);
+#pragma unroll
+  for (int j = 0; j < TN; ++j)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) f(r0 + 8 * (v >> 2) + (v & 3), c0 + 32 * j, acc[i][j][v]);
+}
+
+template <typename AccT, int TM, int TN, class F>
+__device__ __forceinline__ void for_each_acc(AccT (&acc)[TM][TN], int m0, int n0, int lane, F&& f) {
+#pragma unroll
+  for (int i = 0; i < TM; ++i) for_each_acc_row(acc, i, m0, n0, lane, f);
 }
 
 // The GEMM kernel: mainloop + epilogue functor
 //   epi(acc, m_base, n_base, lane, smem, split) with m_base / n_base the
-//   origin of this wave's sub-tile. smem may be reused by the epilogue.
+//   origin of this wave's sub-tile and acc in the path's MFMA layout
+//   (f32x4_t[8][8] for the 256 x 256 tile, f32x16_t[TM][TN] otherwise).
+//   smem may be reused by the epilogue.
 template <class C, int LA, int LB, class Epi>
 __global__ __launch_bounds__(kThreads) void gemm_kernel(const Problem pb, const Epi epi) {
-  __shared__ __attribute__((aligned(16))) char stage0[C::STAGE_BYTES];
-  __shared__ __attribute__((aligned(16))) char stage1[C::STAGE_BYTES];
-  char* smem = stage0;
   int tm, tn, split;
   if (!tile_coords(pb, tm, tn, split)) return;
-  f32x16_t acc[C::TM][C::TN];
-  if constexpr (LA == kKMajor && C::BM == 256 && C::BN == 256)
-    mainloop_dtl<C, LB>(pb, tm, tn, split, stage0, stage1, acc);
-  else
-    mainloop<C, LA, LB>(pb, tm, tn, split, stage0, stage1, acc);
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
-  epi(acc, tm * C::BM + (wave / C::WAVES_N) * C::WM, tn * C::BN + (wave % C::WAVES_N) * C::WN,
-      tid & 63, smem, split);
+  if constexpr (C::BM == 256 && C::BN == 256) {
+    __shared__ __attribute__((aligned(16))) char s0[big::STAGE_BYTES];
+    __shared__ __attribute__((aligned(16))) char s1[big::STAGE_BYTES];
+    __shared__ __attribute__((aligned(16))) char s2[big::STAGE_BYTES];
+    __shared__ __attribute__((aligned(16))) char s3[big::STAGE_BYTES];
+    char* const st[big::STAGES] = {s0, s1, s2, s3};
+    f32x4_t acc[big::TM][big::TN];
+    big_mainloop<LA, LB>(pb, tm, tn, split, st, acc);
+    epi(acc, tm * 256 + (wave >> 1) * big::WM, tn * 256 + (wave & 1) * big::WN, tid & 63, s0,
+        split);
+  } else {
+    __shared__ __attribute__((aligned(16))) char stage0[C::STAGE_BYTES];
+    __shared__ __attribute__((aligned(16))) char stage1[C::STAGE_BYTES];
+    f32x16_t acc[C::TM][C::TN];
+    mainloop<C, LA, LB>(pb, tm, tn, split, stage0, stage1, acc);
+    epi(acc, tm * C::BM + (wave / C::WAVES_N) * C::WM, tn * C::BN + (wave % C::WAVES_N) * C::WN,
+        tid & 63, stage0, split);
+  }
 }
 
 // --------------------------------------------------------------- epilogues --
 
-// C = alpha * acc + beta * C (C of type TC, row-major with ldc).
+// C = alpha * acc + beta * C (C of type TC, row-major with ldc). With beta,
+// the old values of a whole MFMA-tile row (i) are loaded before any is
+// written, so the loads overlap instead of each waiting for the last.
 template <typename TC>
 struct EpiStore {
   TC* C;
@@ -872,27 +1027,28 @@ struct EpiStore {
   int M, N;
   float alpha, beta;
 
-  template <int TM, int TN>
-  __device__ __forceinline__ void operator()(f32x16_t (&acc)[TM][TN], int m0, int n0, int lane,
-                                             char*, int) const {
-    const int col = lane & 31;
+  template <typename AccT, int TM, int TN>
+  __device__ __forceinline__ void operator()(AccT (&acc)[TM][TN], int m0, int n0, int lane, char*,
+                                             int) const {
+    if (beta == 0.f) {
+      for_each_acc(acc, m0, n0, lane, [&](int m, int n, float v) {
+        if (m < M && n < N) C[(int64_t)m * ldc + n] = from_f32<TC>(alpha * v);
+      });
+      return;
+    }
+    constexpr int V = sizeof(AccT) / sizeof(float);
 #pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      const int n = n0 + 32 * j + col;
-      if (n >= N) continue;
-#pragma unroll
-      for (int i = 0; i < TM; ++i) {
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const int m = m0 + 32 * i + acc_row(v, lane);
-          if (m < M) {
-            TC* p = C + (int64_t)m * ldc + n;
-            float r = alpha * acc[i][j][v];
-            if (beta != 0.f) r += beta * to_f32(*p);
-            *p = from_f32<TC>(r);
-          }
-        }
-      }
+    for (int i = 0; i < TM; ++i) {
+      float old[TN * V];
+      int k = 0;
+      for_each_acc_row(acc, i, m0, n0, lane, [&](int m, int n, float) {
+        old[k++] = (m < M && n < N) ? to_f32(C[(int64_t)m * ldc + n]) : 0.f;
+      });
+      k = 0;
+      for_each_acc_row(acc, i, m0, n0, lane, [&](int m, int n, float v) {
+        const float o = old[k++];
+        if (m < M && n < N) C[(int64_t)m * ldc + n] = from_f32<TC>(alpha * v + beta * o);
+      });
     }
   }
 };
@@ -902,23 +1058,13 @@ struct EpiPartial {
   float* P;
   int M, N;
 
-  template <int TM, int TN>
-  __device__ __forceinline__ void operator()(f32x16_t (&acc)[TM][TN], int m0, int n0, int lane,
-                                             char*, int split) const {
-    const int col = lane & 31;
+  template <typename AccT, int TM, int TN>
+  __device__ __forceinline__ void operator()(AccT (&acc)[TM][TN], int m0, int n0, int lane, char*,
+                                             int split) const {
     float* base = P + (int64_t)split * M * N;
-#pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      const int n = n0 + 32 * j + col;
-      if (n >= N) continue;
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const int m = m0 + 32 * i + acc_row(v, lane);
-          if (m < M) base[(int64_t)m * N + n] = acc[i][j][v];
-        }
-    }
+    for_each_acc(acc, m0, n0, lane, [&](int m, int n, float v) {
+      if (m < M && n < N) base[(int64_t)m * N + n] = v;
+    });
   }
 };
 

@@ -76,30 +76,18 @@ struct EpiSwigluBwd {
   int64_t ld;
   int M, N;
 
-  template <int TM, int TN>
-  __device__ __forceinline__ void operator()(f32x16_t (&acc)[TM][TN], int m0, int n0, int lane,
-                                             char*, int) const {
-    const int col = lane & 31;
-#pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      const int n = n0 + 32 * j + col;
-      if (n >= N) continue;
-#pragma unroll
-      for (int i = 0; i < TM; ++i) {
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const int m = m0 + 32 * i + acc_row(v, lane);
-          if (m >= M) continue;
-          const int64_t o = (int64_t)m * ld + n;
-          const float g = to_f32(gate[o]);
-          const float u = to_f32(up[o]);
-          const float dh = acc[i][j][v];
-          const float s = sigmoid_f(g);
-          dgate[o] = from_f32<bf16>(((dh * u) * s) * (1.0f + g * (1.0f - s)));
-          dup[o] = from_f32<bf16>(dh * (g * s));
-        }
-      }
-    }
+  template <typename AccT, int TM, int TN>
+  __device__ __forceinline__ void operator()(AccT (&acc)[TM][TN], int m0, int n0, int lane, char*,
+                                             int) const {
+    for_each_acc(acc, m0, n0, lane, [&](int m, int n, float dh) {
+      if (m >= M || n >= N) return;
+      const int64_t o = (int64_t)m * ld + n;
+      const float g = to_f32(gate[o]);
+      const float u = to_f32(up[o]);
+      const float s = sigmoid_f(g);
+      dgate[o] = from_f32<bf16>(((dh * u) * s) * (1.0f + g * (1.0f - s)));
+      dup[o] = from_f32<bf16>(dh * (g * s));
+    });
   }
 };
 
