@@ -104,10 +104,12 @@ def bench_rmsnorm(dev, stream, reps):
             "bwd_us": round(b_ms * 1e3, 2), "bwd_GB/s": round(RMS_BWD_BYTES / (b_ms * 1e-3) / 1e9, 1)}
 
 
-def bench_flce(dev, stream, reps):
-    """Chunked fused linear cross-entropy fwd + bwd: hidden [8192, 2048],
-    lm_head [151936, 2048] ~N(0, 0.02), no bias, 10% of labels ignored,
-    chunk 8192; 15.29 TFLOP per fwd+bwd."""
+def bench_flce(dev, stream, reps, token_chunk=None):
+    """Fused linear cross-entropy fwd + bwd as the autograd Function runs it:
+    hidden [8192, 2048], lm_head [151936, 2048] ~N(0, 0.02), no bias, 10% of
+    labels ignored; the forward forms loss, dH and dW in one pass (logits
+    computed once), the backward applies grad_output. 15.29 TFLOP of
+    necessary GEMM work (logits, dH, dW) per fwd+bwd."""
     import torch
 
     from metal_liger_amd import hip_ops
@@ -120,20 +122,21 @@ def bench_flce(dev, stream, reps):
     state = {}
 
     def fwd():
-        state["f"] = hip_ops.flce_fwd(h, w, lab)
+        state["f"] = hip_ops.flce_fwd_grad(h, w, lab, token_chunk=token_chunk)
 
     def bwd():
-        _, lse, nv = state["f"]
-        hip_ops.flce_bwd(h, w, lab, None, -100, lse, nv, one, FLCE_CHUNK)
+        _, _, _, dh, dw = state["f"]
+        hip_ops.flce_scale_grads(one, dh, dw)
 
     f_ms = time_launches(fwd, stream, reps)
     b_ms = time_launches(bwd, stream, reps)
     tot = f_ms + b_ms
     tf = FLCE_FLOP / (tot * 1e-3) / 1e12
+    T = token_chunk or hip_ops.flce_token_chunk(FLCE_N, FLCE_V)
     del h, w, lab, state
     torch.cuda.empty_cache()
     return {"fwd_ms": round(f_ms, 3), "bwd_ms": round(b_ms, 3), "TFLOP/s": round(tf, 1),
-            "mfma_frac": round(tf / MFMA_PEAK_TFLOPS, 4), "flop": FLCE_FLOP}
+            "mfma_frac": round(tf / MFMA_PEAK_TFLOPS, 4), "flop": FLCE_FLOP, "token_chunk": T}
 
 
 def bench_lora_bwd(dev, stream, reps):

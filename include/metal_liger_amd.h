@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define ML_ABI_VERSION 1
+#define ML_ABI_VERSION 2
 
 /* dtype tags */
 #define ML_F32 0
@@ -177,6 +177,35 @@ int ml_flce_bwd(const void* hidden, int64_t ldh, const void* weight, int64_t ldw
                 int64_t hidden_size, int64_t ignore_index, const float* lse, const float* n_valid,
                 const float* grad_loss, int64_t chunk, void* d_hidden, void* d_weight,
                 void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Loss and gradients in one call, with the logits computed once (the schedule
+ * _FusedLinearCrossEntropyFunction uses; replaces its forward + backward,
+ * ops/fused_linear_cross_entropy.py:93-185, whose backward recomputes every
+ * logits chunk). Tokens go in chunks of token_chunk: per chunk one bf16
+ * [token_chunk, vocab] workspace buffer holds exp(z - max) and then the
+ * dlogits, dH rows come from a split-K GEMM and dW accumulates (bf16).
+ * Outputs as ml_flce_fwd, plus d_hidden [n_tokens, hidden_size] and d_weight
+ * [vocab, hidden_size] (bf16, dense; either may be NULL) formed for
+ * d(loss) = 1. With both NULL this is the loss-only forward.
+ */
+size_t ml_flce_fwd_grad_workspace_bytes(int64_t n_tokens, int64_t vocab, int64_t hidden_size,
+                                        int64_t token_chunk, int need_dhidden);
+int ml_flce_fwd_grad(const void* hidden, int64_t ldh, const void* weight, int64_t ldw,
+                     const void* bias, int bias_dtype, const int64_t* labels, int64_t n_tokens,
+                     int64_t vocab, int64_t hidden_size, int64_t ignore_index, int64_t token_chunk,
+                     float* loss, float* lse, float* n_valid, void* d_hidden, void* d_weight,
+                     void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * The upstream gradient of the loss (the grad_output of the reference's
+ * backward, ops/fused_linear_cross_entropy.py:160-167) applied to gradients
+ * from ml_flce_fwd_grad: d_hidden[0:n_hidden] and d_weight[0:n_weight] (bf16)
+ * are multiplied by *grad_loss (device fp32 scalar) in place; nothing is
+ * written when it equals 1. Either array may be NULL with its size 0.
+ */
+int ml_flce_scale_grads(const float* grad_loss, void* d_hidden, int64_t n_hidden, void* d_weight,
+                        int64_t n_weight, void* stream);
 
 /* ----------------------------------------------------------- fused LoRA bwd
  * Replaces _LoRA_QKV.backward (ops/fused_lora.py:121-171). Three adapters

@@ -69,6 +69,13 @@ SIGNATURES: dict[str, tuple] = {
         [_p, _i64, _p, _i64, _p, _i32, _p, _i64, _i64, _i64, _i64, _p, _p, _p, _i64, _p, _p, _p,
          _sz, _p],
     ),
+    "ml_flce_fwd_grad_workspace_bytes": (_sz, [_i64, _i64, _i64, _i64, _i32]),
+    "ml_flce_fwd_grad": (
+        _i32,
+        [_p, _i64, _p, _i64, _p, _i32, _p, _i64, _i64, _i64, _i64, _i64, _p, _p, _p, _p, _p, _p,
+         _sz, _p],
+    ),
+    "ml_flce_scale_grads": (_i32, [_p, _p, _i64, _p, _i64, _p]),
     "ml_gemm_splitk_workspace_bytes": (_sz, [_i64, _i64, _i64, _i32]),
     "ml_gemm_bf16_splitk": (
         _i32,
@@ -89,7 +96,7 @@ SIGNATURES: dict[str, tuple] = {
     ),
 }
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _lib = None
 _lock = threading.Lock()

@@ -1,23 +1,41 @@
 // Fused linear cross-entropy for gfx950
 // (ops/fused_linear_cross_entropy.py:39-185 of the reference).
 //
-// Forward: ONE bf16 MFMA GEMM over the whole vocabulary, z = h W^T (+ b).
-//   The logits never leave registers: each wave reduces its 128-column slice
-//   of the tile to per-row (max, sum exp(z - max)) partials and the lane that
-//   holds (row, label) writes the label logit. A row-parallel pass merges the
-//   partials into lse (the online-softmax merge of the reference's chunk
-//   loop, :39-55) and the masked per-token loss; a fixed-order single-block
-//   pass forms the mean over valid tokens (clamped at 1, :149).
-// Backward, per vocabulary chunk of `chunk` columns (the reference's
-//   chunk_size, :57-80):
-//   1. recompute the logits tile and write dlogits in bf16 from the epilogue:
-//      d = (exp(z - lse) - [col == label]) * mask * (grad / n_valid)
-//   2. dH += D W_c   (fp32 accumulation across chunks; MN-major B operand)
-//   3. dW_c = D^T H  (written once per chunk, straight to bf16)
-//   Memory beyond inputs/outputs: one [tokens, chunk] bf16 buffer plus an
-//   fp32 [tokens, hidden] dH accumulator; the [tokens, vocab] logits never
-//   exist. dH / dW are skipped when not requested (frozen lm_head).
+// Two schedules share the kernels below.
+//
+// Loss and gradients in one pass (ml_flce_fwd_grad), over chunks of T tokens:
+//   1. Z = H_c W^T (+ b) as a bf16 MFMA GEMM; its epilogue reduces each wave's
+//      128 logit columns per row to (m, s) = (max z, sum exp(z - m)) and
+//      stores e = exp(z - m) in bf16 ([T, vocab] buffer). e lies in (0, 1],
+//      so bf16 keeps it to 2^-9 relative whatever the logit's size. The
+//      label logits come from a dot product of each token with its label's
+//      weight row.
+//   2. a row pass merges the (m, s) partials into lse and the masked loss;
+//   3. an elementwise pass turns e into dlogits in place:
+//        d = (e exp(m - lse) - [col == label]) * mask / n_valid
+//   4. dH_c = D W     (split-K MFMA GEMM over the vocabulary; MN-major W)
+//   5. dW  += D^T H_c (MFMA GEMM, both operands MN-major; accumulated in bf16
+//      across token chunks).
+//   The logits are computed once: three GEMMs (2 N V H FLOP each) in total,
+//   against the four of a vocabulary-chunked schedule that must recompute
+//   them after the logsumexp is known. The gradients are formed for
+//   d(loss) = 1; ml_flce_scale_grads applies the actual upstream gradient.
+//   Peak extra memory: one [T, vocab] bf16 buffer (no [tokens, vocab]
+//   tensor exists; the reference keeps an fp32 copy of W, an fp32 dW and an
+//   fp32 [tokens, chunk] logits chunk).
+//
+// Loss only (ml_flce_fwd) + vocabulary-chunked backward (ml_flce_bwd), for
+// callers that keep only (lse, n_valid) between the passes:
+//   forward: ONE logits GEMM over the whole vocabulary with the (m, s)
+//   epilogue (nothing stored), the row pass and a fixed-order mean over
+//   valid tokens (clamped at 1, :149).
+//   backward, per vocabulary chunk of `chunk` columns (the reference's
+//   chunk_size, :57-80): recompute the logits tile, write bf16 dlogits from
+//   the epilogue, dH += D W_c (fp32 accumulator), dW_c = D^T H.
+// dH / dW are skipped when not requested (frozen lm_head).
 #include <math.h>
+
+#include <algorithm>
 
 #include "gemm_core.h"
 
@@ -33,16 +51,28 @@ constexpr int kColBlock = big::WN;  // columns per (max, sum) partial: one wave'
 __device__ __forceinline__ float exp_f(float x) { return __builtin_amdgcn_exp2f(x * kLog2e); }
 
 // Reductions over the 16 lanes of a group (the lanes that hold one row of a
-// 16 x 16 accumulator tile).
+// 16 x 16 accumulator tile), with DPP lane moves inside 16-lane rows:
+// quad_perm [1,0,3,2] (xor 1), quad_perm [2,3,0,1] (xor 2), row_half_mirror
+// (lane i <-> 7 - i in each half-row) and row_mirror (i <-> 15 - i); after
+// the four steps every lane holds the result over its 16 lanes.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF,
+                                                            0xF, false));
+}
+constexpr int kDppXor1 = 0xB1, kDppXor2 = 0x4E, kDppHalfMirror = 0x141, kDppMirror = 0x140;
+
 __device__ __forceinline__ float grp16_max(float v) {
-#pragma unroll
-  for (int off = 8; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 16));
-  return v;
+  v = fmaxf(v, dpp_f<kDppXor1>(v));
+  v = fmaxf(v, dpp_f<kDppXor2>(v));
+  v = fmaxf(v, dpp_f<kDppHalfMirror>(v));
+  return fmaxf(v, dpp_f<kDppMirror>(v));
 }
 __device__ __forceinline__ float grp16_sum(float v) {
-#pragma unroll
-  for (int off = 8; off > 0; off >>= 1) v += __shfl_xor(v, off, 16);
-  return v;
+  v += dpp_f<kDppXor1>(v);
+  v += dpp_f<kDppXor2>(v);
+  v += dpp_f<kDppHalfMirror>(v);
+  return v + dpp_f<kDppMirror>(v);
 }
 
 template <typename TB>
@@ -52,36 +82,35 @@ __device__ __forceinline__ float bias_at(const TB* b, int64_t n) {
 
 // ------------------------------------------------------------ forward epi --
 // Each wave reduces its 128 logit columns to a (max, sum exp(z - max))
-// partial per row; the lane holding (row, label) writes the label logit.
-template <typename TB>
-struct EpiLse {
+// partial per row. With STORE, e = exp(z - max) also replaces the
+// accumulators and is written (bf16) at E[row * ldE + col] through the staged
+// epilogue (16-byte stores). The label logits come from label_logit_kernel.
+template <typename TB, bool STORE>
+struct EpiRowLse {
   const TB* bias;
-  const int64_t* labels;
   float* pmax;  // [M][nblk]
   float* psum;  // [M][nblk]
-  float* zy;    // [M]
+  bf16* E;      // STORE only
+  int64_t ldE;
   int M, V, nblk;
 
-  __device__ __forceinline__ void operator()(f32x4_t (&acc)[big::TM][big::TN], int m0, int n0,
-                                             int lane, char*, int) const {
-    // a wave whose 128 columns all lie past the vocabulary (second half of
-    // the last tile) owns no partial slot
-    if (n0 >= V) return;
+  template <bool FULL>
+  __device__ __forceinline__ void rows(f32x4_t (&acc)[big::TM][big::TN], int m0, int n0,
+                                       int lane) const {
     const int c = lane & 15;
     float bj[big::TN];
     bool okj[big::TN];
 #pragma unroll
     for (int j = 0; j < big::TN; ++j) {
       const int n = n0 + 16 * j + c;
-      okj[j] = n < V;
-      bj[j] = okj[j] ? bias_at(bias, n) : 0.f;
+      okj[j] = FULL || n < V;
+      bj[j] = bias ? (okj[j] ? to_f32(bias[n]) : 0.f) : 0.f;
     }
     const int nb = n0 / kColBlock;
 #pragma unroll
     for (int i = 0; i < big::TM; ++i) {
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        const int m = m0 + 16 * i + 4 * (lane >> 4) + v;
         float z[big::TN];
         float mx = -INFINITY;
 #pragma unroll
@@ -89,19 +118,16 @@ struct EpiLse {
           z[j] = okj[j] ? acc[i][j][v] + bj[j] : -INFINITY;
           mx = fmaxf(mx, z[j]);
         }
-        if (m < M) {
-          const int64_t lab = labels[m];
-#pragma unroll
-          for (int j = 0; j < big::TN; ++j)
-            if (okj[j] && lab == (int64_t)(n0 + 16 * j + c)) zy[m] = z[j];
-        }
-        mx = grp16_max(mx);
+        mx = grp16_max(mx);  // finite: a wave's first column is always < V
         float s = 0.f;
-        if (mx != -INFINITY) {
 #pragma unroll
-          for (int j = 0; j < big::TN; ++j) s += exp_f(z[j] - mx);
+        for (int j = 0; j < big::TN; ++j) {
+          const float e = exp_f(z[j] - mx);  // 0 for columns past V
+          s += e;
+          if constexpr (STORE) acc[i][j][v] = e;
         }
         s = grp16_sum(s);
+        const int m = m0 + 16 * i + 4 * (lane >> 4) + v;
         if (c == 0 && m < M) {
           pmax[(int64_t)m * nblk + nb] = mx;
           psum[(int64_t)m * nblk + nb] = s;
@@ -109,7 +135,117 @@ struct EpiLse {
       }
     }
   }
+
+  __device__ __forceinline__ void operator()(f32x4_t (&acc)[big::TM][big::TN], int m0, int n0,
+                                             int lane, char* lds, int) const {
+    // a wave whose 128 columns all lie past the vocabulary (second half of
+    // the last tile) owns no partial slot
+    if (n0 >= V) return;
+    if (n0 + big::WN <= V)
+      rows<true>(acc, m0, n0, lane);
+    else
+      rows<false>(acc, m0, n0, lane);
+    if constexpr (STORE) {
+      stage_rows_bf16(
+          lds, lane, m0, n0, [&](int i, int j, int v) { return acc[i][j][v]; },
+          [&](int m, int n, const float (&x)[8]) {
+            if (m < M && n < V) store_row8_bf16(E + (int64_t)m * ldE + n, n, V, x);
+          });
+    }
+  }
 };
+
+// zy[t] = h_t . W[label_t] (+ b[label_t]) for a label in [0, V), else 0
+// (the label logit, as the reference forms it from the gathered weight rows,
+// ops/fused_linear_cross_entropy.py:131-134). One wave per token; H % 8 == 0.
+template <typename TB>
+__global__ __launch_bounds__(256) void label_logit_kernel(
+    const bf16* __restrict__ hidden, int64_t ldh, const bf16* __restrict__ weight, int64_t ldw,
+    const TB* __restrict__ bias, const int64_t* __restrict__ labels, int M, int64_t V, int H,
+    float* __restrict__ zy) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= M) return;
+  const int64_t lab = labels[row];
+  if (lab < 0 || lab >= V) {
+    if (lane == 0) zy[row] = 0.f;
+    return;
+  }
+  const bf16* h = hidden + (int64_t)row * ldh;
+  const bf16* w = weight + lab * ldw;
+  float acc = 0.f;
+  for (int k = lane * 8; k < H; k += 64 * 8) {
+    float a[8], b[8];
+    load_n<bf16, 8>(h + k, a);
+    load_n<bf16, 8>(w + k, b);
+#pragma unroll
+    for (int q = 0; q < 8; ++q) acc += a[q] * b[q];
+  }
+  acc = wave_sum(acc);
+  if (lane == 0) zy[row] = acc + (bias ? to_f32(bias[lab]) : 0.f);
+}
+
+// n_valid = #(labels != ignore), as fp32 (one block).
+__global__ __launch_bounds__(1024) void count_valid_kernel(const int64_t* __restrict__ labels, int M,
+                                                           int64_t ignore, float* __restrict__ n_valid) {
+  __shared__ float sc[16];
+  float c = 0.f;
+  for (int i = threadIdx.x; i < M; i += 1024) c += labels[i] != ignore ? 1.f : 0.f;
+  c = wave_sum(c);
+  if ((threadIdx.x & 63) == 0) sc[threadIdx.x >> 6] = c;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float t = 0.f;
+    for (int i = 0; i < 16; ++i) t += sc[i];
+    n_valid[0] = t;
+  }
+}
+
+// In place over E [rows, V] (row stride ldE): d = (e exp(m_blk - lse) -
+// [col == label]) * mask / max(n_valid, 1), bf16. 8 columns per thread (one
+// 16-byte vector; 8 divides the 128-column partial block).
+__global__ __launch_bounds__(256) void dlogit_pass_kernel(bf16* __restrict__ E, int64_t ldE, int rows,
+                                                          int V, const float* __restrict__ pmax,
+                                                          int nblk, const float* __restrict__ lse,
+                                                          const int64_t* __restrict__ labels,
+                                                          int64_t ignore,
+                                                          const float* __restrict__ n_valid) {
+  const int vpr = V / 8;  // vectors per row
+  const int64_t total = (int64_t)rows * vpr;
+  const float inv = 1.0f / fmaxf(n_valid[0], 1.0f);
+  for (int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x; q < total;
+       q += (int64_t)gridDim.x * 256) {
+    const int r = (int)(q / vpr);
+    const int v0 = (int)(q - (int64_t)r * vpr) * 8;
+    const int64_t lab = labels[r];
+    const float sc = lab != ignore ? inv : 0.f;
+    const float f = exp_f(pmax[(int64_t)r * nblk + v0 / kColBlock] - lse[r]) * sc;
+    bf16* p = E + (int64_t)r * ldE + v0;
+    float e[8];
+    load_n<bf16, 8>(p, e);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) e[k] = e[k] * f - (v0 + k == lab ? sc : 0.f);
+    store_n<bf16, 8>(p, e);
+  }
+}
+
+// x *= g[0] for bf16 arrays (skipped as a whole when g[0] == 1).
+__global__ __launch_bounds__(256) void scale_bf16_kernel(bf16* __restrict__ x, int64_t n,
+                                                         const float* __restrict__ g) {
+  const float s = g[0];
+  if (s == 1.0f) return;
+  const int64_t nv = n / 8;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < nv; i += (int64_t)gridDim.x * 256) {
+    float v[8];
+    load_n<bf16, 8>(x + i * 8, v);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) v[k] *= s;
+    store_n<bf16, 8>(x + i * 8, v);
+  }
+  for (int64_t i = nv * 8 + (int64_t)blockIdx.x * 256 + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * 256)
+    x[i] = from_f32<bf16>(to_f32(x[i]) * s);
+}
 
 // One wave per row: merge the row's partials into lse and its loss term.
 __global__ __launch_bounds__(256) void lse_reduce_kernel(
@@ -172,7 +308,8 @@ __global__ __launch_bounds__(1024) void loss_mean_kernel(const float* __restrict
 }
 
 // ----------------------------------------------------------- backward epi --
-// d = (exp(z - lse) - [col == label]) * mask * (grad / n_valid), to bf16.
+// d = (exp(z - lse) - [col == label]) * mask * (grad / n_valid), to bf16
+// (staged epilogue, 16-byte stores).
 template <typename TB>
 struct EpiDlogit {
   const TB* bias;  // chunk-relative (bias + c0) or null
@@ -187,37 +324,37 @@ struct EpiDlogit {
   int64_t c0;
 
   __device__ __forceinline__ void operator()(f32x4_t (&acc)[big::TM][big::TN], int m0, int n0,
-                                             int lane, char*, int) const {
+                                             int lane, char* lds, int) const {
     const int c = lane & 15;
     const float scale = grad[0] / fmaxf(n_valid[0], 1.0f);
     float bj[big::TN];
-    bool okj[big::TN];
 #pragma unroll
     for (int j = 0; j < big::TN; ++j) {
       const int n = n0 + 16 * j + c;
-      okj[j] = n < C;
-      bj[j] = okj[j] ? bias_at(bias, n) : 0.f;
+      bj[j] = n < C ? bias_at(bias, n) : 0.f;
     }
 #pragma unroll
     for (int i = 0; i < big::TM; ++i) {
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const int m = m0 + 16 * i + 4 * (lane >> 4) + v;
-        if (m >= M) continue;
-        const int64_t lab = labels[m];
+        const int64_t lab = m < M ? labels[m] : ignore;
         const float sc = lab != ignore ? scale : 0.f;
-        const float L = lse[m];
-        bf16* drow = D + (int64_t)m * ldd;
+        const float L = m < M ? lse[m] : 0.f;
 #pragma unroll
         for (int j = 0; j < big::TN; ++j) {
-          if (!okj[j]) continue;
           const int n = n0 + 16 * j + c;
           float p = exp_f((acc[i][j][v] + bj[j]) - L);
           if (c0 + n == lab) p -= 1.0f;
-          drow[n] = from_f32<bf16>(p * sc);
+          acc[i][j][v] = p * sc;
         }
       }
     }
+    stage_rows_bf16(
+        lds, lane, m0, n0, [&](int i, int j, int v) { return acc[i][j][v]; },
+        [&](int m, int n, const float (&x)[8]) {
+          if (m < M && n < C) store_row8_bf16(D + (int64_t)m * ldd + n, n, C, x);
+        });
   }
 };
 
@@ -291,13 +428,154 @@ int fwd_impl(const bf16* hidden, int64_t ldh, const bf16* weight, int64_t ldw, c
   Problem pb;
   int rc = make_problem<BigCfg>(pb, M, V, 1, &seg, kKMajor, kKMajor, 0);
   if (rc) return rc;
-  EpiLse<TB> epi{bias, labels, w.pmax, w.psum, w.zy, M, V, nblk};
-  gemm_kernel<BigCfg, kKMajor, kKMajor, EpiLse<TB>><<<dim3(grid_blocks(pb)), kThreads, 0, st>>>(pb, epi);
+  EpiRowLse<TB, false> epi{bias, w.pmax, w.psum, nullptr, 0, M, V, nblk};
+  gemm_kernel<BigCfg, kKMajor, kKMajor, EpiRowLse<TB, false>>
+      <<<dim3(grid_blocks(pb)), kThreads, 0, st>>>(pb, epi);
+  ML_LAUNCH_CHECK();
+  label_logit_kernel<TB><<<dim3((M + 3) / 4), 256, 0, st>>>(hidden, ldh, weight, ldw, bias, labels,
+                                                            M, V, H, w.zy);
   ML_LAUNCH_CHECK();
   lse_reduce_kernel<<<dim3((M + 3) / 4), 256, 0, st>>>(w.pmax, w.psum, nblk, w.zy, labels, ignore,
                                                        M, V, lse, w.loss_row, w.valid_row);
   ML_LAUNCH_CHECK();
   loss_mean_kernel<<<1, 1024, 0, st>>>(w.loss_row, w.valid_row, M, loss, n_valid);
+  ML_LAUNCH_CHECK();
+  return ML_OK;
+}
+
+// ------------------------------------------ loss + gradients in one pass --
+constexpr int kDhTargetItems = 512;  // split-K work items for the dH product (~2 per CU)
+
+int dh_ksplit(int T, int H, int V) {
+  const int tiles = ((T + 255) / 256) * ((H + 255) / 256);
+  const int k64 = (V + kBK - 1) / kBK;
+  int ks = (kDhTargetItems + tiles - 1) / tiles;
+  ks = ks < 1 ? 1 : ks;
+  return ks < k64 ? ks : k64;
+}
+
+// dH split-K partial bytes for a chunk of Tc tokens.
+size_t dh_part_bytes(int64_t Tc, int64_t H, int64_t V) {
+  const int ks = dh_ksplit((int)Tc, (int)H, (int)V);
+  const int k64 = (int)((V + kBK - 1) / kBK);
+  const int kps = (k64 + ks - 1) / ks;
+  const int splits = (k64 + kps - 1) / kps;
+  return (size_t)splits * Tc * H * 4;
+}
+
+struct GradWs {
+  bf16* E;                           // [T, V]
+  float *pmax, *psum;                // [T, nblk]
+  float *zy, *loss_row, *valid_row;  // [N]
+  float* part;                       // dH split-K partials
+  size_t part_bytes;
+};
+
+// Workspace layout (base == nullptr: size only). T = tokens per chunk.
+size_t grad_ws_layout(int64_t N, int64_t V, int64_t H, int64_t T, bool need_dh, GradWs* w,
+                      char* base) {
+  auto al = [](size_t b) { return (b + 255) / 256 * 256; };
+  const int64_t nblk = nblocks(V);
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    char* p = base ? base + off : nullptr;
+    off += al(bytes);
+    return p;
+  };
+  char* e = take((size_t)(T * V) * 2);
+  char* pm = take((size_t)(T * nblk) * 4);
+  char* ps = take((size_t)(T * nblk) * 4);
+  char* zy = take((size_t)N * 4);
+  char* lr = take((size_t)N * 4);
+  char* vr = take((size_t)N * 4);
+  size_t part = 0;
+  if (need_dh) {
+    part = dh_part_bytes(T, H, V);
+    if (N % T) part = std::max(part, dh_part_bytes(N % T, H, V));
+  }
+  char* pt = take(part);
+  if (w) {
+    w->E = reinterpret_cast<bf16*>(e);
+    w->pmax = reinterpret_cast<float*>(pm);
+    w->psum = reinterpret_cast<float*>(ps);
+    w->zy = reinterpret_cast<float*>(zy);
+    w->loss_row = reinterpret_cast<float*>(lr);
+    w->valid_row = reinterpret_cast<float*>(vr);
+    w->part = reinterpret_cast<float*>(pt);
+    w->part_bytes = part;
+  }
+  return off;
+}
+
+template <typename TB>
+int fwd_grad_impl(const bf16* hidden, int64_t ldh, const bf16* weight, int64_t ldw, const TB* bias,
+                  const int64_t* labels, int N, int V, int H, int64_t ignore, int T, float* loss,
+                  float* lse, float* n_valid, bf16* d_hidden, bf16* d_weight, char* ws,
+                  hipStream_t st) {
+  GradWs w;
+  grad_ws_layout(N, V, H, T, d_hidden != nullptr, &w, ws);
+  const int nblk = (int)nblocks(V);
+  const bool grads = d_hidden || d_weight;
+  count_valid_kernel<<<1, 1024, 0, st>>>(labels, N, ignore, n_valid);
+  ML_LAUNCH_CHECK();
+  int rc;
+  for (int t0 = 0; t0 < N; t0 += T) {
+    const int Tc = N - t0 < T ? N - t0 : T;
+    const bf16* hc = hidden + (int64_t)t0 * ldh;
+    const int64_t* lc = labels + t0;
+    {  // 1. logits + (m, s) partials + e
+      Segment seg{{hc, ldh}, {weight, ldw}, H};
+      Problem pb;
+      rc = make_problem<BigCfg>(pb, Tc, V, 1, &seg, kKMajor, kKMajor, 0);
+      if (rc) return rc;
+      if (grads) {
+        EpiRowLse<TB, true> epi{bias, w.pmax, w.psum, w.E, (int64_t)V, Tc, V, nblk};
+        gemm_kernel<BigCfg, kKMajor, kKMajor, EpiRowLse<TB, true>>
+            <<<dim3(grid_blocks(pb)), kThreads, 0, st>>>(pb, epi);
+      } else {
+        EpiRowLse<TB, false> epi{bias, w.pmax, w.psum, nullptr, 0, Tc, V, nblk};
+        gemm_kernel<BigCfg, kKMajor, kKMajor, EpiRowLse<TB, false>>
+            <<<dim3(grid_blocks(pb)), kThreads, 0, st>>>(pb, epi);
+      }
+      ML_LAUNCH_CHECK();
+      label_logit_kernel<TB><<<dim3((Tc + 3) / 4), 256, 0, st>>>(hc, ldh, weight, ldw, bias, lc, Tc,
+                                                                 V, H, w.zy + t0);
+      ML_LAUNCH_CHECK();
+    }
+    // 2. lse and per-token loss terms
+    lse_reduce_kernel<<<dim3((Tc + 3) / 4), 256, 0, st>>>(w.pmax, w.psum, nblk, w.zy + t0, lc,
+                                                          ignore, Tc, V, lse + t0,
+                                                          w.loss_row + t0, w.valid_row + t0);
+    ML_LAUNCH_CHECK();
+    if (!grads) continue;
+    {  // 3. dlogits in place
+      const int64_t vec = (int64_t)Tc * (V / 8);
+      int64_t blocks = (vec + 255) / 256;
+      blocks = blocks < 8192 ? blocks : 8192;
+      dlogit_pass_kernel<<<dim3((unsigned)blocks), 256, 0, st>>>(w.E, V, Tc, V, w.pmax, nblk,
+                                                                 lse + t0, lc, ignore, n_valid);
+      ML_LAUNCH_CHECK();
+    }
+    if (d_hidden) {  // 4. dH_c = D W (split-K over the vocabulary)
+      Segment seg{{w.E, (int64_t)V}, {weight, ldw}, V};
+      Problem pb;
+      rc = make_problem<BigCfg>(pb, Tc, H, 1, &seg, kKMajor, kMNMajor, 0, dh_ksplit(Tc, H, V));
+      if (rc) return rc;
+      ML_CHECK(splitk_ws_bytes(pb) <= w.part_bytes, "flce: dH partial workspace too small");
+      rc = launch_splitk<BigCfg, kKMajor, kMNMajor, bf16>(pb, w.part, d_hidden + (int64_t)t0 * H,
+                                                          H, 1.0f, 0.0f, st);
+      if (rc) return rc;
+    }
+    if (d_weight) {  // 5. dW (+)= D^T H_c
+      Segment seg{{w.E, (int64_t)V}, {hc, ldh}, Tc};
+      Problem pb;
+      rc = make_problem<BigCfg>(pb, V, H, 1, &seg, kMNMajor, kMNMajor, 0);
+      if (rc) return rc;
+      rc = launch_store<bf16>(pb, kMNMajor, kMNMajor, d_weight, H, 1.0f, t0 > 0 ? 1.0f : 0.0f, st);
+      if (rc) return rc;
+    }
+  }
+  loss_mean_kernel<<<1, 1024, 0, st>>>(w.loss_row, w.valid_row, N, loss, n_valid);
   ML_LAUNCH_CHECK();
   return ML_OK;
 }
@@ -437,4 +715,72 @@ extern "C" int ml_flce_bwd(const void* hidden, int64_t ldh, const void* weight, 
                                (int)n_tokens, (int)vocab, (int)H, ignore_index, lse, n_valid,
                                grad_loss, (int)chunk, static_cast<bf16*>(d_hidden),
                                static_cast<bf16*>(d_weight), ws, st);
+}
+
+extern "C" size_t ml_flce_fwd_grad_workspace_bytes(int64_t n_tokens, int64_t vocab,
+                                                   int64_t hidden_size, int64_t token_chunk,
+                                                   int need_dhidden) {
+  if (n_tokens <= 0 || vocab <= 0 || hidden_size <= 0 || token_chunk <= 0) return 0;
+  const int64_t T = token_chunk < n_tokens ? token_chunk : n_tokens;
+  return flce::grad_ws_layout(n_tokens, vocab, hidden_size, T, need_dhidden != 0, nullptr, nullptr);
+}
+
+extern "C" int ml_flce_fwd_grad(const void* hidden, int64_t ldh, const void* weight, int64_t ldw,
+                                const void* bias, int bias_dtype, const int64_t* labels,
+                                int64_t n_tokens, int64_t vocab, int64_t hidden_size,
+                                int64_t ignore_index, int64_t token_chunk, float* loss, float* lse,
+                                float* n_valid, void* d_hidden, void* d_weight, void* workspace,
+                                size_t workspace_bytes, void* stream) {
+  int rc = flce::check_common(hidden, ldh, weight, ldw, labels, n_tokens, vocab, hidden_size,
+                              bias_dtype);
+  if (rc) return rc;
+  ML_CHECK(loss && n_valid && (n_tokens == 0 || lse), "flce: null output pointer");
+  ML_CHECK(token_chunk > 0 && token_chunk < (1LL << 31), "flce: token_chunk must be positive");
+  hipStream_t st = (hipStream_t)stream;
+  const int64_t H = hidden_size;
+  if (n_tokens == 0) {
+    flce::empty_loss_kernel<<<1, 1, 0, st>>>(loss, n_valid);
+    ML_LAUNCH_CHECK();
+    if (d_weight) {
+      flce::zero_bf16_kernel<<<1024, 256, 0, st>>>(static_cast<bf16*>(d_weight), vocab * H);
+      ML_LAUNCH_CHECK();
+    }
+    return ML_OK;
+  }
+  const int64_t T = token_chunk < n_tokens ? token_chunk : n_tokens;
+  ML_CHECK(T * vocab < (1LL << 40), "flce: token_chunk * vocab too large");
+  const size_t need = ml_flce_fwd_grad_workspace_bytes(n_tokens, vocab, H, T, d_hidden != nullptr);
+  ML_CHECK(workspace && workspace_bytes >= need, "flce: workspace too small (%zu < %zu bytes)",
+           workspace_bytes, need);
+  const bf16* h = static_cast<const bf16*>(hidden);
+  const bf16* w = static_cast<const bf16*>(weight);
+  char* ws = static_cast<char*>(workspace);
+  if (bias_dtype == ML_BF16)
+    return flce::fwd_grad_impl<bf16>(h, ldh, w, ldw, static_cast<const bf16*>(bias), labels,
+                                     (int)n_tokens, (int)vocab, (int)H, ignore_index, (int)T, loss,
+                                     lse, n_valid, static_cast<bf16*>(d_hidden),
+                                     static_cast<bf16*>(d_weight), ws, st);
+  return flce::fwd_grad_impl<float>(h, ldh, w, ldw, static_cast<const float*>(bias), labels,
+                                    (int)n_tokens, (int)vocab, (int)H, ignore_index, (int)T, loss,
+                                    lse, n_valid, static_cast<bf16*>(d_hidden),
+                                    static_cast<bf16*>(d_weight), ws, st);
+}
+
+extern "C" int ml_flce_scale_grads(const float* grad_loss, void* d_hidden, int64_t n_hidden,
+                                   void* d_weight, int64_t n_weight, void* stream) {
+  ML_CHECK(grad_loss, "flce: null grad_loss");
+  ML_CHECK(n_hidden >= 0 && n_weight >= 0, "flce: negative sizes");
+  ML_CHECK((n_hidden == 0 || d_hidden) && (n_weight == 0 || d_weight), "flce: null gradient");
+  hipStream_t st = (hipStream_t)stream;
+  void* ptrs[2] = {d_hidden, d_weight};
+  const int64_t ns[2] = {n_hidden, n_weight};
+  for (int i = 0; i < 2; ++i) {
+    if (ns[i] == 0) continue;
+    int64_t blocks = (ns[i] / 8 + 255) / 256;
+    blocks = blocks < 4096 ? (blocks > 0 ? blocks : 1) : 4096;
+    flce::scale_bf16_kernel<<<dim3((unsigned)blocks), 256, 0, st>>>(static_cast<bf16*>(ptrs[i]),
+                                                                    ns[i], grad_loss);
+    ML_LAUNCH_CHECK();
+  }
+  return ML_OK;
 }

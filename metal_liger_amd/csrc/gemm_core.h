@@ -35,6 +35,7 @@
 //   so concurrently running tiles of one XCD share operands in its L2.
 #pragma once
 
+#include <type_traits>
 #include <utility>
 
 #include "common.h"
@@ -984,11 +985,88 @@ __device__ __forceinline__ void for_each_acc(AccT (&acc)[TM][TN], int m0, int n0
   for (int i = 0; i < TM; ++i) for_each_acc_row(acc, i, m0, n0, lane, f);
 }
 
+// ------------------------------------------------ staged bf16 epilogues --
+// Global stores of single bf16 elements (the accumulator layout gives a lane
+// one column of 4 consecutive rows) use a 64-lane instruction for 128 bytes
+// in 2-byte pieces. Instead, a wave stages its 128 x 128 results, rounded to
+// bf16, in 32 KB of LDS of its own and takes them back as rows of 8
+// consecutive columns, one 16-byte vector per lane:
+//   phase 1: lane (G = lane / 16, c = lane % 16) writes rows 4 G .. 4 G + 3 of
+//            column c of each 16 x 16 block as one 8-byte ds_write_b64; the
+//            blocks are stored column-major ([16 columns][16 rows]).
+//   phase 2: two ds_read_b64_tr_b16 per 16-lane group read columns cb .. cb + 3
+//            and cb + 4 .. cb + 7 (cb = 0 or 8) of a block: lane 4 a + b
+//            addresses column cb + a, rows 4 b .. 4 b + 3, so lane i receives
+//            row i at 4 consecutive columns. Lanes 32-63 take the next block.
+// val(i, j, v) gives the value of accumulator element (i, j, v); row(m, n, x)
+// receives x[0..7] = columns n .. n + 7 of row m (n a multiple of 8).
+typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+
+template <class Val, class Row>
+__device__ __forceinline__ void stage_rows_bf16(char* lds, int lane, int m0, int n0, Val&& val,
+                                                Row&& row) {
+  const int G = lane >> 4, c = lane & 15;
+  char* wr = lds + (c * 16 + 4 * G) * 2;
+#pragma unroll
+  for (int i = 0; i < big::TM; ++i)
+#pragma unroll
+    for (int j = 0; j < big::TN; ++j) {
+      bf16x4_t w;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) w[v] = static_cast<bf16>(val(i, j, v));
+      *reinterpret_cast<bf16x4_t*>(wr + (i * big::TN + j) * 512) = w;
+    }
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's writes are in LDS
+  __builtin_amdgcn_wave_barrier();
+  typedef __attribute__((address_space(3))) i16x4_t* lp;
+  const int L = lane & 15, a = L >> 2, b = L & 3;
+  const int cb = 8 * ((lane >> 4) & 1);
+  const int jo = lane >> 5;
+  const char* rd = lds + jo * 512 + ((cb + a) * 16 + 4 * b) * 2;
+#pragma unroll
+  for (int i = 0; i < big::TM; ++i)
+#pragma unroll
+    for (int jp = 0; jp < big::TN / 2; ++jp) {
+      const char* blk = rd + (i * big::TN + 2 * jp) * 512;
+      const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lp)(blk));
+      const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lp)(blk + 4 * 32));
+      float x[8];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        x[e] = __builtin_bit_cast(float, (uint32_t)(uint16_t)lo[e] << 16);
+        x[4 + e] = __builtin_bit_cast(float, (uint32_t)(uint16_t)hi[e] << 16);
+      }
+      row(m0 + 16 * i + L, n0 + 16 * (2 * jp + jo) + cb, x);
+    }
+}
+
+// Stores x[0..7] at p[0..7] as bf16 (one 16-byte store when all 8 columns are
+// inside [.., N), element by element otherwise).
+__device__ __forceinline__ void store_row8_bf16(bf16* p, int n, int N, const float (&x)[8]) {
+  if (n + 8 <= N) {
+    store_n<bf16, 8>(p, x);
+  } else {
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+      if (n + k < N) p[k] = from_f32<bf16>(x[k]);
+  }
+}
+
+__device__ __forceinline__ void load_row8_bf16(const bf16* p, int n, int N, float (&x)[8]) {
+  if (n + 8 <= N) {
+    load_n<bf16, 8>(p, x);
+  } else {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) x[k] = n + k < N ? to_f32(p[k]) : 0.f;
+  }
+}
+
 // The GEMM kernel: mainloop + epilogue functor
 //   epi(acc, m_base, n_base, lane, smem, split) with m_base / n_base the
 //   origin of this wave's sub-tile and acc in the path's MFMA layout
 //   (f32x4_t[8][8] for the 256 x 256 tile, f32x16_t[TM][TN] otherwise).
-//   smem may be reused by the epilogue.
+//   smem: LDS the epilogue may use - for the 256 x 256 tile, 32 KB private
+//   to the wave (staged bf16 epilogues); otherwise the block's stage 0.
 template <class C, int LA, int LB, class Epi>
 __global__ __launch_bounds__(kThreads) void gemm_kernel(const Problem pb, const Epi epi) {
   int tm, tn, split;
@@ -1003,7 +1081,10 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(const Problem pb, const 
     char* const st[big::STAGES] = {s0, s1, s2, s3};
     f32x4_t acc[big::TM][big::TN];
     big_mainloop<LA, LB>(pb, tm, tn, split, st, acc);
-    epi(acc, tm * 256 + (wave >> 1) * big::WM, tn * 256 + (wave & 1) * big::WN, tid & 63, s0,
+    // each wave gets one stage (32 KB) of LDS for its epilogue
+    const int w = __builtin_amdgcn_readfirstlane(wave);
+    char* wl = w == 0 ? s0 : w == 1 ? s1 : w == 2 ? s2 : s3;
+    epi(acc, tm * 256 + (wave >> 1) * big::WM, tn * 256 + (wave & 1) * big::WN, tid & 63, wl,
         split);
   } else {
     __shared__ __attribute__((aligned(16))) char stage0[C::STAGE_BYTES];
@@ -1027,9 +1108,41 @@ struct EpiStore {
   int M, N;
   float alpha, beta;
 
+  // 256 x 256 tile, bf16 C: staged through LDS, 16-byte accesses (with beta,
+  // alpha * acc is rounded to bf16 before beta * C is added).
+  __device__ __forceinline__ void operator()(f32x4_t (&acc)[big::TM][big::TN], int m0, int n0,
+                                             int lane, char* lds, int) const {
+    if constexpr (std::is_same_v<TC, bf16>) {
+      stage_rows_bf16(
+          lds, lane, m0, n0, [&](int i, int j, int v) { return alpha * acc[i][j][v]; },
+          [&](int m, int n, const float (&x)[8]) {
+            if (m >= M || n >= N) return;
+            bf16* p = C + (int64_t)m * ldc + n;
+            float y[8];
+            if (beta != 0.f) {
+              float o[8];
+              load_row8_bf16(p, n, N, o);
+#pragma unroll
+              for (int k = 0; k < 8; ++k) y[k] = x[k] + beta * o[k];
+            } else {
+#pragma unroll
+              for (int k = 0; k < 8; ++k) y[k] = x[k];
+            }
+            store_row8_bf16(p, n, N, y);
+          });
+    } else {
+      generic(acc, m0, n0, lane);
+    }
+  }
+
+  template <int TM, int TN>
+  __device__ __forceinline__ void operator()(f32x16_t (&acc)[TM][TN], int m0, int n0, int lane,
+                                             char*, int) const {
+    generic(acc, m0, n0, lane);
+  }
+
   template <typename AccT, int TM, int TN>
-  __device__ __forceinline__ void operator()(AccT (&acc)[TM][TN], int m0, int n0, int lane, char*,
-                                             int) const {
+  __device__ __forceinline__ void generic(AccT (&acc)[TM][TN], int m0, int n0, int lane) const {
     if (beta == 0.f) {
       for_each_acc(acc, m0, n0, lane, [&](int m, int n, float v) {
         if (m < M && n < N) C[(int64_t)m * ldc + n] = from_f32<TC>(alpha * v);

@@ -65,9 +65,12 @@ __device__ __forceinline__ float sigmoid_f(float x) {
   return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-x * 1.4426950408889634f));
 }
 
-// dH (fp32 accumulators) -> SwiGLU backward with the saved gate / up
-// (ops/fused_lora.py:235-244): d_gate = ((dH up) s) (1 + g (1 - s)),
-// d_up = dH (g s), s = sigmoid(g); bf16 outputs.
+// dH -> SwiGLU backward with the saved gate / up (ops/fused_lora.py:235-244):
+// d_gate = ((dH up) s) (1 + g (1 - s)), d_up = dH (g s), s = sigmoid(g),
+// in fp32 from dH rounded to bf16 (the reference's dH is a bf16 matmul
+// output); bf16 outputs. On the 256 x 256 tile dH goes through the staged
+// epilogue, so gate / up are read and d_gate / d_up written as 16-byte
+// vectors.
 struct EpiSwigluBwd {
   const bf16* gate;
   const bf16* up;
@@ -76,12 +79,36 @@ struct EpiSwigluBwd {
   int64_t ld;
   int M, N;
 
-  template <typename AccT, int TM, int TN>
-  __device__ __forceinline__ void operator()(AccT (&acc)[TM][TN], int m0, int n0, int lane, char*,
-                                             int) const {
-    for_each_acc(acc, m0, n0, lane, [&](int m, int n, float dh) {
+  __device__ __forceinline__ void row8(int m, int n, const float (&dh)[8]) const {
+    if (m >= M || n >= N) return;
+    const int64_t o = (int64_t)m * ld + n;
+    float g[8], u[8], dg[8], du[8];
+    load_row8_bf16(gate + o, n, N, g);
+    load_row8_bf16(up + o, n, N, u);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const float s = sigmoid_f(g[k]);
+      dg[k] = ((dh[k] * u[k]) * s) * (1.0f + g[k] * (1.0f - s));
+      du[k] = dh[k] * (g[k] * s);
+    }
+    store_row8_bf16(dgate + o, n, N, dg);
+    store_row8_bf16(dup + o, n, N, du);
+  }
+
+  __device__ __forceinline__ void operator()(f32x4_t (&acc)[big::TM][big::TN], int m0, int n0,
+                                             int lane, char* lds, int) const {
+    stage_rows_bf16(
+        lds, lane, m0, n0, [&](int i, int j, int v) { return acc[i][j][v]; },
+        [&](int m, int n, const float (&x)[8]) { row8(m, n, x); });
+  }
+
+  template <int TM, int TN>
+  __device__ __forceinline__ void operator()(f32x16_t (&acc)[TM][TN], int m0, int n0, int lane,
+                                             char*, int) const {
+    for_each_acc(acc, m0, n0, lane, [&](int m, int n, float v) {
       if (m >= M || n >= N) return;
       const int64_t o = (int64_t)m * ld + n;
+      const float dh = to_f32(from_f32<bf16>(v));
       const float g = to_f32(gate[o]);
       const float u = to_f32(up[o]);
       const float s = sigmoid_f(g);

@@ -367,6 +367,61 @@ def flce_fwd(hidden, weight, labels, bias=None, ignore_index: int = -100):
     return loss, lse, n_valid
 
 
+# Bytes of the [token_chunk, vocab] bf16 buffer the one-pass schedule holds.
+FLCE_CHUNK_BYTES = 640 << 20
+
+
+def flce_token_chunk(n_tokens: int, vocab: int) -> int:
+    """Tokens per chunk of ml_flce_fwd_grad: all of them when the [tokens,
+    vocab] bf16 buffer fits FLCE_CHUNK_BYTES, else the largest multiple of
+    256 that does (at least 256)."""
+    if n_tokens * vocab * 2 <= FLCE_CHUNK_BYTES:
+        return max(n_tokens, 1)
+    return max(256, (FLCE_CHUNK_BYTES // (vocab * 2)) // 256 * 256)
+
+
+def flce_fwd_grad(hidden, weight, labels, bias=None, ignore_index: int = -100,
+                  need_dhidden: bool = True, need_dweight: bool = True,
+                  token_chunk: int | None = None):
+    """Loss and gradients in one pass (logits computed once).
+
+    Returns (loss 0-d fp32, lse [N] fp32, n_valid [1] fp32, d_hidden bf16 or
+    None, d_weight bf16 or None); the gradients are for d(loss) = 1.
+    """
+    hidden, weight, labels, bias = _flce_operands(hidden, weight, labels, bias)
+    N, H = hidden.shape
+    V = weight.shape[0]
+    dev = hidden.device
+    loss = torch.empty((), dtype=torch.float32, device=dev)
+    lse = torch.empty(N, dtype=torch.float32, device=dev)
+    n_valid = torch.empty(1, dtype=torch.float32, device=dev)
+    dh = torch.empty(N, H, dtype=torch.bfloat16, device=dev) if need_dhidden else None
+    dw = torch.empty(V, H, dtype=torch.bfloat16, device=dev) if need_dweight else None
+    T = int(token_chunk) if token_chunk else flce_token_chunk(N, V)
+    wsb = _hip.query("ml_flce_fwd_grad_workspace_bytes", N, V, H, T, 1 if need_dhidden else 0)
+    ws = torch.empty(max(wsb, 16), dtype=torch.uint8, device=dev)
+    call(
+        "ml_flce_fwd_grad", ptr(hidden), hidden.stride(0) if N > 0 else H, ptr(weight),
+        weight.stride(0), ptr(bias), dtype_tag(bias, "bias") if bias is not None else 0, ptr(labels),
+        N, V, H, int(ignore_index), T, ptr(loss), ptr(lse), ptr(n_valid), ptr(dh), ptr(dw), ptr(ws),
+        ws.numel(), stream_of(weight),
+    )
+    return loss, lse, n_valid, dh, dw
+
+
+def flce_scale_grads(grad_loss, d_hidden, d_weight):
+    """d_hidden *= grad_loss, d_weight *= grad_loss in place (bf16; no-op
+    on the device when grad_loss == 1)."""
+    t = d_hidden if d_hidden is not None else d_weight
+    if t is None:
+        return
+    g = grad_loss.detach().to(device=t.device, dtype=torch.float32).reshape(1).contiguous()
+    call(
+        "ml_flce_scale_grads", ptr(g), ptr(d_hidden), d_hidden.numel() if d_hidden is not None else 0,
+        ptr(d_weight), d_weight.numel() if d_weight is not None else 0, stream_of(t),
+    )
+
+
 def flce_bwd(hidden, weight, labels, bias, ignore_index, lse, n_valid, grad_loss, chunk_size,
              need_dhidden=True, need_dweight=True):
     """Returns (d_hidden bf16 or None, d_weight bf16 or None)."""
