@@ -148,8 +148,11 @@ struct EpiRowLse {
     if constexpr (STORE) {
       stage_rows_bf16(
           lds, lane, m0, n0, [&](int i, int j, int v) { return acc[i][j][v]; },
-          [&](int m, int n, const float (&x)[8]) {
-            if (m < M && n < V) store_row8_bf16(E + (int64_t)m * ldE + n, n, V, x);
+          [&](const int (&m)[kStageBatch], const int (&n)[kStageBatch],
+              const float (&x)[kStageBatch][8]) {
+#pragma unroll
+            for (int q = 0; q < kStageBatch; ++q)
+              if (m[q] < M && n[q] < V) store_row8_bf16(E + (int64_t)m[q] * ldE + n[q], n[q], V, x[q]);
           });
     }
   }
@@ -352,8 +355,11 @@ struct EpiDlogit {
     }
     stage_rows_bf16(
         lds, lane, m0, n0, [&](int i, int j, int v) { return acc[i][j][v]; },
-        [&](int m, int n, const float (&x)[8]) {
-          if (m < M && n < C) store_row8_bf16(D + (int64_t)m * ldd + n, n, C, x);
+        [&](const int (&m)[kStageBatch], const int (&n)[kStageBatch],
+            const float (&x)[kStageBatch][8]) {
+#pragma unroll
+          for (int q = 0; q < kStageBatch; ++q)
+            if (m[q] < M && n[q] < C) store_row8_bf16(D + (int64_t)m[q] * ldd + n[q], n[q], C, x[q]);
         });
   }
 };

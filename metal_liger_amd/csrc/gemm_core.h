@@ -998,13 +998,17 @@ __device__ __forceinline__ void for_each_acc(AccT (&acc)[TM][TN], int m0, int n0
 //            and cb + 4 .. cb + 7 (cb = 0 or 8) of a block: lane 4 a + b
 //            addresses column cb + a, rows 4 b .. 4 b + 3, so lane i receives
 //            row i at 4 consecutive columns. Lanes 32-63 take the next block.
-// val(i, j, v) gives the value of accumulator element (i, j, v); row(m, n, x)
-// receives x[0..7] = columns n .. n + 7 of row m (n a multiple of 8).
+// val(i, j, v) gives the value of accumulator element (i, j, v). The 32
+// row vectors of a lane go to rows(m, n, x) in batches of kStageBatch:
+// x[q][0..7] = columns n[q] .. n[q] + 7 of row m[q] (n[q] a multiple of 8),
+// so a functor that reads global memory can issue all of a batch's loads
+// before its first store.
 typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+constexpr int kStageBatch = 8;
 
-template <class Val, class Row>
+template <class Val, class Rows>
 __device__ __forceinline__ void stage_rows_bf16(char* lds, int lane, int m0, int n0, Val&& val,
-                                                Row&& row) {
+                                                Rows&& rows) {
   const int G = lane >> 4, c = lane & 15;
   char* wr = lds + (c * 16 + 4 * G) * 2;
 #pragma unroll
@@ -1023,21 +1027,28 @@ __device__ __forceinline__ void stage_rows_bf16(char* lds, int lane, int m0, int
   const int cb = 8 * ((lane >> 4) & 1);
   const int jo = lane >> 5;
   const char* rd = lds + jo * 512 + ((cb + a) * 16 + 4 * b) * 2;
+  constexpr int kVecs = big::TM * big::TN / 2;  // 32 row vectors per lane
+  static_assert(kVecs % kStageBatch == 0, "whole batches");
 #pragma unroll
-  for (int i = 0; i < big::TM; ++i)
+  for (int q0 = 0; q0 < kVecs; q0 += kStageBatch) {
+    int m[kStageBatch], n[kStageBatch];
+    float x[kStageBatch][8];
 #pragma unroll
-    for (int jp = 0; jp < big::TN / 2; ++jp) {
+    for (int q = 0; q < kStageBatch; ++q) {
+      const int i = (q0 + q) / (big::TN / 2), jp = (q0 + q) % (big::TN / 2);
       const char* blk = rd + (i * big::TN + 2 * jp) * 512;
       const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lp)(blk));
       const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lp)(blk + 4 * 32));
-      float x[8];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        x[e] = __builtin_bit_cast(float, (uint32_t)(uint16_t)lo[e] << 16);
-        x[4 + e] = __builtin_bit_cast(float, (uint32_t)(uint16_t)hi[e] << 16);
+        x[q][e] = __builtin_bit_cast(float, (uint32_t)(uint16_t)lo[e] << 16);
+        x[q][4 + e] = __builtin_bit_cast(float, (uint32_t)(uint16_t)hi[e] << 16);
       }
-      row(m0 + 16 * i + L, n0 + 16 * (2 * jp + jo) + cb, x);
+      m[q] = m0 + 16 * i + L;
+      n[q] = n0 + 16 * (2 * jp + jo) + cb;
     }
+    rows(m, n, x);
+  }
 }
 
 // Stores x[0..7] at p[0..7] as bf16 (one 16-byte store when all 8 columns are
@@ -1115,20 +1126,24 @@ struct EpiStore {
     if constexpr (std::is_same_v<TC, bf16>) {
       stage_rows_bf16(
           lds, lane, m0, n0, [&](int i, int j, int v) { return alpha * acc[i][j][v]; },
-          [&](int m, int n, const float (&x)[8]) {
-            if (m >= M || n >= N) return;
-            bf16* p = C + (int64_t)m * ldc + n;
-            float y[8];
+          [&](const int (&m)[kStageBatch], const int (&n)[kStageBatch],
+              const float (&x)[kStageBatch][8]) {
+            float o[kStageBatch][8];
             if (beta != 0.f) {
-              float o[8];
-              load_row8_bf16(p, n, N, o);
 #pragma unroll
-              for (int k = 0; k < 8; ++k) y[k] = x[k] + beta * o[k];
-            } else {
-#pragma unroll
-              for (int k = 0; k < 8; ++k) y[k] = x[k];
+              for (int q = 0; q < kStageBatch; ++q) {
+                if (m[q] < M && n[q] < N)
+                  load_row8_bf16(C + (int64_t)m[q] * ldc + n[q], n[q], N, o[q]);
+              }
             }
-            store_row8_bf16(p, n, N, y);
+#pragma unroll
+            for (int q = 0; q < kStageBatch; ++q) {
+              if (m[q] >= M || n[q] >= N) continue;
+              float y[8];
+#pragma unroll
+              for (int k = 0; k < 8; ++k) y[k] = beta != 0.f ? x[q][k] + beta * o[q][k] : x[q][k];
+              store_row8_bf16(C + (int64_t)m[q] * ldc + n[q], n[q], N, y);
+            }
           });
     } else {
       generic(acc, m0, n0, lane);
@@ -1181,13 +1196,48 @@ struct EpiPartial {
   }
 };
 
-// out[m, n] = alpha * sum_s P[s][m][n] + beta * out[m, n]  (fixed order)
+// out[m, n] = alpha * sum_s P[s][m][n] + beta * out[m, n]  (fixed order).
+// Four consecutive elements per thread when N % 4 == 0 (16-byte partial
+// loads, the splits unrolled so several loads are in flight), one otherwise.
 template <typename TC>
 __global__ __launch_bounds__(256) void reduce_partials_kernel(const float* __restrict__ P,
                                                               int ksplit, int M, int N,
                                                               TC* __restrict__ out, int64_t ldo,
                                                               float alpha, float beta) {
   const int64_t total = (int64_t)M * N;
+  if (N % 4 == 0) {
+    const int64_t nv = total / 4;
+    for (int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x; q < nv;
+         q += (int64_t)gridDim.x * 256) {
+      const int64_t e = q * 4;
+      float s[4] = {0.f, 0.f, 0.f, 0.f};
+      int k = 0;
+      for (; k + 4 <= ksplit; k += 4) {
+        float v[4][4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) load_n<float, 4>(P + (int64_t)(k + u) * total + e, v[u]);
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+          for (int c = 0; c < 4; ++c) s[c] += v[u][c];
+      }
+      for (; k < ksplit; ++k) {
+        float v[4];
+        load_n<float, 4>(P + (int64_t)k * total + e, v);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) s[c] += v[c];
+      }
+      const int64_t m = e / N, n = e - m * N;
+      TC* p = out + m * ldo + n;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        float r = alpha * s[c];
+        if (beta != 0.f) r += beta * to_f32(p[c]);
+        p[c] = from_f32<TC>(r);
+      }
+    }
+    return;
+  }
   for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < total;
        e += (int64_t)gridDim.x * 256) {
     float s = 0.f;
@@ -1286,8 +1336,9 @@ inline int launch_splitk(const Problem& pb, float* ws, TC* out, int64_t ldo, flo
   gemm_kernel<C, LA, LB, EpiPartial><<<dim3(grid_blocks(pb)), kThreads, 0, st>>>(pb, epi);
   ML_LAUNCH_CHECK();
   const int64_t total = (int64_t)pb.M * pb.N;
-  int64_t blocks = (total + 255) / 256;
-  blocks = blocks < 2048 ? blocks : 2048;
+  const int64_t per_thread = pb.N % 4 == 0 ? 4 : 1;
+  int64_t blocks = (total / per_thread + 255) / 256;
+  blocks = blocks < 2048 ? (blocks > 0 ? blocks : 1) : 2048;
   reduce_partials_kernel<TC><<<dim3((unsigned)blocks), 256, 0, st>>>(ws, pb.ksplit, pb.M, pb.N,
                                                                      out, ldo, alpha, beta);
   ML_LAUNCH_CHECK();

@@ -79,27 +79,37 @@ struct EpiSwigluBwd {
   int64_t ld;
   int M, N;
 
-  __device__ __forceinline__ void row8(int m, int n, const float (&dh)[8]) const {
-    if (m >= M || n >= N) return;
-    const int64_t o = (int64_t)m * ld + n;
-    float g[8], u[8], dg[8], du[8];
-    load_row8_bf16(gate + o, n, N, g);
-    load_row8_bf16(up + o, n, N, u);
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const float s = sigmoid_f(g[k]);
-      dg[k] = ((dh[k] * u[k]) * s) * (1.0f + g[k] * (1.0f - s));
-      du[k] = dh[k] * (g[k] * s);
-    }
-    store_row8_bf16(dgate + o, n, N, dg);
-    store_row8_bf16(dup + o, n, N, du);
-  }
-
   __device__ __forceinline__ void operator()(f32x4_t (&acc)[big::TM][big::TN], int m0, int n0,
                                              int lane, char* lds, int) const {
     stage_rows_bf16(
         lds, lane, m0, n0, [&](int i, int j, int v) { return acc[i][j][v]; },
-        [&](int m, int n, const float (&x)[8]) { row8(m, n, x); });
+        [&](const int (&m)[kStageBatch], const int (&n)[kStageBatch],
+            const float (&dh)[kStageBatch][8]) {
+          // every gate / up load of the batch before the first store
+          float g[kStageBatch][8], u[kStageBatch][8];
+#pragma unroll
+          for (int q = 0; q < kStageBatch; ++q) {
+            if (m[q] < M && n[q] < N) {
+              const int64_t o = (int64_t)m[q] * ld + n[q];
+              load_row8_bf16(gate + o, n[q], N, g[q]);
+              load_row8_bf16(up + o, n[q], N, u[q]);
+            }
+          }
+#pragma unroll
+          for (int q = 0; q < kStageBatch; ++q) {
+            if (m[q] >= M || n[q] >= N) continue;
+            float dg[8], du[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+              const float s = sigmoid_f(g[q][k]);
+              dg[k] = ((dh[q][k] * u[q][k]) * s) * (1.0f + g[q][k] * (1.0f - s));
+              du[k] = dh[q][k] * (g[q][k] * s);
+            }
+            const int64_t o = (int64_t)m[q] * ld + n[q];
+            store_row8_bf16(dgate + o, n[q], N, dg);
+            store_row8_bf16(dup + o, n[q], N, du);
+          }
+        });
   }
 
   template <int TM, int TN>

@@ -24,7 +24,7 @@ namespace {
 
 constexpr int kFwdWaves = 4;        // rows per forward block (one wave per row)
 constexpr int kBwdWaves = 8;        // waves per backward block
-constexpr int kMaxBwdBlocks = 512;  // dW partial rows
+constexpr int kMaxBwdBlocks = 256;  // dW partial rows (one 8-wave block per CU)
 constexpr int kGenericThreads = 256;
 
 // Column of chunk `it` for `lane`, clamped to the last valid chunk of the row.
@@ -279,7 +279,53 @@ __global__ __launch_bounds__(kGenericThreads) void rms_bwd_generic(
   }
 }
 
-// Sums G partial rows in fixed order: 32 columns x 8 row slices per block.
+// Sums G partial rows in a fixed order.
+// Vector form (cols % 4 == 0): a block covers 16 columns as 4 vectors of 4
+// floats x 64 row slices; thread (slice r, vector cv) sums rows r, r + 64,
+// ... with 16-byte loads (unrolled, so several are in flight), then the 64
+// slices are added in a fixed binary tree through LDS.
+// Scalar form (any cols): 32 columns x 8 row slices per block.
+constexpr int kRedVec = 4;      // column vectors per block (vector form)
+constexpr int kRedSlices = 64;  // row slices per block (vector form)
+
+template <typename TW>
+__global__ __launch_bounds__(256) void rms_dw_reduce_vec(const float* __restrict__ partial, int G,
+                                                          int64_t cols, TW* __restrict__ dw) {
+  __shared__ float sm[kRedSlices][kRedVec * 4 + 1];
+  const int cv = threadIdx.x % kRedVec;
+  const int r = threadIdx.x / kRedVec;
+  const int64_t c = ((int64_t)blockIdx.x * kRedVec + cv) * 4;
+  float s[4] = {0.f, 0.f, 0.f, 0.f};
+  if (c < cols) {
+    int g = r;
+#pragma unroll 4
+    for (; g < G; g += kRedSlices) {
+      float v[4];
+      load_n<float, 4>(partial + (int64_t)g * cols + c, v);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) s[e] += v[e];
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 4; ++e) sm[r][cv * 4 + e] = s[e];
+  __syncthreads();
+#pragma unroll
+  for (int half = kRedSlices / 2; half >= 1; half >>= 1) {
+    if (r < half) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) sm[r][cv * 4 + e] += sm[r + half][cv * 4 + e];
+    }
+    __syncthreads();
+  }
+  if (r == 0 && c < cols) {
+    float o[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[e] = sm[0][cv * 4 + e];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) dw[c + e] = from_f32<TW>(o[e]);
+  }
+}
+
 template <typename TW>
 __global__ __launch_bounds__(256) void rms_dw_reduce(const float* __restrict__ partial, int G,
                                                       int64_t cols, TW* __restrict__ dw) {
@@ -411,7 +457,12 @@ int launch_bwd(const void* x, int64_t ldx, const void* w, const void* dy, int64_
     ML_LAUNCH_CHECK();
   }
   if (cols > 0) {
-    rms_dw_reduce<TW><<<dim3((unsigned)((cols + 31) / 32)), 256, 0, st>>>(part, (int)G, cols, dwp);
+    if (cols % 4 == 0)
+      rms_dw_reduce_vec<TW><<<dim3((unsigned)((cols + 4 * kRedVec - 1) / (4 * kRedVec))), 256, 0,
+                              st>>>(part, (int)G, cols, dwp);
+    else
+      rms_dw_reduce<TW><<<dim3((unsigned)((cols + 31) / 32)), 256, 0, st>>>(part, (int)G, cols,
+                                                                             dwp);
     ML_LAUNCH_CHECK();
   }
   return ML_OK;
