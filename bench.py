@@ -18,15 +18,19 @@ on a bounded sample of the same workload, on the host's cores.
 breakdown: each op's average launch time; plus, outside the step, chunked
 FLCE fwd+bwd (hidden [8192, 2048], lm_head [151936, 2048], chunk 8192:
 15.29 TFLOP) and the fused LoRA backward of a Qwen3-style 2B layer (QKV +
-MLP, rank 16: 774.2 GFLOP), as TFLOP/s against the 2.5 PFLOP/s bf16 peak.
+MLP, rank 16: 774.2 GFLOP), as TFLOP/s against the 2.5 PFLOP/s bf16 peak;
+and the 4-layer Qwen3-style LoRA train step (batch 4 x 2048 tokens, every
+fused op patched in, FLCE loss, AdamW on the adapters) in tokens/s.
 
-Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline] [--no-mfma-ops] [--pmc-probe]
+Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline] [--no-mfma-ops] [--no-train-step]
+       [--train-step-only] [--pmc-probe]
 """
 
 from __future__ import annotations
 
 import argparse
 import json
+import math
 import os
 import sys
 import time
@@ -185,6 +189,104 @@ def bench_lora_bwd(dev, stream, reps):
             "tokens_per_s": round(N / (tot * 1e-3), 1)}
 
 
+TRAIN_LAYERS, TRAIN_B, TRAIN_S, TRAIN_V = 4, 4, 2048, 151936
+
+
+def build_train_model(dev, layers=TRAIN_LAYERS):
+    """Qwen3-style decoder (hidden 2048, 16 q / 8 kv heads, head_dim 128, MLP
+    6144, eps 1e-6, theta 1e6, vocab 151936, tied embeddings, HF's random
+    init) with rank-16 alpha-32 LoRA on q, k, v, o, gate, up, down in PEFT's
+    layout, bf16, every fused op patched in. Only the adapters train."""
+    import torch
+    from transformers import Qwen3Config, Qwen3ForCausalLM
+
+    from metal_liger_amd import apply_metal_liger_to_qwen3vl
+    from tests.peft_shim import LoraLinear, init_lora, wrap_lora
+    from tests.qwen_tiny import PeftLike
+    cfg = Qwen3Config(vocab_size=TRAIN_V, hidden_size=LORA_H, intermediate_size=LORA_I,
+                      num_hidden_layers=layers, num_attention_heads=16, num_key_value_heads=8,
+                      head_dim=128, rms_norm_eps=1e-6, rope_theta=THETA,
+                      max_position_embeddings=TRAIN_S, tie_word_embeddings=True)
+    cfg._attn_implementation = "sdpa"
+    torch.manual_seed(0)
+    with torch.device(dev):
+        lm = Qwen3ForCausalLM(cfg)
+    for i, layer in enumerate(lm.model.layers):
+        wrap_lora(layer.self_attn, ["q_proj", "k_proj", "v_proj", "o_proj"], r=LORA_R, alpha=32)
+        wrap_lora(layer.mlp, ["gate_proj", "up_proj", "down_proj"], r=LORA_R, alpha=32)
+        for j, m in enumerate(list(layer.self_attn.children()) + list(layer.mlp.children())):
+            if isinstance(m, LoraLinear):
+                init_lora(m, 10 * i + j)
+    lm.to(device=dev, dtype=torch.bfloat16)
+    # the patcher wraps norm weights in new (trainable) Parameters, as the
+    # reference's MetalLigerRMSNorm does: freeze after patching
+    model = apply_metal_liger_to_qwen3vl(PeftLike(lm))
+    for n, p in model.named_parameters():
+        p.requires_grad_("lora_" in n)
+    return model
+
+
+def bench_train_step(dev, steps=5, warmup=2):
+    """4-layer Qwen3-style LoRA train step: token ids [4, 2048] uniform in
+    [0, 151936), forward through the patched decoder (fused RMSNorm, SwiGLU,
+    LoRA QKV / MLP, RoPE from the rotary module's tables), next-token loss by
+    the chunked fused linear cross-entropy (labels shifted left, the last
+    position of each sequence ignored), backward, AdamW on the adapters.
+    Attention is torch's scaled_dot_product_attention restricted to its
+    flash / memory-efficient kernels (an unavailable kernel raises instead of
+    falling back to the batched-matmul path). tokens/s = 8192 / step time."""
+    import torch
+    import transformers.models.qwen3.modeling_qwen3 as mq
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+
+    from metal_liger_amd import MetalLigerFusedLinearCrossEntropy
+    from metal_liger_amd.ops.fused_rope import apply_fused_rotary
+    model = build_train_model(dev)
+    lm = model.base_model.model
+    loss_fn = MetalLigerFusedLinearCrossEntropy(lm.lm_head)
+    params = [p for p in model.parameters() if p.requires_grad]
+    opt = torch.optim.AdamW(params, lr=1e-4, foreach=True)
+    g = torch.Generator().manual_seed(0)
+    ids = torch.randint(0, TRAIN_V, (TRAIN_B, TRAIN_S), generator=g).to(dev)
+    labels = torch.cat([ids[:, 1:], torch.full((TRAIN_B, 1), -100, device=dev)], 1)
+
+    def rotary(q, k, cos, sin, unsqueeze_dim=1):
+        return apply_fused_rotary(q, k, cos.unsqueeze(unsqueeze_dim), sin.unsqueeze(unsqueeze_dim))
+
+    def step():
+        opt.zero_grad(set_to_none=True)
+        hidden = lm.model(input_ids=ids).last_hidden_state
+        loss = loss_fn(hidden, labels)
+        loss.backward()
+        opt.step()
+        return loss
+
+    saved_rotary = mq.apply_rotary_pos_emb
+    mq.apply_rotary_pos_emb = rotary
+    try:
+        with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+            for _ in range(warmup):
+                loss = step()
+            torch.cuda.synchronize()
+            first = loss.item()
+            t0 = time.perf_counter()
+            for _ in range(steps):
+                loss = step()
+            torch.cuda.synchronize()
+            dt = (time.perf_counter() - t0) / steps
+    finally:
+        mq.apply_rotary_pos_emb = saved_rotary
+    last = loss.item()
+    if not (math.isfinite(first) and math.isfinite(last)):
+        raise RuntimeError(f"train step: non-finite loss {first} -> {last}")
+    n_tok = TRAIN_B * TRAIN_S
+    return {"layers": TRAIN_LAYERS, "tokens": n_tok, "ms_per_step": round(dt * 1e3, 2),
+            "tokens_per_s": round(n_tok / dt, 1), "loss_first": round(first, 4),
+            "loss_last": round(last, 4), "steps": steps, "warmup": warmup,
+            "includes": "fwd + FLCE loss + bwd + AdamW on LoRA params",
+            "attention": "torch SDPA (flash / mem-efficient)"}
+
+
 def pmc_probe(dev):
     """Launch sequence for rocprofv3 --pmc traffic counting: 3 copies of a
     1 GiB buffer (the calibration: a plain copy reads and writes exactly
@@ -281,6 +383,10 @@ def main():
                     help="only the launch sequence used for rocprofv3 --pmc traffic counting")
     ap.add_argument("--no-mfma-ops", action="store_true",
                     help="skip the FLCE / LoRA-backward lines of the breakdown")
+    ap.add_argument("--no-train-step", action="store_true",
+                    help="skip the 4-layer Qwen3 LoRA train-step line")
+    ap.add_argument("--train-step-only", action="store_true",
+                    help="only the 4-layer Qwen3 LoRA train step (one JSON line)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -295,6 +401,9 @@ def main():
     torch.cuda.set_device(dev)
     if args.pmc_probe:
         pmc_probe(dev)
+        return
+    if args.train_step_only:
+        print(json.dumps({"train_step_4layer": bench_train_step(dev)}), flush=True)
         return
     bf = torch.bfloat16
     gate = seeded((N_TOK, INTER), 0, bf).to(dev)
@@ -363,6 +472,8 @@ def main():
     if not args.no_mfma_ops:
         breakdown["flce_fwd_bwd"] = bench_flce(dev, stream, 5)
         breakdown["lora_bwd_layer"] = bench_lora_bwd(dev, stream, 10)
+    if not args.no_train_step:
+        breakdown["train_step_4layer"] = bench_train_step(dev)
     dom_ms = per_op["swiglu_bwd"]
     achieved = SWIGLU_BWD_BYTES / (dom_ms * 1e-3) / 1e9
     roofline = {
