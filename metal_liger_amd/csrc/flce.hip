@@ -5,7 +5,7 @@
 //
 // Loss and gradients in one pass (ml_flce_fwd_grad), over chunks of T tokens:
 //   1. Z = H_c W^T (+ b) as a bf16 MFMA GEMM; its epilogue reduces each wave's
-//      128 logit columns per row to (m, s) = (max z, sum exp(z - m)) and
+//      64 logit columns per row to (m, s) = (max z, sum exp(z - m)) and
 //      stores e = exp(z - m) in bf16 ([T, vocab] buffer). e lies in (0, 1],
 //      so bf16 keeps it to 2^-9 relative whatever the logit's size. The
 //      label logits come from a dot product of each token with its label's
@@ -81,7 +81,7 @@ __device__ __forceinline__ float bias_at(const TB* b, int64_t n) {
 }
 
 // ------------------------------------------------------------ forward epi --
-// Each wave reduces its 128 logit columns to a (max, sum exp(z - max))
+// Each wave reduces its 64 logit columns to a (max, sum exp(z - max))
 // partial per row. With STORE, e = exp(z - max) also replaces the
 // accumulators and is written (bf16) at E[row * ldE + col] through the staged
 // epilogue (16-byte stores). The label logits come from label_logit_kernel.
@@ -138,20 +138,20 @@ struct EpiRowLse {
 
   __device__ __forceinline__ void operator()(f32x4_t (&acc)[big::TM][big::TN], int m0, int n0,
                                              int lane, char* lds, int) const {
-    // a wave whose 128 columns all lie past the vocabulary (second half of
-    // the last tile) owns no partial slot
+    // a wave whose 64 columns all lie past the vocabulary (in the last tile)
+    // owns no partial slot
     if (n0 >= V) return;
     if (n0 + big::WN <= V)
       rows<true>(acc, m0, n0, lane);
     else
       rows<false>(acc, m0, n0, lane);
     if constexpr (STORE) {
-      stage_rows_bf16(
+      constexpr int B = 2;  // stores only
+      stage_rows_bf16<B>(
           lds, lane, m0, n0, [&](int i, int j, int v) { return acc[i][j][v]; },
-          [&](const int (&m)[kStageBatch], const int (&n)[kStageBatch],
-              const float (&x)[kStageBatch][8]) {
+          [&](const int (&m)[B], const int (&n)[B], const float (&x)[B][8]) {
 #pragma unroll
-            for (int q = 0; q < kStageBatch; ++q)
+            for (int q = 0; q < B; ++q)
               if (m[q] < M && n[q] < V) store_row8_bf16(E + (int64_t)m[q] * ldE + n[q], n[q], V, x[q]);
           });
     }
@@ -206,7 +206,7 @@ __global__ __launch_bounds__(1024) void count_valid_kernel(const int64_t* __rest
 
 // In place over E [rows, V] (row stride ldE): d = (e exp(m_blk - lse) -
 // [col == label]) * mask / max(n_valid, 1), bf16. 8 columns per thread (one
-// 16-byte vector; 8 divides the 128-column partial block).
+// 16-byte vector; 8 divides the 64-column partial block).
 __global__ __launch_bounds__(256) void dlogit_pass_kernel(bf16* __restrict__ E, int64_t ldE, int rows,
                                                           int V, const float* __restrict__ pmax,
                                                           int nblk, const float* __restrict__ lse,
@@ -353,12 +353,12 @@ struct EpiDlogit {
         }
       }
     }
-    stage_rows_bf16(
+    constexpr int B = 2;  // stores only
+    stage_rows_bf16<B>(
         lds, lane, m0, n0, [&](int i, int j, int v) { return acc[i][j][v]; },
-        [&](const int (&m)[kStageBatch], const int (&n)[kStageBatch],
-            const float (&x)[kStageBatch][8]) {
+        [&](const int (&m)[B], const int (&n)[B], const float (&x)[B][8]) {
 #pragma unroll
-          for (int q = 0; q < kStageBatch; ++q)
+          for (int q = 0; q < B; ++q)
             if (m[q] < M && n[q] < C) store_row8_bf16(D + (int64_t)m[q] * ldd + n[q], n[q], C, x[q]);
         });
   }
@@ -436,7 +436,7 @@ int fwd_impl(const bf16* hidden, int64_t ldh, const bf16* weight, int64_t ldw, c
   if (rc) return rc;
   EpiRowLse<TB, false> epi{bias, w.pmax, w.psum, nullptr, 0, M, V, nblk};
   gemm_kernel<BigCfg, kKMajor, kKMajor, EpiRowLse<TB, false>>
-      <<<dim3(grid_blocks(pb)), kThreads, 0, st>>>(pb, epi);
+      <<<dim3(grid_blocks(pb)), BigCfg::THREADS, 0, st>>>(pb, epi);
   ML_LAUNCH_CHECK();
   label_logit_kernel<TB><<<dim3((M + 3) / 4), 256, 0, st>>>(hidden, ldh, weight, ldw, bias, labels,
                                                             M, V, H, w.zy);
@@ -537,11 +537,11 @@ int fwd_grad_impl(const bf16* hidden, int64_t ldh, const bf16* weight, int64_t l
       if (grads) {
         EpiRowLse<TB, true> epi{bias, w.pmax, w.psum, w.E, (int64_t)V, Tc, V, nblk};
         gemm_kernel<BigCfg, kKMajor, kKMajor, EpiRowLse<TB, true>>
-            <<<dim3(grid_blocks(pb)), kThreads, 0, st>>>(pb, epi);
+            <<<dim3(grid_blocks(pb)), BigCfg::THREADS, 0, st>>>(pb, epi);
       } else {
         EpiRowLse<TB, false> epi{bias, w.pmax, w.psum, nullptr, 0, Tc, V, nblk};
         gemm_kernel<BigCfg, kKMajor, kKMajor, EpiRowLse<TB, false>>
-            <<<dim3(grid_blocks(pb)), kThreads, 0, st>>>(pb, epi);
+            <<<dim3(grid_blocks(pb)), BigCfg::THREADS, 0, st>>>(pb, epi);
       }
       ML_LAUNCH_CHECK();
       label_logit_kernel<TB><<<dim3((Tc + 3) / 4), 256, 0, st>>>(hc, ldh, weight, ldw, bias, lc, Tc,
@@ -605,7 +605,7 @@ int bwd_impl(const bf16* hidden, int64_t ldh, const bf16* weight, int64_t ldw, c
       EpiDlogit<TB> epi{bias ? bias + c0 : nullptr, labels, ignore, lse, grad, n_valid, D,
                         (int64_t)chunk, M, C, (int64_t)c0};
       gemm_kernel<BigCfg, kKMajor, kKMajor, EpiDlogit<TB>>
-          <<<dim3(grid_blocks(pb)), kThreads, 0, st>>>(pb, epi);
+          <<<dim3(grid_blocks(pb)), BigCfg::THREADS, 0, st>>>(pb, epi);
       ML_LAUNCH_CHECK();
     }
     if (dh32) {  // 2. dH (+)= D W_c

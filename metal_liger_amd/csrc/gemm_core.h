@@ -68,13 +68,15 @@ struct Cfg {
   static constexpr int A_BYTES = BM * kRowBytes, B_BYTES = BN * kRowBytes;
   static constexpr int STAGE_BYTES = A_BYTES + B_BYTES;
   static constexpr int LDS_BYTES = 2 * STAGE_BYTES;
+  // the 256 x 256 tile runs its own engine with 8 waves
+  static constexpr int THREADS = (BM_ == 256 && BN_ == 256) ? 512 : 256;
   static_assert(WAVES_M * WAVES_N == 4, "4 waves per block");
   static_assert(TM >= 1 && TN >= 1 && WM % 32 == 0 && WN % 32 == 0, "wave tile of 32x32 MFMAs");
   static_assert(BM <= 256 && BN <= 256, "at most one 16-byte chunk set per thread");
   static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
 };
 
-using BigCfg = Cfg<256, 256, 2>;   // 2 x 2 waves of 128 x 128
+using BigCfg = Cfg<256, 256, 2>;   // 2 x 4 waves of 128 x 64 (its own engine)
 using TallCfg = Cfg<256, 32, 4>;   // 4 x 1 waves of 64 x 32  (rank-r wide outputs)
 using WideCfg = Cfg<64, 256, 1>;   // 1 x 4 waves of 64 x 64  (few-row outputs)
 
@@ -634,18 +636,26 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef short i16x4_t __attribute__((ext_vector_type(4)));
 
 namespace big {
+constexpr int THREADS = 512;  // 8 waves: two per SIMD
 constexpr int BK = 32;
-constexpr int TM = 8, TN = 8;  // 16 x 16 MFMA tiles per wave
-constexpr int WM = 128, WN = 128;
+constexpr int TM = 8, TN = 4;  // 16 x 16 MFMA tiles per wave
+constexpr int WM = 128, WN = 64;
 constexpr int OP_BYTES = 256 * BK * 2;  // 16 KB per operand per stage
 constexpr int STAGE_BYTES = 2 * OP_BYTES;
-constexpr int STAGES = 4;
-constexpr int LOADS = 4;  // 1-KB loads per wave per operand per k-tile
-// vmcnt immediates (gfx9 encoding): 3 k-tiles (24 loads per wave) in flight
-// after the prologue, 2 k-tiles (16) in the loop.
-constexpr int kWaitVm24 = 0x4F78;
-constexpr int kWaitVm16 = 0x4F70;
-constexpr int kWaitVm0 = 0x0F70;
+#ifndef ML_BIG_STAGES
+#define ML_BIG_STAGES 4
+#endif
+constexpr int STAGES = ML_BIG_STAGES;
+constexpr int DIST = STAGES - 1;  // k-tiles loaded ahead of the one being read
+constexpr int LOADS = 2;  // 1-KB loads per wave per operand per k-tile
+constexpr int EPI_BYTES = 16384;  // LDS per wave for the epilogue
+static_assert(8 * EPI_BYTES <= STAGES * STAGE_BYTES, "epilogue LDS inside the stages");
+// s_waitcnt immediate (gfx9 encoding) for vmcnt(n), other counters ignored.
+constexpr int wait_vm(int n) { return 0x0F70 | (n & 15) | ((n >> 4) << 14); }
+// With DIST k-tiles of 2 * LOADS loads per wave in flight, k-tile t + 1 has
+// landed once at most (DIST - 1) * 2 * LOADS remain.
+constexpr int kWaitVmAhead = wait_vm((DIST - 1) * 2 * LOADS);
+constexpr int kWaitVm0 = wait_vm(0);
 constexpr uint32_t kOob = 0x80000000u;  // past every resource range used here
 constexpr uint32_t kRange = 0x7FFFFFFFu;
 constexpr uint32_t kDword3 = 0x00020000u;  // raw buffer, 32-bit data format
@@ -697,8 +707,8 @@ struct BigIter {
   int kr[big::LOADS];  // MN-major: the k-row of each load
 };
 
-// Wave w issues the 1-KB groups g = w + 4 i (i < 4): rows 16 g .. 16 g + 15
-// (K-major) or k-rows 2 g, 2 g + 1 (MN-major).
+// Wave w (of 8) issues the 1-KB groups g = w + 8 i (i < 2) of each operand:
+// rows 16 g .. 16 g + 15 (K-major) or k-rows 2 g, 2 g + 1 (MN-major).
 template <int L>
 __device__ __forceinline__ void big_setup(BigIter<L>& it, const Operand& op, int row0, int rows,
                                           int wave) {
@@ -710,7 +720,7 @@ __device__ __forceinline__ void big_setup(BigIter<L>& it, const Operand& op, int
     const int last = rows - 1 - row0;
 #pragma unroll
     for (int i = 0; i < big::LOADS; ++i) {
-      const int r = 16 * (wave + 4 * i) + (l >> 2);
+      const int r = 16 * (wave + 8 * i) + (l >> 2);
       const int rc = r < last ? r : last;  // rows past the end re-read the last row
       it.off[i] = (uint32_t)(((int64_t)rc * op.ld + 8 * lc) * 2);
       it.kr[i] = 0;
@@ -722,7 +732,7 @@ __device__ __forceinline__ void big_setup(BigIter<L>& it, const Operand& op, int
     const int last8 = rows - row0 - 8;  // last 8-row group of the operand (rows % 8 == 0)
 #pragma unroll
     for (int i = 0; i < big::LOADS; ++i) {
-      const int r = 2 * (wave + 4 * i) + (l >> 5);
+      const int r = 2 * (wave + 8 * i) + (l >> 5);
       const int h = (r & 3) | (((r >> 3) & 1) << 2);
       int e = 8 * (2 * ((p >> 1) ^ h) + (p & 1));  // first row of the 8 this lane fetches
       e = e < last8 ? e : last8;
@@ -734,13 +744,13 @@ __device__ __forceinline__ void big_setup(BigIter<L>& it, const Operand& op, int
 
 // Per-lane LDS byte offsets (within an operand tile) of the fragment reads
 // of a wave whose sub-tile starts at row wbase of the block tile.
-template <int L>
+template <int L, int NF>
 struct FragAddr {
-  uint32_t a[L == kKMajor ? 1 : big::TM];
+  uint32_t a[L == kKMajor ? 1 : NF];
 };
 
-template <int L>
-__device__ __forceinline__ void frag_addr_setup(FragAddr<L>& fa, int wbase, int lane) {
+template <int L, int NF>
+__device__ __forceinline__ void frag_addr_setup(FragAddr<L, NF>& fa, int wbase, int lane) {
   if constexpr (L == kKMajor) {
     // row wbase + 16 f + (lane & 15), chunk lane >> 4; the swizzle term
     // kswz(row) only depends on row % 16 = lane & 15
@@ -751,9 +761,9 @@ __device__ __forceinline__ void frag_addr_setup(FragAddr<L>& fa, int wbase, int 
     // ((i >> 2) & 3) | (G & 1) << 2 (G = lane >> 4, i = lane & 15)
     const int G = lane >> 4, i = lane & 15;
     const int h = ((i >> 2) & 3) | ((G & 1) << 2);
-    const uint32_t b = (uint32_t)((8 * G + (i >> 2)) * 512 + 8 * (i & 3) + wbase * 2);
+    const uint32_t b = (uint32_t)((8 * G + (i >> 2)) * 512 + 8 * (i & 3));
 #pragma unroll
-    for (int f = 0; f < big::TM; ++f) fa.a[f] = b + (uint32_t)((f ^ h) << 5);
+    for (int f = 0; f < NF; ++f) fa.a[f] = b + (uint32_t)((((wbase >> 4) + f) ^ h) << 5);
   }
 }
 
@@ -767,9 +777,9 @@ struct BigFrags {
 template <int L>
 constexpr int reads_per_frag() { return L == kKMajor ? 1 : 2; }
 
-template <int L>
-__device__ __forceinline__ void read_big_frag(bf16x8_t& dst, const char* op, const FragAddr<L>& fa,
-                                              int f, int half) {
+template <int L, int NF>
+__device__ __forceinline__ void read_big_frag(bf16x8_t& dst, const char* op,
+                                              const FragAddr<L, NF>& fa, int f, int half) {
   if constexpr (L == kKMajor) {
     dst = *reinterpret_cast<const bf16x8_t*>(op + fa.a[0] + 1024 * f);
   } else {
@@ -786,7 +796,8 @@ __device__ __forceinline__ void read_big_frag(bf16x8_t& dst, const char* op, con
 
 template <int LA, int LB, int Q>
 __device__ __forceinline__ void big_read(BigFrags& f, const char* As, const char* Bs,
-                                         const FragAddr<LA>& fa, const FragAddr<LB>& fb) {
+                                         const FragAddr<LA, big::TM>& fa,
+                                         const FragAddr<LB, big::TN>& fb) {
   constexpr int RB = reads_per_frag<LB>(), RA = reads_per_frag<LA>();
   if constexpr (Q < big::TN * RB) {
     read_big_frag<LB>(f.b[Q / RB], Bs, fb, Q / RB, Q % RB);
@@ -803,47 +814,26 @@ __device__ __forceinline__ uint32_t big_oob(const BigIter<L>& it, int i, bool li
   return (live && k < klen) ? 0u : big::kOob;
 }
 
-// One k-tile: 64 MFMAs on fc; reads of the next k-tile's fragments into fn
-// (from As_n, Bs_n) in the first slots; the 8 loads of a k-tile into
-// (ldA, ldB) in slots 32, 36, .., 60.
-template <int LA, int LB>
-__device__ __forceinline__ void big_tile(f32x4_t (&acc)[big::TM][big::TN], BigFrags& fn,
-                                         const BigFrags& fc, const char* As_n, const char* Bs_n,
-                                         const FragAddr<LA>& fa, const FragAddr<LB>& fb,
-                                         const BigIter<LA>& ia, const BigIter<LB>& ib, rsrc_t ra,
-                                         rsrc_t rb, const uint32_t (&oa)[big::LOADS],
-                                         const uint32_t (&ob)[big::LOADS], char* ldA, char* ldB,
-                                         int wave) {
-  constexpr int kReads = big::TN * reads_per_frag<LB>() + big::TM * reads_per_frag<LA>();
-  static_assert(kReads <= 32, "reads fit in the first half");
-  static_for<big::TM * big::TN>([&](auto qc) {
-    constexpr int q = decltype(qc)::value;
-    if constexpr (q < kReads) big_read<LA, LB, q>(fn, As_n, Bs_n, fa, fb);
-    if constexpr (q >= 32 && (q - 32) % 4 == 0) {
-      constexpr int ld = (q - 32) / 4;  // 0..7: A loads 0..3, then B loads 0..3
-      if constexpr (ld < big::LOADS)
-        buf_load_lds(ra, ia.off[ld] | oa[ld], ldA + (wave + 4 * ld) * 1024);
-      else
-        buf_load_lds(rb, ib.off[ld - big::LOADS] | ob[ld - big::LOADS],
-                     ldB + (wave + 4 * (ld - big::LOADS)) * 1024);
-    }
-    constexpr int i = q / big::TN, j = q % big::TN;
-    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fc.a[i], fc.b[j], acc[i][j], 0, 0, 0);
-    __builtin_amdgcn_sched_barrier(0);
-  });
+// A barrier the compiler schedules nothing across (the MFMA clusters and the
+// memory clusters stay on their own side of it).
+__device__ __forceinline__ void big_barrier() {
+  __builtin_amdgcn_sched_barrier(0);
+  __syncthreads();
+  __builtin_amdgcn_sched_barrier(0);
 }
 
-// Main loop of the big tile; st[] are four distinct __shared__ arrays of
-// STAGE_BYTES (A tile, then B tile).
+// Main loop of the big tile; lds holds STAGES stages of STAGE_BYTES (A tile,
+// then B tile). Wave w = 4 g + s computes rows 128 g .. 128 g + 127 and
+// columns 64 s .. 64 s + 63 of the block tile.
 template <int LA, int LB>
 __device__ __forceinline__ void big_mainloop(const Problem& pb, int tm, int tn, int split,
-                                             char* const (&st)[big::STAGES],
-                                             f32x4_t (&acc)[big::TM][big::TN]) {
+                                             char* lds, f32x4_t (&acc)[big::TM][big::TN]) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = (wave >> 1) * big::WM;
-  const int wn = (wave & 1) * big::WN;
+  const int grp = wave >> 2;
+  const int wm = grp * big::WM;
+  const int wn = (wave & 3) * big::WN;
   const int m0 = tm * 256;
   const int n0 = tn * 256;
 #pragma unroll
@@ -863,6 +853,7 @@ __device__ __forceinline__ void big_mainloop(const Problem& pb, int tm, int tn, 
     nk = 0;
     for (int s = 0; s < pb.nseg; ++s) nk += (pb.seg[s].k_len + big::BK - 1) / big::BK;
   }
+  // (nk is block-uniform: every wave returns here or none does)
   if (nk <= 0) return;
 
   // Load cursor: the next k-tile to load (segment seg, offset kc, length
@@ -874,23 +865,23 @@ __device__ __forceinline__ void big_mainloop(const Problem& pb, int tm, int tn, 
   big_setup<LA>(ia, pb.seg[0].a, m0, pb.M, wave);
   big_setup<LB>(ib, pb.seg[0].b, n0, pb.N, wave);
   const int kb = 8 * ((lane & 3) ^ kswz(lane >> 2));  // K-major lanes: k offset in a k-tile
-  FragAddr<LA> fa;
-  FragAddr<LB> fb;
-  frag_addr_setup<LA>(fa, wm, lane);
-  frag_addr_setup<LB>(fb, wn, lane);
+  FragAddr<LA, big::TM> fa;
+  FragAddr<LB, big::TN> fb;
+  frag_addr_setup<LA, big::TM>(fa, wm, lane);
+  frag_addr_setup<LB, big::TN>(fb, wn, lane);
 
-  auto cursor_loads = [&](rsrc_t& ra, rsrc_t& rb, uint32_t (&oa)[big::LOADS],
-                          uint32_t (&ob)[big::LOADS]) __attribute__((always_inline)) {
+  // Issues this wave's loads of the cursor's k-tile into stage dst.
+  auto cursor_loads = [&](char* dst) __attribute__((always_inline)) {
     const bool live = loaded < nk;
-    ra = make_rsrc(ia.base + (int64_t)kc * ia.kstep);
-    rb = make_rsrc(ib.base + (int64_t)kc * ib.kstep);
+    const rsrc_t ra = make_rsrc(ia.base + (int64_t)kc * ia.kstep);
+    const rsrc_t rb = make_rsrc(ib.base + (int64_t)kc * ib.kstep);
 #pragma unroll
     for (int i = 0; i < big::LOADS; ++i) {
-      oa[i] = big_oob<LA>(ia, i, live, kc, kb, klen);
-      ob[i] = big_oob<LB>(ib, i, live, kc, kb, klen);
+      buf_load_lds(ra, ia.off[i] | big_oob<LA>(ia, i, live, kc, kb, klen),
+                   dst + (wave + 8 * i) * 1024);
+      buf_load_lds(rb, ib.off[i] | big_oob<LB>(ib, i, live, kc, kb, klen),
+                   dst + big::OP_BYTES + (wave + 8 * i) * 1024);
     }
-  };
-  auto advance = [&]() __attribute__((always_inline)) {
     ++loaded;
     if (loaded >= nk) return;
     kc += big::BK;
@@ -903,50 +894,58 @@ __device__ __forceinline__ void big_mainloop(const Problem& pb, int tm, int tn, 
     }
   };
 
-  // Prologue: k-tiles 0..3 into the four stages; wait for k-tile 0.
+  // Prologue: k-tiles 0 .. DIST - 1; k-tile 0 published by the barrier.
 #pragma unroll
-  for (int j = 0; j < big::STAGES; ++j) {
-    rsrc_t ra, rb;
-    uint32_t oa[big::LOADS], ob[big::LOADS];
-    cursor_loads(ra, rb, oa, ob);
+  for (int j = 0; j < big::DIST; ++j) cursor_loads(lds + j * big::STAGE_BYTES);
+  __builtin_amdgcn_s_waitcnt(big::kWaitVmAhead);
+  big_barrier();
+  // Ping-pong: group 1 runs one phase behind group 0, so that while one
+  // wave of a SIMD issues its MFMA cluster the other issues its loads and
+  // fragment reads. Each k-tile t is two phases of a group:
+  //   memory: loads of k-tile t + DIST into stage (t + DIST) % 4, the
+  //           fragment reads of k-tile t, then a wait until this wave's loads
+  //           of k-tile t + 1 have landed and its reads are in registers;
+  //   compute: the 32 MFMAs of k-tile t.
+  // A barrier ends every phase. Stage (t + DIST) % 4 last held k-tile t - 1,
+  // whose last reads (group 1's memory phase of t - 1) ended before the
+  // barrier that starts group 0's memory phase of t; k-tile t + 1 is
+  // published by the barriers that end both groups' memory phases of t.
+  if (grp == 1) big_barrier();
+  BigFrags f;
+  auto iteration = [&](const char* cur, char* ld) __attribute__((always_inline)) {
+    cursor_loads(ld);
+    static_for<big::TN * reads_per_frag<LB>() + big::TM * reads_per_frag<LA>()>([&](auto qc) {
+      big_read<LA, LB, decltype(qc)::value>(f, cur, cur + big::OP_BYTES, fa, fb);
+    });
+    __builtin_amdgcn_s_waitcnt(big::kWaitVmAhead);
+    big_barrier();
 #pragma unroll
-    for (int i = 0; i < big::LOADS; ++i) {
-      buf_load_lds(ra, ia.off[i] | oa[i], st[j] + (wave + 4 * i) * 1024);
-      buf_load_lds(rb, ib.off[i] | ob[i], st[j] + big::OP_BYTES + (wave + 4 * i) * 1024);
-    }
-    advance();
-  }
-  __builtin_amdgcn_s_waitcnt(big::kWaitVm24);
-  __syncthreads();
-  BigFrags f0, f1;
-  static_for<big::TN * reads_per_frag<LB>() + big::TM * reads_per_frag<LA>()>([&](auto qc) {
-    big_read<LA, LB, decltype(qc)::value>(f0, st[0], st[0] + big::OP_BYTES, fa, fb);
-  });
-
-  // k-tile t in stage j = t % 4 (fragments in fc), k-tile t + 1 in stage j + 1.
-  auto iteration = [&](char* cur, char* nxt, BigFrags& fc, BigFrags& fn)
-      __attribute__((always_inline)) {
-    // This wave's loads of k-tile t + 1 have landed (the vmcnt wait is
-    // explicit: the compiler's fence does not cover loads into LDS) and its
-    // fragment reads of k-tile t are done (fence); the barrier publishes
-    // k-tile t + 1 and releases stage cur.
-    __builtin_amdgcn_s_waitcnt(big::kWaitVm16);
-    __syncthreads();
-    rsrc_t ra, rb;
-    uint32_t oa[big::LOADS], ob[big::LOADS];
-    cursor_loads(ra, rb, oa, ob);
-    big_tile<LA, LB>(acc, fn, fc, nxt, nxt + big::OP_BYTES, fa, fb, ia, ib, ra, rb, oa, ob, cur,
-                     cur + big::OP_BYTES, wave);
-    advance();
+    for (int i = 0; i < big::TM; ++i)
+#pragma unroll
+      for (int j = 0; j < big::TN; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(f.a[i], f.b[j], acc[i][j], 0, 0, 0);
+    big_barrier();
   };
-  // The body runs the four stages in turn; the k-tile count is rounded up to
-  // a multiple of four (the extra k-tiles are zeros and add nothing).
-  for (int t = 0; t < nk; t += big::STAGES) {
-    iteration(st[0], st[1], f0, f1);
-    iteration(st[1], st[2], f1, f0);
-    iteration(st[2], st[3], f0, f1);
-    iteration(st[3], st[0], f1, f0);
+#ifdef ML_BIG_ROLLED
+  // k-tile t reads stage t % STAGES and loads stage (t + DIST) % STAGES.
+  uint32_t rd = 0, wr = big::DIST * big::STAGE_BYTES;
+  constexpr uint32_t kWrap = big::STAGES * big::STAGE_BYTES;
+  for (int t = 0; t < nk; ++t) {
+    iteration(lds + rd, lds + wr);
+    rd = rd + big::STAGE_BYTES == kWrap ? 0u : rd + big::STAGE_BYTES;
+    wr = wr + big::STAGE_BYTES == kWrap ? 0u : wr + big::STAGE_BYTES;
   }
+#else
+  // The body runs the stages in turn; the k-tile count is rounded up to a
+  // multiple of STAGES (the extra k-tiles are zeros and add nothing).
+  for (int t = 0; t < nk; t += big::STAGES) {
+    static_for<big::STAGES>([&](auto jc) {
+      constexpr int j = decltype(jc)::value;
+      iteration(lds + j * big::STAGE_BYTES, lds + ((j + big::DIST) % big::STAGES) * big::STAGE_BYTES);
+    });
+  }
+#endif
+  if (grp == 0) big_barrier();
   __builtin_amdgcn_s_waitcnt(big::kWaitVm0);
   __syncthreads();  // loads past the end have landed; the epilogue may reuse the LDS
 }
@@ -988,8 +987,8 @@ __device__ __forceinline__ void for_each_acc(AccT (&acc)[TM][TN], int m0, int n0
 // ------------------------------------------------ staged bf16 epilogues --
 // Global stores of single bf16 elements (the accumulator layout gives a lane
 // one column of 4 consecutive rows) use a 64-lane instruction for 128 bytes
-// in 2-byte pieces. Instead, a wave stages its 128 x 128 results, rounded to
-// bf16, in 32 KB of LDS of its own and takes them back as rows of 8
+// in 2-byte pieces. Instead, a wave stages its 128 x 64 results, rounded to
+// bf16, in LDS of its own (512 bytes per MFMA tile) and takes them back as rows of 8
 // consecutive columns, one 16-byte vector per lane:
 //   phase 1: lane (G = lane / 16, c = lane % 16) writes rows 4 G .. 4 G + 3 of
 //            column c of each 16 x 16 block as one 8-byte ds_write_b64; the
@@ -998,27 +997,28 @@ __device__ __forceinline__ void for_each_acc(AccT (&acc)[TM][TN], int m0, int n0
 //            and cb + 4 .. cb + 7 (cb = 0 or 8) of a block: lane 4 a + b
 //            addresses column cb + a, rows 4 b .. 4 b + 3, so lane i receives
 //            row i at 4 consecutive columns. Lanes 32-63 take the next block.
-// val(i, j, v) gives the value of accumulator element (i, j, v). The 32
-// row vectors of a lane go to rows(m, n, x) in batches of kStageBatch:
+// val(i, j, v) gives the value of accumulator element (i, j, v). The 16
+// row vectors of a lane go to rows(m, n, x) in batches of BATCH (default kStageBatch):
 // x[q][0..7] = columns n[q] .. n[q] + 7 of row m[q] (n[q] a multiple of 8),
 // so a functor that reads global memory can issue all of a batch's loads
-// before its first store.
+// before its first store (store-only functors use smaller batches: fewer
+// live registers).
 typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
 constexpr int kStageBatch = 8;
 
-template <class Val, class Rows>
+template <int BATCH = kStageBatch, int TM = big::TM, int TN = big::TN, class Val, class Rows>
 __device__ __forceinline__ void stage_rows_bf16(char* lds, int lane, int m0, int n0, Val&& val,
                                                 Rows&& rows) {
   const int G = lane >> 4, c = lane & 15;
   char* wr = lds + (c * 16 + 4 * G) * 2;
 #pragma unroll
-  for (int i = 0; i < big::TM; ++i)
+  for (int i = 0; i < TM; ++i)
 #pragma unroll
-    for (int j = 0; j < big::TN; ++j) {
+    for (int j = 0; j < TN; ++j) {
       bf16x4_t w;
 #pragma unroll
       for (int v = 0; v < 4; ++v) w[v] = static_cast<bf16>(val(i, j, v));
-      *reinterpret_cast<bf16x4_t*>(wr + (i * big::TN + j) * 512) = w;
+      *reinterpret_cast<bf16x4_t*>(wr + (i * TN + j) * 512) = w;
     }
   __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's writes are in LDS
   __builtin_amdgcn_wave_barrier();
@@ -1027,16 +1027,16 @@ __device__ __forceinline__ void stage_rows_bf16(char* lds, int lane, int m0, int
   const int cb = 8 * ((lane >> 4) & 1);
   const int jo = lane >> 5;
   const char* rd = lds + jo * 512 + ((cb + a) * 16 + 4 * b) * 2;
-  constexpr int kVecs = big::TM * big::TN / 2;  // 32 row vectors per lane
-  static_assert(kVecs % kStageBatch == 0, "whole batches");
+  constexpr int kVecs = TM * TN / 2;  // row vectors per lane
+  static_assert(kVecs % BATCH == 0, "whole batches");
 #pragma unroll
-  for (int q0 = 0; q0 < kVecs; q0 += kStageBatch) {
-    int m[kStageBatch], n[kStageBatch];
-    float x[kStageBatch][8];
+  for (int q0 = 0; q0 < kVecs; q0 += BATCH) {
+    int m[BATCH], n[BATCH];
+    float x[BATCH][8];
 #pragma unroll
-    for (int q = 0; q < kStageBatch; ++q) {
-      const int i = (q0 + q) / (big::TN / 2), jp = (q0 + q) % (big::TN / 2);
-      const char* blk = rd + (i * big::TN + 2 * jp) * 512;
+    for (int q = 0; q < BATCH; ++q) {
+      const int i = (q0 + q) / (TN / 2), jp = (q0 + q) % (TN / 2);
+      const char* blk = rd + (i * TN + 2 * jp) * 512;
       const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lp)(blk));
       const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lp)(blk + 4 * 32));
 #pragma unroll
@@ -1075,27 +1075,22 @@ __device__ __forceinline__ void load_row8_bf16(const bf16* p, int n, int N, floa
 // The GEMM kernel: mainloop + epilogue functor
 //   epi(acc, m_base, n_base, lane, smem, split) with m_base / n_base the
 //   origin of this wave's sub-tile and acc in the path's MFMA layout
-//   (f32x4_t[8][8] for the 256 x 256 tile, f32x16_t[TM][TN] otherwise).
-//   smem: LDS the epilogue may use - for the 256 x 256 tile, 32 KB private
+//   (f32x4_t[8][4] for the 256 x 256 tile, f32x16_t[TM][TN] otherwise).
+//   smem: LDS the epilogue may use - for the 256 x 256 tile, 16 KB private
 //   to the wave (staged bf16 epilogues); otherwise the block's stage 0.
 template <class C, int LA, int LB, class Epi>
-__global__ __launch_bounds__(kThreads) void gemm_kernel(const Problem pb, const Epi epi) {
+__global__ __launch_bounds__(C::THREADS) void gemm_kernel(const Problem pb, const Epi epi) {
   int tm, tn, split;
   if (!tile_coords(pb, tm, tn, split)) return;
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   if constexpr (C::BM == 256 && C::BN == 256) {
-    __shared__ __attribute__((aligned(16))) char s0[big::STAGE_BYTES];
-    __shared__ __attribute__((aligned(16))) char s1[big::STAGE_BYTES];
-    __shared__ __attribute__((aligned(16))) char s2[big::STAGE_BYTES];
-    __shared__ __attribute__((aligned(16))) char s3[big::STAGE_BYTES];
-    char* const st[big::STAGES] = {s0, s1, s2, s3};
+    __shared__ __attribute__((aligned(16))) char lds[big::STAGES * big::STAGE_BYTES];
     f32x4_t acc[big::TM][big::TN];
-    big_mainloop<LA, LB>(pb, tm, tn, split, st, acc);
-    // each wave gets one stage (32 KB) of LDS for its epilogue
-    const int w = __builtin_amdgcn_readfirstlane(wave);
-    char* wl = w == 0 ? s0 : w == 1 ? s1 : w == 2 ? s2 : s3;
-    epi(acc, tm * 256 + (wave >> 1) * big::WM, tn * 256 + (wave & 1) * big::WN, tid & 63, wl,
+    big_mainloop<LA, LB>(pb, tm, tn, split, lds, acc);
+    // each wave gets 16 KB of LDS of its own for its epilogue
+    char* wl = lds + __builtin_amdgcn_readfirstlane(wave) * big::EPI_BYTES;
+    epi(acc, tm * 256 + (wave >> 2) * big::WM, tn * 256 + (wave & 3) * big::WN, tid & 63, wl,
         split);
   } else {
     __shared__ __attribute__((aligned(16))) char stage0[C::STAGE_BYTES];
@@ -1317,7 +1312,8 @@ inline int launch_store(const Problem& pb, int la, int lb, void* C, int64_t ldc,
                         float beta, hipStream_t st) {
   EpiStore<TC> epi{static_cast<TC*>(C), ldc, pb.M, pb.N, alpha, beta};
   const dim3 grid(grid_blocks(pb));
-#define ML_G(LA, LB) gemm_kernel<BigCfg, LA, LB, EpiStore<TC>><<<grid, kThreads, 0, st>>>(pb, epi)
+#define ML_G(LA, LB) \
+  gemm_kernel<BigCfg, LA, LB, EpiStore<TC>><<<grid, BigCfg::THREADS, 0, st>>>(pb, epi)
   if (la == kKMajor && lb == kKMajor) ML_G(kKMajor, kKMajor);
   else if (la == kKMajor && lb == kMNMajor) ML_G(kKMajor, kMNMajor);
   else if (la == kMNMajor && lb == kKMajor) ML_G(kMNMajor, kKMajor);
@@ -1333,7 +1329,7 @@ template <class C, int LA, int LB, typename TC>
 inline int launch_splitk(const Problem& pb, float* ws, TC* out, int64_t ldo, float alpha, float beta,
                          hipStream_t st) {
   EpiPartial epi{ws, pb.M, pb.N};
-  gemm_kernel<C, LA, LB, EpiPartial><<<dim3(grid_blocks(pb)), kThreads, 0, st>>>(pb, epi);
+  gemm_kernel<C, LA, LB, EpiPartial><<<dim3(grid_blocks(pb)), C::THREADS, 0, st>>>(pb, epi);
   ML_LAUNCH_CHECK();
   const int64_t total = (int64_t)pb.M * pb.N;
   const int64_t per_thread = pb.N % 4 == 0 ? 4 : 1;

@@ -294,7 +294,7 @@ extern "C" int ml_lora_mlp_bwd(const void* X, int64_t n_tokens, int64_t hidden,
     lora::EpiSwigluBwd epi{static_cast<const bf16*>(gate), static_cast<const bf16*>(up), dgate,
                            dup, (int64_t)I, N, I};
     gemm_kernel<BigCfg, kKMajor, kMNMajor, lora::EpiSwigluBwd>
-        <<<dim3(grid_blocks(pb)), kThreads, 0, st>>>(pb, epi);
+        <<<dim3(grid_blocks(pb)), BigCfg::THREADS, 0, st>>>(pb, epi);
     ML_LAUNCH_CHECK();
   }
   // gate / up adapters
