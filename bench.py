@@ -23,7 +23,7 @@ and the 4-layer Qwen3-style LoRA train step (batch 4 x 2048 tokens, every
 fused op patched in, FLCE loss, AdamW on the adapters) in tokens/s.
 
 Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline] [--no-mfma-ops] [--no-train-step]
-       [--train-step-only] [--pmc-probe]
+       [--train-step-only] [--pmc-probe] [--pmc-mfma-probe]
 """
 
 from __future__ import annotations
@@ -290,8 +290,10 @@ def bench_train_step(dev, steps=5, warmup=2):
 def pmc_probe(dev):
     """Launch sequence for rocprofv3 --pmc traffic counting: 3 copies of a
     1 GiB buffer (the calibration: a plain copy reads and writes exactly
-    1 GiB each), then 5 launches of the SwiGLU backward on gate, up, dy
-    [8192, 6144] bf16 (503,316,480 algorithmic bytes per launch)."""
+    1 GiB each), then 5 launches each of the SwiGLU backward and forward on
+    gate, up, dy [8192, 6144] bf16, RoPE (positions, in-kernel cos/sin) on
+    q [4, 16, 2048, 128], k [4, 8, 2048, 128] bf16, and RMSNorm forward and
+    backward on x [8192, 2048] fp32."""
     import torch
 
     from metal_liger_amd import hip_ops
@@ -300,14 +302,51 @@ def pmc_probe(dev):
     gate = gpu_randn((N_TOK, INTER), 0, dev)
     up = gpu_randn((N_TOK, INTER), 1, dev)
     dy = gpu_randn((N_TOK, INTER), 2, dev)
+    q = gpu_randn((RB, RHQ, RS, RD), 3, dev)
+    k = gpu_randn((RB, RHK, RS, RD), 4, dev)
+    pos = torch.arange(RS, device=dev)
+    inv = hip_ops.rope_inv_freq(RD, THETA, dev)
+    x = gpu_randn((RMS_N, RMS_H), 40, dev, dtype=torch.float32)
+    w = 1.0 + 0.1 * gpu_randn((RMS_H,), 41, dev, dtype=torch.float32)
+    gx = gpu_randn((RMS_N, RMS_H), 42, dev, dtype=torch.float32)
+    _, rrms = hip_ops.rms_norm_fwd(x, w, 1e-6)
     torch.cuda.synchronize()
     for _ in range(3):
         dst.copy_(src)
     torch.cuda.synchronize()
-    for _ in range(5):
-        hip_ops.swiglu_bwd(gate, up, dy)
+    for fn in (lambda: hip_ops.swiglu_bwd(gate, up, dy),
+               lambda: hip_ops.swiglu_fwd(gate, up),
+               lambda: hip_ops.rope_pos(q, k, pos, inv, 1.0),
+               lambda: hip_ops.rms_norm_fwd(x, w, 1e-6),
+               lambda: hip_ops.rms_norm_bwd(x, w, gx, rrms, 1e-6)):
+        for _ in range(5):
+            fn()
+        torch.cuda.synchronize()
+    print("pmc probe: 3 x 1 GiB copy; 5 x each of swiglu_bwd, swiglu_fwd [8192, 6144] bf16, "
+          "rope_pos q/k bf16, rms_norm fwd, bwd [8192, 2048] fp32", flush=True)
+
+
+def pmc_mfma_probe(dev):
+    """Launch sequence for rocprofv3 --pmc matrix-core counting: one warm-up
+    and one measured call each of the one-pass FLCE forward (loss, dH, dW;
+    hidden [8192, 2048], lm_head [151936, 2048]) and of the LoRA QKV and MLP
+    backward of the Qwen3-style 2B layer."""
+    import torch
+
+    from metal_liger_amd import hip_ops
+    h = gpu_randn((FLCE_N, FLCE_H), 10, dev)
+    w = gpu_randn((FLCE_V, FLCE_H), 11, dev, 0.02)
+    g = torch.Generator(device=dev).manual_seed(12)
+    lab = torch.randint(0, FLCE_V, (FLCE_N,), generator=g, device=dev)
+    for _ in range(2):
+        out = hip_ops.flce_fwd_grad(h, w, lab)
     torch.cuda.synchronize()
-    print("pmc probe: 3 x 1 GiB copy, 5 x swiglu_bwd [8192, 6144] bf16", flush=True)
+    del out, h, w, lab
+    torch.cuda.empty_cache()
+    stream = torch.cuda.current_stream(dev)
+    bench_lora_bwd(dev, stream, 1)
+    torch.cuda.synchronize()
+    print("pmc mfma probe: 2 x flce_fwd_grad, 2 x (lora qkv bwd + mlp bwd)", flush=True)
 
 
 def load_traffic():
@@ -381,6 +420,9 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--pmc-probe", action="store_true",
                     help="only the launch sequence used for rocprofv3 --pmc traffic counting")
+    ap.add_argument("--pmc-mfma-probe", action="store_true",
+                    help="only the FLCE / LoRA-backward launches used for rocprofv3 --pmc "
+                         "matrix-core counting")
     ap.add_argument("--no-mfma-ops", action="store_true",
                     help="skip the FLCE / LoRA-backward lines of the breakdown")
     ap.add_argument("--no-train-step", action="store_true",
@@ -401,6 +443,9 @@ def main():
     torch.cuda.set_device(dev)
     if args.pmc_probe:
         pmc_probe(dev)
+        return
+    if args.pmc_mfma_probe:
+        pmc_mfma_probe(dev)
         return
     if args.train_step_only:
         print(json.dumps({"train_step_4layer": bench_train_step(dev)}), flush=True)
