@@ -103,6 +103,8 @@ int ml_swiglu_fwd(const void* gate, const void* up, void* out, int64_t n, int dt
  *
  *   dup   = dy * (gate * s)
  *   dgate = ((dy * up) * s) * (1 + gate * (1 - s)),    s = sigmoid(gate)
+ *
+ * dy may be the same buffer as dgate (the backward then runs in place).
  */
 int ml_swiglu_bwd(const void* gate, const void* up, const void* dy, void* dgate, void* dup,
                   int64_t n, int dtype, void* stream);

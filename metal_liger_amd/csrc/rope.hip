@@ -5,9 +5,9 @@
 // cos/sin values once (from the tables, or computed in-kernel from the
 // position and inv_freq), then rotates up to kHeadsPerThread heads of the
 // concatenated [q heads | k heads] list with them, issuing all of those
-// heads' loads before any arithmetic (measured on MI355X: 8 heads per
-// thread with hoisted loads moves the q+k config at 5.4 TB/s, against 3.8
-// TB/s for 4 heads loaded one at a time). Eight threads cover a
+// heads' loads before any arithmetic (measured on MI355X: hoisted loads move
+// the q+k config at 5.4-5.6 TB/s, against 3.8 TB/s for heads loaded one at a
+// time; 4 heads per thread is slightly ahead of 2, 3 and 8). Eight threads cover a
 // 128-wide head; a wave covers 8 consecutive positions, so each 16-byte
 // load/store instruction of a wave touches 2 KiB of contiguous rows for a
 // contiguous [B, H, S, D] tensor (and whole rows for HF's transposed views).
@@ -21,7 +21,7 @@ namespace mla {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kHeadsPerThread = 8;
+constexpr int kHeadsPerThread = 4;
 
 struct RopeTensor {
   const void* in;
@@ -58,9 +58,14 @@ __device__ __forceinline__ void load_any(const T* p, float* out) {
   }
 }
 
+// Outputs are streamed (never re-read by this kernel): 16-byte stores carry
+// the non-temporal hint, so they do not sit in L2 as dirty lines to be
+// written back when the kernel ends.
 template <typename T, int N>
 __device__ __forceinline__ void store_any(T* p, const float* in) {
-  if constexpr (N * sizeof(T) >= 16 || N == 1) {
+  if constexpr (N * sizeof(T) >= 16) {
+    store_n_nt<T, N>(p, in);
+  } else if constexpr (N == 1) {
     store_n<T, N>(p, in);
   } else {
 #pragma unroll

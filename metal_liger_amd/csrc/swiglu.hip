@@ -65,9 +65,11 @@ __global__ __launch_bounds__(kThreads) void swiglu_fwd_vec(const T* __restrict__
 }
 
 template <typename T, int UNROLL, bool FULL>
+// dy may alias dg (an in-place backward): it carries no __restrict__, and
+// every element is loaded before its result is stored.
 __device__ __forceinline__ void swiglu_bwd_step(const T* __restrict__ g, const T* __restrict__ u,
-                                                const T* __restrict__ dy, T* __restrict__ dg,
-                                                T* __restrict__ du, int64_t base, int64_t nvec) {
+                                                const T* dy, T* dg, T* __restrict__ du,
+                                                int64_t base, int64_t nvec) {
   constexpr int VEC = vec16<T>();
   float gv[UNROLL][VEC], uv[UNROLL][VEC], yv[UNROLL][VEC];
 #pragma unroll
@@ -98,8 +100,8 @@ __device__ __forceinline__ void swiglu_bwd_step(const T* __restrict__ g, const T
 
 template <typename T, int UNROLL>
 __global__ __launch_bounds__(kThreads) void swiglu_bwd_vec(
-    const T* __restrict__ g, const T* __restrict__ u, const T* __restrict__ dy,
-    T* __restrict__ dg, T* __restrict__ du, int64_t nvec) {
+    const T* __restrict__ g, const T* __restrict__ u, const T* dy, T* dg, T* __restrict__ du,
+    int64_t nvec) {
   const int64_t stride = (int64_t)gridDim.x * kThreads * UNROLL;
   int64_t base = (int64_t)blockIdx.x * kThreads * UNROLL + threadIdx.x;
   for (; base + (int64_t)(UNROLL - 1) * kThreads < nvec; base += stride)
@@ -122,8 +124,8 @@ __global__ __launch_bounds__(kThreads) void swiglu_fwd_scalar(const T* __restric
 
 template <typename T>
 __global__ __launch_bounds__(kThreads) void swiglu_bwd_scalar(
-    const T* __restrict__ g, const T* __restrict__ u, const T* __restrict__ dy,
-    T* __restrict__ dg, T* __restrict__ du, int64_t begin, int64_t n) {
+    const T* __restrict__ g, const T* __restrict__ u, const T* dy, T* dg, T* __restrict__ du,
+    int64_t begin, int64_t n) {
   for (int64_t i = begin + (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n;
        i += (int64_t)gridDim.x * kThreads) {
     const float gv = to_f32(g[i]);

@@ -201,6 +201,26 @@ def test_swiglu_empty(dev):
     assert hip_ops.swiglu_fwd(e, e).shape == (0, 8)
 
 
+@pytest.mark.parametrize("n", [8192 * 48 + 5, 4096])
+def test_swiglu_bwd_in_place(dev, n):
+    """ml_swiglu_bwd with dy and dgate the same buffer (the LoRA MLP backward
+    runs it that way) gives the out-of-place result bit for bit, vector path
+    and scalar tail included."""
+    from metal_liger_amd import hip_ops
+    from metal_liger_amd._hip import call
+    g = seeded((n,), 31, torch.bfloat16).to(dev)
+    u = seeded((n,), 32, torch.bfloat16).to(dev)
+    dy = seeded((n,), 33, torch.bfloat16).to(dev)
+    rdg, rdu = hip_ops.swiglu_bwd(g, u, dy)
+    buf = dy.clone()
+    du = torch.empty_like(buf)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    call("ml_swiglu_bwd", g.data_ptr(), u.data_ptr(), buf.data_ptr(), buf.data_ptr(),
+         du.data_ptr(), n, 1, stream)
+    assert torch.equal(buf, rdg)
+    assert torch.equal(du, rdu)
+
+
 # --------------------------------------------------------------------- RoPE --
 
 
