@@ -693,6 +693,13 @@ __device__ __forceinline__ void buf_load_lds(rsrc_t r, uint32_t voff, char* lds)
                : "v"(voff), "s"(r), "s"(lds_addr(lds))
                : "m0");
 }
+// The 4-byte form: lane l's dword lands at LDS offset 4 l (256 B per instruction).
+__device__ __forceinline__ void buf_load_lds_dword(rsrc_t r, uint32_t voff, char* lds) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dword %0, %1, 0 offen lds"
+               :
+               : "v"(voff), "s"(r), "s"(lds_addr(lds))
+               : "m0");
+}
 #pragma clang diagnostic pop
 
 // Chunk swizzle of the K-major tile (a function of the row's low 4 bits).

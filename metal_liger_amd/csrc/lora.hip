@@ -3,19 +3,18 @@
 // Per adapter with base W [out, in], A [r, in], B [out, r], scale s, the
 // reference computes (dY the output grad, X the saved input):
 //   dA = s (dY B)^T X          dB = s dY^T (X A^T)        dX += dY W + s (dY B) A
-// Here, with every product on the bf16 MFMA engine (fp32 accumulation):
-//   P   = s dY B               [tokens, r]   256x32 tiles, split-K over out
+// Here, with every product on bf16 MFMAs (fp32 accumulation):
+//   P, dB = s dY B, s dY^T XA  ONE pass over dY (dy_pass_kernel, rank 16;
+//                              XA = X A^T saved by the forward); other ranks
+//                              use two split-K skinny products
 //   dA  = P^T X                [r, in]       64x256 tiles, split-K over tokens
-//   dB  = s dY^T XA            [out, r]      256x32 tiles, split-K over tokens
-//                                            (XA = X A^T saved by the forward)
 //   dX  = [dY_1 | .. | dY_n | P_1..n] [W_1; ..; W_n; A_1..n]
 //         ONE 256x256-tile GEMM over the K-concatenation of every adapter's
 //         dY with its W plus the stacked rank-r terms (K = sum(out) + n r).
-// The MLP backward first forms dH = dY_D W_D + P_D A_D with the SwiGLU
-// backward fused into that GEMM's epilogue (gate / up read there, d_gate /
-// d_up written in bf16; sigmoid recomputed), then treats (d_gate, d_up) as
-// the output grads of the gate / up adapters. Split-K partials are summed in
-// a fixed order, so every gradient is bit-reproducible.
+// The MLP backward first forms dH = dY_D W_D + P_D A_D (bf16), runs the
+// SwiGLU backward over it in place (sigmoid recomputed), then treats
+// (d_gate, d_up) as the output grads of the gate / up adapters. Partials are
+// summed in a fixed order, so every gradient is bit-reproducible.
 #include <algorithm>
 
 #include "gemm_core.h"
@@ -27,6 +26,8 @@ namespace {
 using namespace gemm;
 
 constexpr int kTargetItems = 512;  // work items per skinny launch (~2 per CU)
+
+size_t align256(size_t b) { return (b + 255) / 256 * 256; }
 
 int pick_ksplit(int tiles, int k_len) {
   const int ktiles = (k_len + kBK - 1) / kBK;
@@ -61,7 +62,310 @@ size_t skinny_ws(int M, int N, int k_len) {
   return (size_t)splits * M * N * sizeof(float);
 }
 
-size_t align256(size_t b) { return (b + 255) / 256 * 256; }
+// ------------------------------------------------------------- dY pass --
+// One pass over an adapter's output grad dY [N, O] (bf16) gives both rank-r
+// products that read it (rank padded to 16):
+//   P  = s dY B       [N, 16]    (a reduction over O)
+//   dB = s dY^T XA    [O, 16]    (a reduction over N; XA = X A^T)
+// A workgroup of 4 waves owns a 256 x 256 tile of dY (rows m0 .., columns
+// c0 ..) and streams it through LDS in chunks of 32 rows, loaded global ->
+// LDS three chunks ahead, each chunk laid out like the GEMM engine's
+// MN-major k-tile (32 rows of 512 B; the 32-byte unit u of row r at
+// u ^ h(r)), with the chunk's 32 XA rows (1 KB) beside it. Per chunk:
+//   P:  A = the chunk's rows (ds_read_b128 of 8 columns), B = B[c][0..15]
+//       in registers (loaded once); wave w takes columns 64 w .. 64 w + 63
+//       (two k-steps of 32), the four waves' partial sums meet in LDS and
+//       the tile's fp32 partial goes to Ppart[ctile][row][16];
+//   dB: A = the chunk transposed (two ds_read_b64_tr_b16 per fragment),
+//       B = the chunk's XA rows; wave w accumulates columns 64 w .. 64 w + 63
+//       (four 16 x 16 tiles) over the tile's rows, written at the end to
+//       dBpart[rtile][col][16].
+// The partials are summed in a fixed order by dy_reduce_kernel, which also
+// applies s (bit-reproducible results). Columns past O load the last
+// valid 8 columns again and meet B = 0 / are not stored; rows past N load
+// as zeros.
+constexpr int kDyRows = 256, kDyCols = 256, kDyChunk = 32, kDyStages = 4, kDyRank = 16;
+constexpr int kDyChunkBytes = kDyChunk * kDyCols * 2;  // 16 KB
+constexpr int kDyXaBytes = kDyChunk * kDyRank * 2;     // 1 KB
+constexpr int kDyStageBytes = kDyChunkBytes + kDyXaBytes;
+constexpr int kDyMaxAdapters = 3;
+// 5 loads per wave per chunk (4 x 1 KB of dY, 256 B of XA); with three
+// chunks in flight, chunk t has landed once at most 10 remain.
+constexpr int kDyWaitAhead = big::wait_vm(10);
+
+struct DyAdapter {
+  const bf16* dy;  // [N, O], row stride ldy
+  const bf16* b;   // [O, 16] (B padded to rank 16), row stride ldb
+  const bf16* xa;  // [N, 16] slice of X A^T, row stride ldxa
+  float* ppart;    // [ctiles][N][16]
+  float* dbpart;   // [rtiles][O][16]
+  int64_t ldy, ldb, ldxa;
+  int O, ctiles, first;  // first: this adapter's first workgroup
+};
+
+struct DyArgs {
+  DyAdapter ad[kDyMaxAdapters];
+  int nadp, N;
+};
+
+inline int dy_ctiles(int O) { return (O + kDyCols - 1) / kDyCols; }
+inline int dy_rtiles(int N) { return (N + kDyRows - 1) / kDyRows; }
+inline size_t dy_ppart_bytes(int N, int O) { return (size_t)dy_ctiles(O) * N * kDyRank * 4; }
+inline size_t dy_dbpart_bytes(int N, int O) { return (size_t)dy_rtiles(N) * O * kDyRank * 4; }
+
+__global__ __launch_bounds__(256) void dy_pass_kernel(const DyArgs args) {
+  __shared__ __attribute__((aligned(16))) char lds[kDyStages * kDyStageBytes];
+  __shared__ __attribute__((aligned(16))) float pred[4][kDyChunk * kDyRank];
+  const int bid = blockIdx.x;
+  const int ai = (args.nadp > 2 && bid >= args.ad[2].first) ? 2
+                 : (args.nadp > 1 && bid >= args.ad[1].first) ? 1 : 0;
+  const DyAdapter& A = ai == 0 ? args.ad[0] : ai == 1 ? args.ad[1] : args.ad[2];
+  const int local = bid - A.first;
+  const int ct = local % A.ctiles, rt = local / A.ctiles;
+  const int m0 = rt * kDyRows, c0 = ct * kDyCols;
+  const int N = args.N, O = A.O;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int rows = N - m0 < kDyRows ? N - m0 : kDyRows;
+  const int nchunks = (rows + kDyChunk - 1) / kDyChunk;
+
+  // B fragments of this wave's two k-steps: lane (n = lane % 16, k group
+  // lane / 16) holds B[c][n] for c = c0 + 64 w + 32 ks + 8 (lane / 16) + j.
+  bf16x8_t bfr[2];
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) {
+    const int cb = c0 + 64 * wave + 32 * ks + 8 * (lane >> 4);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int c = cb + j;
+      bfr[ks][j] = c < O ? A.b[(int64_t)c * A.ldb + (lane & 15)] : static_cast<bf16>(0.f);
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(big::kWaitVm0);  // before the LDS loads start counting
+
+  // Per-lane load offsets: dY group g = wave + 4 i covers chunk rows 2 g,
+  // 2 g + 1; lane l fetches the 8 columns its LDS slot holds.
+  uint32_t dyoff[4];
+  int dyrow[4];
+  {
+    const int p = lane & 31;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = 2 * (wave + 4 * i) + (lane >> 5);
+      const int h = (r & 3) | (((r >> 3) & 1) << 2);
+      int e = 8 * (2 * ((p >> 1) ^ h) + (p & 1));
+      e = c0 + e <= O - 8 ? e : O - 8 - c0;
+      dyoff[i] = (uint32_t)(((int64_t)r * A.ldy + c0 + e) * 2);
+      dyrow[i] = r;
+    }
+  }
+  // XA: wave w loads rows 8 w .. 8 w + 7 of the chunk, lane l one dword.
+  const int xarow = 8 * wave + (lane >> 3);
+  const uint32_t xaoff = (uint32_t)(((int64_t)xarow * A.ldxa + 2 * (lane & 7)) * 2);
+
+  auto chunk_loads = [&](int t, char* st) __attribute__((always_inline)) {
+    const int rbase = m0 + kDyChunk * t;
+    const rsrc_t ry = make_rsrc(reinterpret_cast<const char*>(A.dy + (int64_t)rbase * A.ldy));
+    const rsrc_t rx = make_rsrc(reinterpret_cast<const char*>(A.xa + (int64_t)rbase * A.ldxa));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const bool ok = t < nchunks && rbase + dyrow[i] < N;
+      buf_load_lds(ry, ok ? dyoff[i] : big::kOob, st + (wave + 4 * i) * 1024);
+    }
+    const bool okx = t < nchunks && rbase + xarow < N;
+    buf_load_lds_dword(rx, okx ? xaoff : big::kOob, st + kDyChunkBytes + wave * 256);
+  };
+
+  FragAddr<kMNMajor, 4> fa;
+  frag_addr_setup<kMNMajor, 4>(fa, 64 * wave, lane);
+  f32x4_t accb[4];
+#pragma unroll
+  for (int f = 0; f < 4; ++f) accb[f] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+#pragma unroll
+  for (int j = 0; j < kDyStages - 1; ++j) chunk_loads(j, lds + j * kDyStageBytes);
+
+  for (int t = 0; t < nchunks; ++t) {
+    char* cur = lds + (t % kDyStages) * kDyStageBytes;
+    __builtin_amdgcn_s_waitcnt(kDyWaitAhead);
+    __syncthreads();  // chunk t published; stage (t - 1) % 4 and pred free
+    chunk_loads(t + kDyStages - 1, lds + ((t + kDyStages - 1) % kDyStages) * kDyStageBytes);
+
+    // P: rows 16 mt + lane % 16, columns 64 w + 32 ks + 8 (lane / 16) ..
+    f32x4_t accp[2] = {f32x4_t{0.f, 0.f, 0.f, 0.f}, f32x4_t{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+      const int r = 16 * mt + (lane & 15);
+      const int h = (r & 3) | (((r >> 3) & 1) << 2);
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        const int c = 64 * wave + 32 * ks + 8 * (lane >> 4);
+        const bf16x8_t a = *reinterpret_cast<const bf16x8_t*>(
+            cur + r * 512 + (((c >> 4) ^ h) << 5) + (c & 15) * 2);
+        accp[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bfr[ks], accp[mt], 0, 0, 0);
+      }
+    }
+    // dB: B operand = XA rows 8 (lane / 16) + j of column lane % 16
+    bf16x8_t xf;
+    {
+      const bf16* xl = reinterpret_cast<const bf16*>(cur + kDyChunkBytes);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) xf[j] = xl[(8 * (lane >> 4) + j) * kDyRank + (lane & 15)];
+    }
+#pragma unroll
+    for (int f = 0; f < 4; ++f) {
+      bf16x8_t af;
+      read_big_frag<kMNMajor, 4>(af, cur, fa, f, 0);
+      read_big_frag<kMNMajor, 4>(af, cur, fa, f, 1);
+      accb[f] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, xf, accb[f], 0, 0, 0);
+    }
+    // the four waves' P partials meet in LDS; element v of tile mt is row
+    // 16 mt + 4 (lane / 16) + v, column lane % 16
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        pred[wave][(16 * mt + 4 * (lane >> 4) + v) * kDyRank + (lane & 15)] = accp[mt][v];
+    __syncthreads();
+#pragma unroll
+    for (int e = tid; e < kDyChunk * kDyRank; e += 256) {
+      const int row = m0 + kDyChunk * t + e / kDyRank;
+      if (row < N)
+        A.ppart[((int64_t)ct * N + row) * kDyRank + (e % kDyRank)] =
+            (pred[0][e] + pred[1][e]) + (pred[2][e] + pred[3][e]);
+    }
+  }
+  // dB partial: element v of tile f is column c0 + 64 w + 16 f + 4 (lane / 16) + v
+#pragma unroll
+  for (int f = 0; f < 4; ++f)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int col = c0 + 64 * wave + 16 * f + 4 * (lane >> 4) + v;
+      if (col < O) A.dbpart[((int64_t)rt * O + col) * kDyRank + (lane & 15)] = accb[f][v];
+    }
+  __builtin_amdgcn_s_waitcnt(big::kWaitVm0);  // loads past the last chunk have landed
+  __syncthreads();
+}
+
+// The fixed-order partial sums of a dY pass, every adapter's P (bf16) and dB
+// (fp32) in one launch: blockIdx.y picks the job. Same arithmetic as
+// reduce_partials_kernel (splits summed in order, then scaled); N = 16.
+struct DyReduceJob {
+  const float* part;
+  int splits, rows;
+  void* out;  // bf16 (P) or fp32 (dB), row stride ld
+  int64_t ld;
+  float scale;
+  int out_f32;
+};
+struct DyReduceArgs {
+  DyReduceJob job[2 * kDyMaxAdapters];
+};
+
+__global__ __launch_bounds__(256) void dy_reduce_kernel(const DyReduceArgs args) {
+  const DyReduceJob& j = args.job[blockIdx.y];
+  const int64_t total = (int64_t)j.rows * kDyRank;
+  for (int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x; q < total / 4;
+       q += (int64_t)gridDim.x * 256) {
+    const int64_t e = q * 4;
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    int k = 0;
+    for (; k + 4 <= j.splits; k += 4) {
+      float v[4][4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) load_n<float, 4>(j.part + (int64_t)(k + u) * total + e, v[u]);
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) acc[c] += v[u][c];
+    }
+    for (; k < j.splits; ++k) {
+      float v[4];
+      load_n<float, 4>(j.part + (int64_t)k * total + e, v);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) acc[c] += v[c];
+    }
+    const int64_t m = e / kDyRank, n = e % kDyRank;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const float r = j.scale * acc[c];
+      if (j.out_f32)
+        static_cast<float*>(j.out)[m * j.ld + n + c] = r;
+      else
+        static_cast<bf16*>(j.out)[m * j.ld + n + c] = from_f32<bf16>(r);
+    }
+  }
+}
+
+// Host side of the dY pass for up to three adapters of one layer. ws holds
+// every adapter's partials; P_i (bf16, row stride ldp) and dB_i (fp32 [O_i,
+// ldb_out]) receive s_i times the sums.
+struct DyJob {
+  const bf16* dy;
+  int64_t ldy;
+  int O;
+  const bf16* b;
+  int64_t ldb;
+  const bf16* xa;
+  int64_t ldxa;
+  float scale;
+  bf16* p;
+  int64_t ldp;
+  float* db;
+  int64_t lddb;
+};
+
+inline size_t dy_pass_ws_bytes(int N, const int* O, int n) {
+  size_t b = 0;
+  for (int i = 0; i < n; ++i)
+    b += align256(dy_ppart_bytes(N, O[i])) + align256(dy_dbpart_bytes(N, O[i]));
+  return b;
+}
+
+inline int dy_pass(int N, const DyJob* jobs, int n, char* ws, size_t ws_bytes, hipStream_t st) {
+  ML_CHECK(n >= 1 && n <= kDyMaxAdapters, "lora dY pass: 1..3 adapters");
+  int O[kDyMaxAdapters];
+  for (int i = 0; i < n; ++i) O[i] = jobs[i].O;
+  ML_CHECK(dy_pass_ws_bytes(N, O, n) <= ws_bytes, "lora dY pass: workspace too small");
+  DyArgs args{};
+  args.nadp = n;
+  args.N = N;
+  int blocks = 0;
+  char* w = ws;
+  for (int i = 0; i < n; ++i) {
+    const DyJob& j = jobs[i];
+    ML_CHECK(j.O >= 8 && j.O % 8 == 0 && j.ldy % 8 == 0 && j.ldxa % 8 == 0,
+             "lora dY pass: out features and strides must be multiples of 8");
+    DyAdapter& a = args.ad[i];
+    a.dy = j.dy;
+    a.b = j.b;
+    a.xa = j.xa;
+    a.ldy = j.ldy;
+    a.ldb = j.ldb;
+    a.ldxa = j.ldxa;
+    a.O = j.O;
+    a.ctiles = dy_ctiles(j.O);
+    a.first = blocks;
+    a.ppart = reinterpret_cast<float*>(w);
+    w += align256(dy_ppart_bytes(N, j.O));
+    a.dbpart = reinterpret_cast<float*>(w);
+    w += align256(dy_dbpart_bytes(N, j.O));
+    blocks += a.ctiles * dy_rtiles(N);
+  }
+  dy_pass_kernel<<<dim3((unsigned)blocks), 256, 0, st>>>(args);
+  ML_LAUNCH_CHECK();
+  DyReduceArgs red{};
+  for (int i = 0; i < n; ++i) {
+    const DyJob& j = jobs[i];
+    const DyAdapter& a = args.ad[i];
+    red.job[2 * i] = DyReduceJob{a.ppart, a.ctiles, N, j.p, j.ldp, j.scale, 0};
+    red.job[2 * i + 1] = DyReduceJob{a.dbpart, dy_rtiles(N), j.O, j.db, j.lddb, j.scale, 1};
+  }
+  dy_reduce_kernel<<<dim3(128, (unsigned)(2 * n)), 256, 0, st>>>(red);
+  ML_LAUNCH_CHECK();
+  return ML_OK;
+}
+
 
 }  // namespace
 }  // namespace lora
@@ -75,6 +379,11 @@ using namespace mla::gemm;
 static size_t qkv_partial_bytes(int64_t N, int64_t in_f, const int64_t* out_f, int nadp,
                                 int64_t r) {
   size_t m = lora::skinny_ws<WideCfg>((int)(nadp * r), (int)in_f, (int)N);
+  if (r == lora::kDyRank) {
+    int O[3];
+    for (int i = 0; i < nadp; ++i) O[i] = (int)out_f[i];
+    return std::max(m, lora::dy_pass_ws_bytes((int)N, O, nadp));
+  }
   for (int i = 0; i < nadp; ++i) {
     m = std::max(m, lora::skinny_ws<TallCfg>((int)N, (int)r, (int)out_f[i]));
     m = std::max(m, lora::skinny_ws<TallCfg>((int)out_f[i], (int)r, (int)N));
@@ -118,7 +427,17 @@ extern "C" int ml_lora_qkv_bwd(const void* X, int64_t n_tokens, int64_t in_featu
   const bf16* x = static_cast<const bf16*>(X);
   const bf16* xa = static_cast<const bf16*>(XA);
   int rc;
-  for (int i = 0; i < nadp; ++i) {
+  if (R == lora::kDyRank) {
+    // P_i and dB_i of the three adapters: one pass over each dY_i
+    lora::DyJob jobs[3];
+    for (int i = 0; i < nadp; ++i)
+      jobs[i] = lora::DyJob{static_cast<const bf16*>(dY[i]), out_features[i],
+                            (int)out_features[i], static_cast<const bf16*>(B[i]), R, xa + i * R,
+                            R3, scale[i], P + i * R, R3, dB[i], R};
+    rc = lora::dy_pass(N, jobs, nadp, reinterpret_cast<char*>(part), part_bytes, st);
+    if (rc) return rc;
+  }
+  for (int i = 0; i < nadp && R != lora::kDyRank; ++i) {
     const int OUT = (int)out_features[i];
     const bf16* dy = static_cast<const bf16*>(dY[i]);
     // P_i = s_i dY_i B_i: A = dY_i [N, out] K-major, B = B_i [out, r] (k = out, n = r) MN-major
@@ -158,6 +477,11 @@ static size_t mlp_partial_bytes(int64_t N, int64_t H, int64_t I, int64_t r) {
   m = std::max(m, lora::skinny_ws<TallCfg>((int)N, (int)r, (int)I));   // P_G, P_U
   m = std::max(m, lora::skinny_ws<WideCfg>((int)(2 * r), (int)H, (int)N));  // dA_GU
   m = std::max(m, lora::skinny_ws<TallCfg>((int)I, (int)r, (int)N));   // dB_G, dB_U
+  if (r == lora::kDyRank) {
+    const int OD[1] = {(int)H}, OGU[2] = {(int)I, (int)I};
+    m = std::max(m, lora::dy_pass_ws_bytes((int)N, OD, 1));
+    m = std::max(m, lora::dy_pass_ws_bytes((int)N, OGU, 2));
+  }
   return m;
 }
 
@@ -207,15 +531,23 @@ extern "C" int ml_lora_mlp_bwd(const void* X, int64_t n_tokens, int64_t hidden,
   int rc;
 
   // down projection: P_D, dA_D = P_D^T h, dB_D = s_D dY^T hA_D
-  Segment s1{{dy, H}, {static_cast<const bf16*>(BD), R}, H};
-  rc = lora::skinny<TallCfg, kKMajor, kMNMajor, bf16>(N, R, s1, PD, R, scale[2], part, part_bytes, st);
-  if (rc) return rc;
+  if (R == lora::kDyRank) {  // P_D and dB_D in one pass over dY
+    const lora::DyJob jd{dy, H, H, static_cast<const bf16*>(BD), R,
+                         static_cast<const bf16*>(hA_D), R, scale[2], PD, R, dB_D, R};
+    rc = lora::dy_pass(N, &jd, 1, reinterpret_cast<char*>(part), part_bytes, st);
+    if (rc) return rc;
+  } else {
+    Segment s1{{dy, H}, {static_cast<const bf16*>(BD), R}, H};
+    rc = lora::skinny<TallCfg, kKMajor, kMNMajor, bf16>(N, R, s1, PD, R, scale[2], part,
+                                                         part_bytes, st);
+    if (rc) return rc;
+    Segment s3{{dy, H}, {static_cast<const bf16*>(hA_D), R}, N};
+    rc = lora::skinny<TallCfg, kMNMajor, kMNMajor, float>(H, R, s3, dB_D, R, scale[2], part,
+                                                           part_bytes, st);
+    if (rc) return rc;
+  }
   Segment s2{{PD, R}, {static_cast<const bf16*>(h), I}, N};
   rc = lora::skinny<WideCfg, kMNMajor, kMNMajor, float>(R, I, s2, dA_D, I, 1.0f, part, part_bytes, st);
-  if (rc) return rc;
-  Segment s3{{dy, H}, {static_cast<const bf16*>(hA_D), R}, N};
-  rc = lora::skinny<TallCfg, kMNMajor, kMNMajor, float>(H, R, s3, dB_D, R, scale[2], part,
-                                                         part_bytes, st);
   if (rc) return rc;
   // dH = dY W_D + P_D A_D, a bf16 product as in the reference
   // (ops/fused_lora.py:230-233), written into d_gate's buffer; then the
@@ -240,7 +572,15 @@ extern "C" int ml_lora_mlp_bwd(const void* X, int64_t n_tokens, int64_t hidden,
   const void* Bs[2] = {BG, BU};
   float* dBs[2] = {dB_G, dB_U};
   const bf16* xa = static_cast<const bf16*>(XA_GU);
-  for (int i = 0; i < 2; ++i) {
+  if (R == lora::kDyRank) {  // P_G, P_U, dB_G, dB_U: one pass over each of d_gate, d_up
+    lora::DyJob jobs[2];
+    for (int i = 0; i < 2; ++i)
+      jobs[i] = lora::DyJob{dgu[i], I, I, static_cast<const bf16*>(Bs[i]), R, xa + i * R, R2,
+                            scale[i], PGU + i * R, R2, dBs[i], R};
+    rc = lora::dy_pass(N, jobs, 2, reinterpret_cast<char*>(part), part_bytes, st);
+    if (rc) return rc;
+  }
+  for (int i = 0; i < 2 && R != lora::kDyRank; ++i) {
     Segment sp{{dgu[i], I}, {static_cast<const bf16*>(Bs[i]), R}, I};
     rc = lora::skinny<TallCfg, kKMajor, kMNMajor, bf16>(N, R, sp, PGU + i * R, R2, scale[i], part,
                                                          part_bytes, st);

@@ -80,7 +80,7 @@ def run_qkv(dev, X, params, dys):
 
 
 @pytest.mark.parametrize("N,IN,OUTS,r", [(32, 128, (128, 128, 128), 8), (300, 256, (256, 128, 128), 16),
-                                         (64, 64, (64, 32, 32), 4)])
+                                         (64, 64, (64, 32, 32), 4), (77, 64, (384, 136, 8), 16)])
 def test_lora_qkv_small(dev, N, IN, OUTS, r):
     X = seeded((N, IN), 1, BF)
     params = [(*adapter(o, IN, r, 10 * i + 2, b_std=0.05), 2.0) for i, o in enumerate(OUTS)]
