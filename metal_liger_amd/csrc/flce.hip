@@ -207,28 +207,47 @@ __global__ __launch_bounds__(1024) void count_valid_kernel(const int64_t* __rest
 // In place over E [rows, V] (row stride ldE): d = (e exp(m_blk - lse) -
 // [col == label]) * mask / max(n_valid, 1), bf16. 8 columns per thread (one
 // 16-byte vector; 8 divides the 64-column partial block).
+constexpr int kDlogitUnroll = 4;
+
 __global__ __launch_bounds__(256) void dlogit_pass_kernel(bf16* __restrict__ E, int64_t ldE, int rows,
                                                           int V, const float* __restrict__ pmax,
                                                           int nblk, const float* __restrict__ lse,
                                                           const int64_t* __restrict__ labels,
                                                           int64_t ignore,
                                                           const float* __restrict__ n_valid) {
+  // Consecutive lanes take consecutive 16-byte vectors (whole cache lines
+  // per instruction); each thread holds kDlogitUnroll vectors, one grid
+  // stride apart, with every load issued before the first store.
   const int vpr = V / 8;  // vectors per row
   const int64_t total = (int64_t)rows * vpr;
+  const int64_t stride = (int64_t)gridDim.x * 256;
   const float inv = 1.0f / fmaxf(n_valid[0], 1.0f);
-  for (int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x; q < total;
-       q += (int64_t)gridDim.x * 256) {
-    const int r = (int)(q / vpr);
-    const int v0 = (int)(q - (int64_t)r * vpr) * 8;
-    const int64_t lab = labels[r];
-    const float sc = lab != ignore ? inv : 0.f;
-    const float f = exp_f(pmax[(int64_t)r * nblk + v0 / kColBlock] - lse[r]) * sc;
-    bf16* p = E + (int64_t)r * ldE + v0;
-    float e[8];
-    load_n<bf16, 8>(p, e);
+  for (int64_t q0 = (int64_t)blockIdx.x * 256 + threadIdx.x; q0 < total;
+       q0 += kDlogitUnroll * stride) {
+    float e[kDlogitUnroll][8], f[kDlogitUnroll], sc[kDlogitUnroll];
+    int v0[kDlogitUnroll];
+    int64_t lab[kDlogitUnroll];
+    bf16* p[kDlogitUnroll];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) e[k] = e[k] * f - (v0 + k == lab ? sc : 0.f);
-    store_n<bf16, 8>(p, e);
+    for (int u = 0; u < kDlogitUnroll; ++u) {
+      const int64_t q = q0 + u * stride;
+      p[u] = nullptr;
+      if (q >= total) continue;
+      const int r = (int)(q / vpr);
+      v0[u] = (int)(q - (int64_t)r * vpr) * 8;
+      lab[u] = labels[r];
+      sc[u] = lab[u] != ignore ? inv : 0.f;
+      f[u] = exp_f(pmax[(int64_t)r * nblk + v0[u] / kColBlock] - lse[r]) * sc[u];
+      p[u] = E + (int64_t)r * ldE + v0[u];
+      load_n<bf16, 8>(p[u], e[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < kDlogitUnroll; ++u) {
+      if (p[u] == nullptr) continue;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) e[u][k] = e[u][k] * f[u] - (v0[u] + k == lab[u] ? sc[u] : 0.f);
+      store_n<bf16, 8>(p[u], e[u]);
+    }
   }
 }
 
@@ -251,6 +270,8 @@ __global__ __launch_bounds__(256) void scale_bf16_kernel(bf16* __restrict__ x, i
 }
 
 // One wave per row: merge the row's partials into lse and its loss term.
+// One pass, each lane folding four partials per step into a running
+// (max, sum exp(. - max)); empty partials (s = 0: columns past V) are skipped.
 __global__ __launch_bounds__(256) void lse_reduce_kernel(
     const float* __restrict__ pmax, const float* __restrict__ psum, int nblk,
     const float* __restrict__ zy, const int64_t* __restrict__ labels, int64_t ignore, int M,
@@ -260,16 +281,31 @@ __global__ __launch_bounds__(256) void lse_reduce_kernel(
   if (row >= M) return;
   const float* pm = pmax + (int64_t)row * nblk;
   const float* ps = psum + (int64_t)row * nblk;
-  float mx = -INFINITY;
-  for (int b = lane; b < nblk; b += 64)
-    if (ps[b] > 0.f) mx = fmaxf(mx, pm[b]);
-  mx = wave_max(mx);
-  float s = 0.f;
-  for (int b = lane; b < nblk; b += 64)
-    if (ps[b] > 0.f) s += ps[b] * expf(pm[b] - mx);
-  s = wave_sum(s);
+  float mx = -INFINITY, s = 0.f;
+  for (int b0 = 4 * lane; b0 < nblk; b0 += 256) {
+    float m4[4], s4[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const bool ok = b0 + u < nblk;
+      m4[u] = ok ? pm[b0 + u] : -INFINITY;
+      s4[u] = ok ? ps[b0 + u] : 0.f;
+    }
+    float mn = mx;
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      if (s4[u] > 0.f) mn = fmaxf(mn, m4[u]);
+    if (mn == -INFINITY) continue;
+    float t = s > 0.f ? s * expf(mx - mn) : 0.f;
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      if (s4[u] > 0.f) t += s4[u] * expf(m4[u] - mn);
+    mx = mn;
+    s = t;
+  }
+  const float M_ = wave_max(mx);
+  s = wave_sum(s > 0.f ? s * expf(mx - M_) : 0.f);
   if (lane == 0) {
-    const float L = mx + logf(s);
+    const float L = M_ + logf(s);
     const int64_t lab = labels[row];
     const bool valid = lab != ignore;
     const bool inrange = lab >= 0 && lab < V;
@@ -556,7 +592,7 @@ int fwd_grad_impl(const bf16* hidden, int64_t ldh, const bf16* weight, int64_t l
     if (!grads) continue;
     {  // 3. dlogits in place
       const int64_t vec = (int64_t)Tc * (V / 8);
-      int64_t blocks = (vec + 255) / 256;
+      int64_t blocks = (vec + 256 * kDlogitUnroll - 1) / (256 * kDlogitUnroll);
       blocks = blocks < 8192 ? blocks : 8192;
       dlogit_pass_kernel<<<dim3((unsigned)blocks), 256, 0, st>>>(w.E, V, Tc, V, w.pmax, nblk,
                                                                  lse + t0, lc, ignore, n_valid);
