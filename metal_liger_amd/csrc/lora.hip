@@ -367,6 +367,157 @@ inline int dy_pass(int N, const DyJob* jobs, int n, char* ws, size_t ws_bytes, h
 }
 
 
+// ------------------------------------------------------------- P^T X pass --
+// dA = P^T X [RT, IN] for RT = 16, 32 or 48 stacked rank-16 adapters (X the
+// saved input or h, P the rank-r products): one pass over X. A workgroup of
+// 4 waves owns a 256 x 256 tile of X and streams it through LDS in chunks of
+// 32 rows (global -> LDS, three chunks ahead; the same swizzled MN-major
+// layout as the dY pass) with the chunk's 32 rows of P beside it. Per chunk,
+// wave w: B = X columns 64 w .. 64 w + 63 (transposing reads), A = P^T (P
+// rows read from LDS), RT / 16 x 4 MFMA tiles of fp32 accumulators kept over
+// the tile's rows and written as the row tile's partial part[rtile][RT][IN];
+// reduce_partials_kernel sums the row tiles in a fixed order.
+constexpr int kPxRows = 256, kPxCols = 256, kPxChunk = 32, kPxStages = 4;
+
+inline int px_rtiles(int N) { return (N + kPxRows - 1) / kPxRows; }
+inline size_t ptx_pass_ws_bytes(int N, int RT, int IN) {
+  return (size_t)px_rtiles(N) * RT * IN * sizeof(float);
+}
+
+template <int RT>
+__global__ __launch_bounds__(256) void ptx_pass_kernel(const bf16* __restrict__ P, int64_t ldp,
+                                                       const bf16* __restrict__ X, int64_t ldx,
+                                                       int N, int IN, float* __restrict__ part) {
+  constexpr int MT = RT / 16;
+  constexpr int kXBytes = kPxChunk * kPxCols * 2;  // 16 KB
+  constexpr int kPBytes = kPxChunk * RT * 2;        // 1 KB per 16 columns of P
+  constexpr int kStage = kXBytes + kPBytes;
+  constexpr int kPLoads = MT;  // 256-byte P loads per wave per chunk
+  static_assert(kPBytes == 4 * kPLoads * 256, "P chunk in whole 256-byte loads");
+  // 4 + kPLoads loads per wave per chunk; chunk t has landed once the two
+  // chunks after it remain in flight
+  constexpr int kWaitAhead = big::wait_vm(2 * (4 + kPLoads));
+  __shared__ __attribute__((aligned(16))) char lds[kPxStages * kStage];
+  const int ctiles = (IN + kPxCols - 1) / kPxCols;
+  const int ct = blockIdx.x % ctiles, rt = blockIdx.x / ctiles;
+  const int m0 = rt * kPxRows, c0 = ct * kPxCols;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int rows = N - m0 < kPxRows ? N - m0 : kPxRows;
+  const int nchunks = (rows + kPxChunk - 1) / kPxChunk;
+
+  // X: group g = wave + 4 i covers chunk rows 2 g, 2 g + 1 (columns clamped
+  // to the last valid 8); P: lane l of load j takes dword (4 j + w) 64 + l
+  // of the chunk's rows (RT / 2 dwords per row).
+  uint32_t xoff[4];
+  int xrow[4];
+  {
+    const int p = lane & 31;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = 2 * (wave + 4 * i) + (lane >> 5);
+      const int h = (r & 3) | (((r >> 3) & 1) << 2);
+      int e = 8 * (2 * ((p >> 1) ^ h) + (p & 1));
+      e = c0 + e <= IN - 8 ? e : IN - 8 - c0;
+      xoff[i] = (uint32_t)(((int64_t)r * ldx + c0 + e) * 2);
+      xrow[i] = r;
+    }
+  }
+  uint32_t poff[kPLoads];
+  int prow[kPLoads];
+#pragma unroll
+  for (int j = 0; j < kPLoads; ++j) {
+    const int d = (4 * j + wave) * 64 + lane;
+    prow[j] = d / (RT / 2);
+    poff[j] = (uint32_t)(((int64_t)prow[j] * ldp + 2 * (d % (RT / 2))) * 2);
+  }
+  auto chunk_loads = [&](int t, char* st) __attribute__((always_inline)) {
+    const int rbase = m0 + kPxChunk * t;
+    const rsrc_t rx = make_rsrc(reinterpret_cast<const char*>(X + (int64_t)rbase * ldx));
+    const rsrc_t rp = make_rsrc(reinterpret_cast<const char*>(P + (int64_t)rbase * ldp));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const bool ok = t < nchunks && rbase + xrow[i] < N;
+      buf_load_lds(rx, ok ? xoff[i] : big::kOob, st + (wave + 4 * i) * 1024);
+    }
+#pragma unroll
+    for (int j = 0; j < kPLoads; ++j) {
+      const bool ok = t < nchunks && rbase + prow[j] < N;
+      buf_load_lds_dword(rp, ok ? poff[j] : big::kOob, st + kXBytes + (4 * j + wave) * 256);
+    }
+  };
+
+  FragAddr<kMNMajor, 4> fb;
+  frag_addr_setup<kMNMajor, 4>(fb, 64 * wave, lane);
+  f32x4_t acc[MT][4];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int f = 0; f < 4; ++f) acc[mt][f] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+#pragma unroll
+  for (int j = 0; j < kPxStages - 1; ++j) chunk_loads(j, lds + j * kStage);
+  for (int t = 0; t < nchunks; ++t) {
+    const char* cur = lds + (t % kPxStages) * kStage;
+    __builtin_amdgcn_s_waitcnt(kWaitAhead);
+    __syncthreads();  // chunk t published; stage (t - 1) % 4 free
+    chunk_loads(t + kPxStages - 1, lds + ((t + kPxStages - 1) % kPxStages) * kStage);
+    bf16x8_t bx[4];
+#pragma unroll
+    for (int f = 0; f < 4; ++f) {
+      read_big_frag<kMNMajor, 4>(bx[f], cur, fb, f, 0);
+      read_big_frag<kMNMajor, 4>(bx[f], cur, fb, f, 1);
+    }
+    // A = P^T: lane (m = r index 16 mt + lane % 16, k = chunk rows 8 (lane / 16) + j)
+    const bf16* pl = reinterpret_cast<const bf16*>(cur + kXBytes);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      bf16x8_t a;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) a[j] = pl[(8 * (lane >> 4) + j) * RT + 16 * mt + (lane & 15)];
+#pragma unroll
+      for (int f = 0; f < 4; ++f)
+        acc[mt][f] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bx[f], acc[mt][f], 0, 0, 0);
+    }
+  }
+  // element v of tile (mt, f): row 16 mt + 4 (lane / 16) + v, column
+  // c0 + 64 w + 16 f + lane % 16
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int f = 0; f < 4; ++f)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int col = c0 + 64 * wave + 16 * f + (lane & 15);
+        if (col < IN)
+          part[((int64_t)rt * RT + 16 * mt + 4 * (lane >> 4) + v) * IN + col] = acc[mt][f][v];
+      }
+  __builtin_amdgcn_s_waitcnt(big::kWaitVm0);  // loads past the last chunk have landed
+  __syncthreads();
+}
+
+// dA [RT, IN] (fp32, row stride ldda) = P^T X.
+inline int ptx_pass(int N, const bf16* P, int64_t ldp, int RT, const bf16* X, int64_t ldx, int IN,
+                    float* dA, int64_t ldda, char* ws, size_t ws_bytes, hipStream_t st) {
+  ML_CHECK(RT == 16 || RT == 32 || RT == 48, "lora P^T X pass: 16, 32 or 48 rows (got %d)", RT);
+  ML_CHECK(IN >= 8 && IN % 8 == 0 && ldx % 8 == 0 && ldp % 8 == 0,
+           "lora P^T X pass: sizes and strides must be multiples of 8");
+  ML_CHECK(ptx_pass_ws_bytes(N, RT, IN) <= ws_bytes, "lora P^T X pass: workspace too small");
+  float* part = reinterpret_cast<float*>(ws);
+  const unsigned blocks = (unsigned)(px_rtiles(N) * ((IN + kPxCols - 1) / kPxCols));
+  if (RT == 16)
+    ptx_pass_kernel<16><<<dim3(blocks), 256, 0, st>>>(P, ldp, X, ldx, N, IN, part);
+  else if (RT == 32)
+    ptx_pass_kernel<32><<<dim3(blocks), 256, 0, st>>>(P, ldp, X, ldx, N, IN, part);
+  else
+    ptx_pass_kernel<48><<<dim3(blocks), 256, 0, st>>>(P, ldp, X, ldx, N, IN, part);
+  ML_LAUNCH_CHECK();
+  reduce_partials_kernel<float><<<dim3(256), 256, 0, st>>>(part, px_rtiles(N), RT, IN, dA, ldda,
+                                                           1.0f, 0.f);
+  ML_LAUNCH_CHECK();
+  return ML_OK;
+}
+
 }  // namespace
 }  // namespace lora
 }  // namespace mla
@@ -382,6 +533,7 @@ static size_t qkv_partial_bytes(int64_t N, int64_t in_f, const int64_t* out_f, i
   if (r == lora::kDyRank) {
     int O[3];
     for (int i = 0; i < nadp; ++i) O[i] = (int)out_f[i];
+    m = std::max(m, lora::ptx_pass_ws_bytes((int)N, (int)(nadp * r), (int)in_f));
     return std::max(m, lora::dy_pass_ws_bytes((int)N, O, nadp));
   }
   for (int i = 0; i < nadp; ++i) {
@@ -452,9 +604,14 @@ extern "C" int ml_lora_qkv_bwd(const void* X, int64_t n_tokens, int64_t in_featu
     if (rc) return rc;
   }
   // dA_stack = P^T X: A = P^T (MN-major, ld 3r), B = X (MN-major, ld in)
-  Segment sa{{P, R3}, {x, IN}, N};
-  rc = lora::skinny<WideCfg, kMNMajor, kMNMajor, float>(R3, IN, sa, dA, IN, 1.0f, part, part_bytes,
-                                                         st);
+  if (R == lora::kDyRank) {
+    rc = lora::ptx_pass(N, P, R3, R3, x, IN, IN, dA, IN, reinterpret_cast<char*>(part), part_bytes,
+                        st);
+  } else {
+    Segment sa{{P, R3}, {x, IN}, N};
+    rc = lora::skinny<WideCfg, kMNMajor, kMNMajor, float>(R3, IN, sa, dA, IN, 1.0f, part,
+                                                           part_bytes, st);
+  }
   if (rc) return rc;
   // dX = [dQ | dK | dV | P] [Wq; Wk; Wv; A_stack]
   Segment segs[4];
@@ -481,6 +638,8 @@ static size_t mlp_partial_bytes(int64_t N, int64_t H, int64_t I, int64_t r) {
     const int OD[1] = {(int)H}, OGU[2] = {(int)I, (int)I};
     m = std::max(m, lora::dy_pass_ws_bytes((int)N, OD, 1));
     m = std::max(m, lora::dy_pass_ws_bytes((int)N, OGU, 2));
+    m = std::max(m, lora::ptx_pass_ws_bytes((int)N, (int)r, (int)I));
+    m = std::max(m, lora::ptx_pass_ws_bytes((int)N, (int)(2 * r), (int)H));
   }
   return m;
 }
@@ -546,8 +705,14 @@ extern "C" int ml_lora_mlp_bwd(const void* X, int64_t n_tokens, int64_t hidden,
                                                            part_bytes, st);
     if (rc) return rc;
   }
-  Segment s2{{PD, R}, {static_cast<const bf16*>(h), I}, N};
-  rc = lora::skinny<WideCfg, kMNMajor, kMNMajor, float>(R, I, s2, dA_D, I, 1.0f, part, part_bytes, st);
+  if (R == lora::kDyRank) {
+    rc = lora::ptx_pass(N, PD, R, R, static_cast<const bf16*>(h), I, I, dA_D, I,
+                        reinterpret_cast<char*>(part), part_bytes, st);
+  } else {
+    Segment s2{{PD, R}, {static_cast<const bf16*>(h), I}, N};
+    rc = lora::skinny<WideCfg, kMNMajor, kMNMajor, float>(R, I, s2, dA_D, I, 1.0f, part,
+                                                           part_bytes, st);
+  }
   if (rc) return rc;
   // dH = dY W_D + P_D A_D, a bf16 product as in the reference
   // (ops/fused_lora.py:230-233), written into d_gate's buffer; then the
@@ -590,9 +755,14 @@ extern "C" int ml_lora_mlp_bwd(const void* X, int64_t n_tokens, int64_t hidden,
                                                            part_bytes, st);
     if (rc) return rc;
   }
-  Segment sa{{PGU, R2}, {x, H}, N};
-  rc = lora::skinny<WideCfg, kMNMajor, kMNMajor, float>(R2, H, sa, dA_GU, H, 1.0f, part,
-                                                         part_bytes, st);
+  if (R == lora::kDyRank) {
+    rc = lora::ptx_pass(N, PGU, R2, R2, x, H, H, dA_GU, H, reinterpret_cast<char*>(part),
+                        part_bytes, st);
+  } else {
+    Segment sa{{PGU, R2}, {x, H}, N};
+    rc = lora::skinny<WideCfg, kMNMajor, kMNMajor, float>(R2, H, sa, dA_GU, H, 1.0f, part,
+                                                           part_bytes, st);
+  }
   if (rc) return rc;
   // dX = [d_gate | d_up | P_GU] [W_G; W_U; A_GU]
   Segment segs[3] = {Segment{{dgate, I}, {static_cast<const bf16*>(WG), H}, I},
