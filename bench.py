@@ -87,6 +87,38 @@ def time_launches(fn, stream, reps):
     return a.elapsed_time(b) / reps
 
 
+def time_graph(fn, stream, reps):
+    """Average milliseconds per call of fn replayed from one captured HIP
+    graph of `reps` calls: the launches' own GPU time, without the host-side
+    argument marshalling of each call. Falls back to time_launches (and says
+    so) when the capture fails."""
+    import torch
+    try:
+        side = torch.cuda.Stream()
+        side.wait_stream(stream)
+        with torch.cuda.stream(side):
+            fn()
+        stream.wait_stream(side)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for _ in range(reps):
+                fn()
+        g.replay()
+        torch.cuda.synchronize()
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        g.replay()
+        b.record(stream)
+        torch.cuda.synchronize()
+        ms = a.elapsed_time(b) / reps
+        del g
+        return ms, "graph replay"
+    except RuntimeError:
+        return time_launches(fn, stream, reps), "eager launches (graph capture failed)"
+
+
 RMS_N, RMS_H = 8192, 2048
 RMS_FWD_BYTES = 2 * RMS_N * RMS_H * 4 + RMS_H * 4 + RMS_N * 4          # x, w in; y, rrms out
 RMS_BWD_BYTES = 3 * RMS_N * RMS_H * 4 + 2 * RMS_H * 4 + RMS_N * 4      # x, dy, w, rrms in; dx, dw out
@@ -141,6 +173,38 @@ def bench_flce(dev, stream, reps, token_chunk=None):
     torch.cuda.empty_cache()
     return {"fwd_ms": round(f_ms, 3), "bwd_ms": round(b_ms, 3), "TFLOP/s": round(tf, 1),
             "mfma_frac": round(tf / MFMA_PEAK_TFLOPS, 4), "flop": FLCE_FLOP, "token_chunk": T}
+
+
+QKN_DIR_TABLE_BYTES = 2 * RB * RS * RD * 2                  # cos + sin [B, S, D] bf16
+QKN_FWD_BYTES = 2 * RB * (RHQ + RHK) * RS * RD * 2 + QKN_DIR_TABLE_BYTES    # x in, y out
+QKN_BWD_BYTES = 3 * RB * (RHQ + RHK) * RS * RD * 2 + QKN_DIR_TABLE_BYTES    # x, dy in; dx out
+
+
+def bench_qk_norm_rope(dev, stream, reps):
+    """Qwen3 q_norm / k_norm fused with RoPE at the RoPE config: q [4, 16,
+    2048, 128], k [4, 8, 2048, 128] bf16 as HF's transposed views of the
+    projections, bf16 weights 1 + 0.1 N(0, 1), bf16 theta-1e6 tables [4,
+    2048, 128] broadcast over heads; backward with the weight gradients."""
+    import torch
+
+    from metal_liger_amd import hip_ops
+    q = gpu_randn((RB, RS, RHQ, RD), 60, dev).transpose(1, 2)
+    k = gpu_randn((RB, RS, RHK, RD), 61, dev).transpose(1, 2)
+    wq = 1.0 + 0.1 * gpu_randn((RD,), 62, dev)
+    wk = 1.0 + 0.1 * gpu_randn((RD,), 63, dev)
+    inv = hip_ops.rope_inv_freq(RD, THETA, dev)
+    ang = torch.arange(RS, device=dev, dtype=torch.float32).unsqueeze(-1) * inv
+    emb = torch.cat((ang, ang), -1).unsqueeze(0).expand(RB, RS, RD)
+    cos = emb.cos().to(torch.bfloat16).unsqueeze(1)
+    sin = emb.sin().to(torch.bfloat16).unsqueeze(1)
+    dq = gpu_randn((RB, RHQ, RS, RD), 64, dev)
+    dk = gpu_randn((RB, RHK, RS, RD), 65, dev)
+    f_ms, how = time_graph(lambda: hip_ops.qk_norm_rope_fwd(q, k, wq, wk, cos, sin, 1e-6), stream, reps)
+    b_ms, _ = time_graph(lambda: hip_ops.qk_norm_rope_bwd(q, k, wq, wk, cos, sin, 1e-6, dq, dk),
+                         stream, reps)
+    return {"fwd_us": round(f_ms * 1e3, 2), "fwd_GB/s": round(QKN_FWD_BYTES / (f_ms * 1e-3) / 1e9, 1),
+            "bwd_us": round(b_ms * 1e3, 2), "bwd_GB/s": round(QKN_BWD_BYTES / (b_ms * 1e-3) / 1e9, 1),
+            "bwd_note": "includes the dw partial-row reduction launch", "timing": how}
 
 
 def bench_lora_bwd(dev, stream, reps):
@@ -220,7 +284,7 @@ def build_train_model(dev, layers=TRAIN_LAYERS):
     lm.to(device=dev, dtype=torch.bfloat16)
     # the patcher wraps norm weights in new (trainable) Parameters, as the
     # reference's MetalLigerRMSNorm does: freeze after patching
-    model = apply_metal_liger_to_qwen3vl(PeftLike(lm))
+    model = apply_metal_liger_to_qwen3vl(PeftLike(lm), fuse_rope=True)
     for n, p in model.named_parameters():
         p.requires_grad_("lora_" in n)
     return model
@@ -229,18 +293,16 @@ def build_train_model(dev, layers=TRAIN_LAYERS):
 def bench_train_step(dev, steps=5, warmup=2):
     """4-layer Qwen3-style LoRA train step: token ids [4, 2048] uniform in
     [0, 151936), forward through the patched decoder (fused RMSNorm, SwiGLU,
-    LoRA QKV / MLP, RoPE from the rotary module's tables), next-token loss by
+    LoRA QKV / MLP, q/k norm + RoPE from the rotary module's tables), next-token loss by
     the chunked fused linear cross-entropy (labels shifted left, the last
     position of each sequence ignored), backward, AdamW on the adapters.
     Attention is torch's scaled_dot_product_attention restricted to its
     flash / memory-efficient kernels (an unavailable kernel raises instead of
     falling back to the batched-matmul path). tokens/s = 8192 / step time."""
     import torch
-    import transformers.models.qwen3.modeling_qwen3 as mq
     from torch.nn.attention import SDPBackend, sdpa_kernel
 
     from metal_liger_amd import MetalLigerFusedLinearCrossEntropy
-    from metal_liger_amd.ops.fused_rope import apply_fused_rotary
     model = build_train_model(dev)
     lm = model.base_model.model
     loss_fn = MetalLigerFusedLinearCrossEntropy(lm.lm_head)
@@ -250,9 +312,6 @@ def bench_train_step(dev, steps=5, warmup=2):
     ids = torch.randint(0, TRAIN_V, (TRAIN_B, TRAIN_S), generator=g).to(dev)
     labels = torch.cat([ids[:, 1:], torch.full((TRAIN_B, 1), -100, device=dev)], 1)
 
-    def rotary(q, k, cos, sin, unsqueeze_dim=1):
-        return apply_fused_rotary(q, k, cos.unsqueeze(unsqueeze_dim), sin.unsqueeze(unsqueeze_dim))
-
     def step():
         opt.zero_grad(set_to_none=True)
         hidden = lm.model(input_ids=ids).last_hidden_state
@@ -261,21 +320,16 @@ def bench_train_step(dev, steps=5, warmup=2):
         opt.step()
         return loss
 
-    saved_rotary = mq.apply_rotary_pos_emb
-    mq.apply_rotary_pos_emb = rotary
-    try:
-        with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
-            for _ in range(warmup):
-                loss = step()
-            torch.cuda.synchronize()
-            first = loss.item()
-            t0 = time.perf_counter()
-            for _ in range(steps):
-                loss = step()
-            torch.cuda.synchronize()
-            dt = (time.perf_counter() - t0) / steps
-    finally:
-        mq.apply_rotary_pos_emb = saved_rotary
+    with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+        for _ in range(warmup):
+            loss = step()
+        torch.cuda.synchronize()
+        first = loss.item()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            loss = step()
+        torch.cuda.synchronize()
+        dt = (time.perf_counter() - t0) / steps
     last = loss.item()
     if not (math.isfinite(first) and math.isfinite(last)):
         raise RuntimeError(f"train step: non-finite loss {first} -> {last}")
@@ -514,6 +568,7 @@ def main():
                  for n in per_op}
     breakdown["gpu_ms_per_step"] = round(gpu_ms_step, 4)
     breakdown["rmsnorm_fp32"] = bench_rmsnorm(dev, stream, reps)
+    breakdown["qk_norm_rope_bf16"] = bench_qk_norm_rope(dev, stream, reps)
     if not args.no_mfma_ops:
         breakdown["flce_fwd_bwd"] = bench_flce(dev, stream, 5)
         breakdown["lora_bwd_layer"] = bench_lora_bwd(dev, stream, 10)

@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define ML_ABI_VERSION 2
+#define ML_ABI_VERSION 3
 
 /* dtype tags */
 #define ML_F32 0
@@ -145,6 +145,53 @@ int ml_rope_table(const void* q, void* q_out, const int64_t* q_geom, const void*
 int ml_rope_pos(const void* q, void* q_out, const int64_t* q_geom, const void* k, void* k_out,
                 const int64_t* k_geom, int64_t D, const int64_t* positions, int64_t pos_sb,
                 int64_t pos_ss, const float* inv_freq, float sgn, int x_dtype, void* stream);
+
+/* ---------------------------------------------- q/k head-dim RMSNorm + RoPE
+ * Qwen3 attention's q_norm / k_norm (transformers' Qwen3RMSNorm over the head
+ * dimension) followed by rotate-half RoPE from cos/sin tables
+ * (apply_rotary_pos_emb), q and k in one launch. The reference's patcher
+ * leaves these norms unfused (patch.py:104-131 replaces only the layer
+ * norms); the fused form replaces the sequence q_norm -> transpose ->
+ * apply_rotary_pos_emb of the Qwen3 attention forward.
+ *
+ * Rows are [B, H, S, D] with D in {32, 64, 128, 256} contiguous; q and k share B,
+ * S, D, eps and the tables. Per row (fp32 arithmetic, one rounding on store):
+ *
+ *   n = x * rsqrt(mean(x^2) + eps) * w
+ *   y[j]     = n[j] c[j] - n[j+D/2] s[j]
+ *   y[j+D/2] = n[j+D/2] c[j+D/2] + n[j] s[j+D/2]          (j < D/2)
+ *
+ * x, y, the tables (and in the backward dy, dx) have dtype x_dtype; the
+ * weights w [D] have x_dtype or fp32 (w_dtype). Every base pointer is 16-byte
+ * aligned and every stride is a multiple of 16 bytes. Per-head tables (a
+ * non-zero head stride) must cover max(Hq, Hk) heads.
+ *
+ * geom (9 int64 per tensor): {B, H, S, x_sb, x_sh, x_ss, y_sb, y_sh, y_ss}.
+ * cs_geom (6 int64): {cos_sb, cos_sh, cos_ss, sin_sb, sin_sh, sin_ss}, 0 on
+ * broadcast dimensions. k may be NULL (q only).
+ */
+int ml_qk_norm_rope_fwd(const void* q, void* q_out, const int64_t* q_geom, const void* q_weight,
+                        const void* k, void* k_out, const int64_t* k_geom, const void* k_weight,
+                        int64_t D, float eps, const void* cos, const void* sin,
+                        const int64_t* cs_geom, int x_dtype, int w_dtype, void* stream);
+
+/*
+ * Backward (exact for any tables): dx from dy, and optionally dw = sum over
+ * rows of dn * x * rsqrt(mean(x^2) + eps) in w_dtype, where dn is dy rotated
+ * back. geom (12 int64 per tensor): {B, H, S, x strides (b, h, s), dy strides,
+ * dx strides}. dq_weight / dk_weight may be NULL to skip a weight gradient;
+ * when either is requested the workspace holds
+ * ml_qk_norm_rope_bwd_workspace_bytes(B, S, Hq, Hk, D) bytes. dw is summed in
+ * a fixed order (deterministic).
+ */
+size_t ml_qk_norm_rope_bwd_workspace_bytes(int64_t B, int64_t S, int64_t Hq, int64_t Hk,
+                                           int64_t D);
+int ml_qk_norm_rope_bwd(const void* q, const void* dq_out, void* dq, const int64_t* q_geom,
+                        const void* q_weight, void* dq_weight, const void* k, const void* dk_out,
+                        void* dk, const int64_t* k_geom, const void* k_weight, void* dk_weight,
+                        int64_t D, float eps, const void* cos, const void* sin,
+                        const int64_t* cs_geom, int x_dtype, int w_dtype, void* workspace,
+                        size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------- fused linear cross-entropy (FLCE)
  * Replaces _FusedLinearCrossEntropyFunction (ops/fused_linear_cross_entropy.py:

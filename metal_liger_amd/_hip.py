@@ -49,6 +49,16 @@ SIGNATURES: dict[str, tuple] = {
         _i32,
         [_p, _p, _i64p, _p, _p, _i64p, _i64, _p, _i64, _i64, _p, _f32, _i32, _p],
     ),
+    "ml_qk_norm_rope_fwd": (
+        _i32,
+        [_p, _p, _i64p, _p, _p, _p, _i64p, _p, _i64, _f32, _p, _p, _i64p, _i32, _i32, _p],
+    ),
+    "ml_qk_norm_rope_bwd_workspace_bytes": (_sz, [_i64, _i64, _i64, _i64, _i64]),
+    "ml_qk_norm_rope_bwd": (
+        _i32,
+        [_p, _p, _p, _i64p, _p, _p, _p, _p, _p, _i64p, _p, _p, _i64, _f32, _p, _p, _i64p, _i32,
+         _i32, _p, _sz, _p],
+    ),
     "ml_gemm_bf16": (
         _i32,
         [_i64, _i64, _i64, _p, _i64, _i32, _p, _i64, _i32, _p, _i64, _i32, _f32, _f32, _p],
@@ -96,7 +106,7 @@ SIGNATURES: dict[str, tuple] = {
     ),
 }
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 _lib = None
 _lock = threading.Lock()

@@ -265,6 +265,170 @@ def rope_pos(q: torch.Tensor, k: torch.Tensor | None, positions: torch.Tensor,
     return o4s[0], (o4s[1] if k is not None else None)
 
 
+# --------------------------------------------------- q/k norm + RoPE --
+
+_QKN_HEAD_DIMS = (32, 64, 128, 256)
+
+
+def _qkn_aligned(t: torch.Tensor, dims: int) -> bool:
+    """16-byte aligned base and the first `dims` strides in multiples of 16
+    bytes, with a contiguous last dimension."""
+    es = t.element_size()
+    return t.stride(-1) == 1 and t.data_ptr() % 16 == 0 and \
+        all((st * es) % 16 == 0 for st in t.stride()[:dims])
+
+
+def _qkn_rows(x: torch.Tensor, what: str) -> torch.Tensor:
+    """x as [B, H, S, D] with D contiguous, 16-byte aligned rows."""
+    if x.dim() != 4:
+        raise ValueError(f"qk_norm_rope: {what} must be [batch, heads, seq, head_dim]")
+    if not _qkn_aligned(x, 3):
+        x = x.clone(memory_format=torch.contiguous_format)
+    return x
+
+
+def _qkn_out(B: int, H: int, S: int, D: int, dtype, device) -> torch.Tensor:
+    """[B, H, S, D] view of fresh [B, S, H, D] memory (the layout of HF's
+    transposed projections)."""
+    return torch.empty(B, S, H, D, dtype=dtype, device=device).transpose(1, 2)
+
+
+def _qkn_weight(w: torch.Tensor, x_dtype, D: int, what: str) -> torch.Tensor:
+    if w.dim() != 1 or w.shape[0] != D:
+        raise ValueError(f"qk_norm_rope: {what} weight must be [{D}] (got {tuple(w.shape)})")
+    if w.dtype not in (x_dtype, torch.float32):
+        w = w.float()
+    if not _qkn_aligned(w, 0):
+        w = w.clone(memory_format=torch.contiguous_format)
+    return w
+
+
+def _qkn_table_strides(t: torch.Tensor, shape) -> list | None:
+    """Strides of t broadcast to the 4-D `shape` (0 on broadcast dims), or
+    None when t does not broadcast to it."""
+    ts = tuple(t.shape)
+    if len(ts) > 4:
+        return None
+    pad = 4 - len(ts)
+    st = t.stride()
+    out = []
+    for d in range(4):
+        if d < pad:
+            out.append(0)
+            continue
+        n = ts[d - pad]
+        if n == shape[d]:
+            out.append(st[d - pad] if n > 1 else 0)
+        elif n == 1:
+            out.append(0)
+        else:
+            return None
+    return out
+
+
+def _qkn_tables(cos: torch.Tensor, sin: torch.Tensor, x: torch.Tensor):
+    """cos/sin in x's dtype with their strides broadcast to x's [B, H, S, D]
+    shape (0 on broadcast dims): (cos, sin, 6-entry stride list)."""
+    shape = tuple(x.shape)
+    out, strides = [], []
+    for t in (cos, sin):
+        if t.dtype != x.dtype:
+            t = t.to(x.dtype)
+        st = _qkn_table_strides(t, shape)
+        if st is None:
+            raise ValueError(f"qk_norm_rope: table shape {tuple(t.shape)} does not broadcast to "
+                             f"{shape}")
+        if st[3] != 1 or t.data_ptr() % 16 or any((v * t.element_size()) % 16 for v in st[:3]):
+            t = t.clone(memory_format=torch.contiguous_format)
+            st = _qkn_table_strides(t, shape)
+        out.append(t)
+        strides.append(st)
+    cs = geom(strides[0][:3] + strides[1][:3])
+    return out[0], out[1], cs
+
+
+def _qkn_common(q, k, q_weight, k_weight, cos, sin):
+    ensure_rocm_device(q, k, q_weight, k_weight, cos, sin)
+    if q.dim() != 4 or k.dim() != 4:
+        raise ValueError("qk_norm_rope: q and k must be [batch, heads, seq, head_dim]")
+    B, _, S, D = q.shape
+    if k.shape[0] != B or k.shape[2] != S or k.shape[3] != D:
+        raise ValueError("qk_norm_rope: q and k must share batch, sequence and head_dim")
+    if k.dtype != q.dtype:
+        raise TypeError("qk_norm_rope: q and k must share a dtype")
+    if D not in _QKN_HEAD_DIMS:
+        raise ValueError(f"qk_norm_rope: head_dim must be one of {_QKN_HEAD_DIMS} (got {D})")
+    wq = _qkn_weight(q_weight, q.dtype, D, "q")
+    wk = _qkn_weight(k_weight, q.dtype, D, "k")
+    if wk.dtype != wq.dtype:
+        wq, wk = wq.float(), wk.float()
+    c4, s4, cs = _qkn_tables(cos, sin, q)
+    if k.shape[1] != q.shape[1] and (cs[1] != 0 or cs[4] != 0):
+        # the tables must not vary across heads when q and k head counts differ
+        raise ValueError("qk_norm_rope: per-head tables need equal q and k head counts")
+    return B, S, D, wq, wk, c4, s4, cs
+
+
+def qk_norm_rope_fwd(q: torch.Tensor, k: torch.Tensor, q_weight: torch.Tensor,
+                     k_weight: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, eps: float):
+    """Head-dim RMSNorm with weight (q_norm / k_norm), then rotate-half RoPE.
+
+    q, k: [B, H, S, D] in one dtype (any strides with D contiguous), D in
+    {32, 64, 128, 256}; weights [D] (x's dtype or fp32); cos/sin broadcastable to
+    q's shape (HF's [B, S, D] tables unsqueezed at dim 1), cast to x's dtype.
+    Returns (q_out, k_out) in x's dtype, [B, H, S, D] views of [B, S, H, D]
+    memory (with fp32 weights and bf16 / fp16 x, transformers' expression
+    would promote to fp32; the fused op keeps x's dtype).
+    """
+    B, S, D, wq, wk, c4, s4, cs = _qkn_common(q, k, q_weight, k_weight, cos, sin)
+    xq, xk = _qkn_rows(q, "q"), _qkn_rows(k, "k")
+    oq = _qkn_out(B, q.shape[1], S, D, q.dtype, q.device)
+    ok = _qkn_out(B, k.shape[1], S, D, q.dtype, q.device)
+    gq = geom([B, xq.shape[1], S, *xq.stride()[:3], *oq.stride()[:3]])
+    gk = geom([B, xk.shape[1], S, *xk.stride()[:3], *ok.stride()[:3]])
+    call(
+        "ml_qk_norm_rope_fwd", ptr(xq), ptr(oq), gq, ptr(wq), ptr(xk), ptr(ok), gk, ptr(wk), D,
+        float(eps), ptr(c4), ptr(s4), cs, dtype_tag(q, "q"), dtype_tag(wq, "weight"), stream_of(q),
+    )
+    return oq, ok
+
+
+def qk_norm_rope_bwd(q: torch.Tensor, k: torch.Tensor, q_weight: torch.Tensor,
+                     k_weight: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, eps: float,
+                     dq_out: torch.Tensor, dk_out: torch.Tensor, need_dq_weight: bool = True,
+                     need_dk_weight: bool = True):
+    """Returns (dq, dk, dq_weight or None, dk_weight or None): dq / dk in x's
+    dtype as [B, H, S, D] views of [B, S, H, D] memory, weight gradients in
+    the weights' dtype (summed in a fixed order)."""
+    B, S, D, wq, wk, c4, s4, cs = _qkn_common(q, k, q_weight, k_weight, cos, sin)
+    xq, xk = _qkn_rows(q, "q"), _qkn_rows(k, "k")
+    ensure_rocm_device(dq_out, dk_out)
+    if dq_out.shape != q.shape or dk_out.shape != k.shape:
+        raise ValueError("qk_norm_rope: gradient shapes must match q and k")
+    yq = _qkn_rows(dq_out.to(q.dtype), "dq")
+    yk = _qkn_rows(dk_out.to(q.dtype), "dk")
+    dq = _qkn_out(B, q.shape[1], S, D, q.dtype, q.device)
+    dk = _qkn_out(B, k.shape[1], S, D, q.dtype, q.device)
+    dwq = torch.empty(D, dtype=wq.dtype, device=q.device) if need_dq_weight else None
+    dwk = torch.empty(D, dtype=wk.dtype, device=q.device) if need_dk_weight else None
+    ws = None
+    if dwq is not None or dwk is not None:
+        wsb = _hip.query("ml_qk_norm_rope_bwd_workspace_bytes", B, S, q.shape[1], k.shape[1], D)
+        ws = torch.empty(max(wsb, 16), dtype=torch.uint8, device=q.device)
+    gq = geom([B, xq.shape[1], S, *xq.stride()[:3], *yq.stride()[:3], *dq.stride()[:3]])
+    gk = geom([B, xk.shape[1], S, *xk.stride()[:3], *yk.stride()[:3], *dk.stride()[:3]])
+    call(
+        "ml_qk_norm_rope_bwd", ptr(xq), ptr(yq), ptr(dq), gq, ptr(wq), ptr(dwq), ptr(xk), ptr(yk),
+        ptr(dk), gk, ptr(wk), ptr(dwk), D, float(eps), ptr(c4), ptr(s4), cs, dtype_tag(q, "q"),
+        dtype_tag(wq, "weight"), ptr(ws), ws.numel() if ws is not None else 0, stream_of(q),
+    )
+    if dwq is not None and dwq.dtype != q_weight.dtype:
+        dwq = dwq.to(q_weight.dtype)
+    if dwk is not None and dwk.dtype != k_weight.dtype:
+        dwk = dwk.to(k_weight.dtype)
+    return dq, dk, dwq, dwk
+
+
 # -------------------------------------------------------------------- GEMM --
 
 

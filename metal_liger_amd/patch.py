@@ -15,6 +15,7 @@ import logging
 import torch.nn as nn
 
 from metal_liger_amd.ops.fused_lora import patch_fused_lora
+from metal_liger_amd.ops.fused_qk_norm_rope import patch_qk_norm_rope
 from metal_liger_amd.ops.fused_rms_norm import MetalLigerRMSNorm
 from metal_liger_amd.ops.fused_swiglu import MetalLigerSwiGLU
 
@@ -120,9 +121,12 @@ def apply_metal_liger_to_qwen3vl(
     """Apply the fused operations to a Qwen3 / Qwen3-VL model in place and
     return it (patch.py:181-240).
 
-    fuse_rope / fuse_cross_entropy only log, as in the reference: RoPE is
-    applied with apply_fused_rotary / apply_fused_rotary_inline and the loss
-    with MetalLigerFusedLinearCrossEntropy by the caller.
+    fuse_rope: attention modules with q_norm / k_norm (Qwen3) get their
+    head-dim norms and RoPE fused into one launch (ops/fused_qk_norm_rope.py;
+    the reference only logs here). Elsewhere RoPE is applied by the caller
+    with apply_fused_rotary / apply_fused_rotary_inline, as in the reference.
+    fuse_cross_entropy only logs, as in the reference: the loss is
+    MetalLigerFusedLinearCrossEntropy, called by the trainer.
     use_optimized_generator is not part of this build (inference path).
     """
     stats = {}
@@ -134,6 +138,11 @@ def apply_metal_liger_to_qwen3vl(
         n = _replace_mlps(model)
         stats["swiglu"] = n
         logger.info(f"MetalLiger: replaced {n} MLP layers with fused SwiGLU")
+    if fuse_rope:
+        # before the LoRA patch, which wraps whatever attention forward it finds
+        n = patch_qk_norm_rope(model)
+        stats["qk_norm_rope"] = n
+        logger.info(f"MetalLiger: fused q/k norm + RoPE on {n} attention modules")
     if fuse_lora:
         n = patch_fused_lora(model)
         stats["fused_lora"] = n

@@ -107,6 +107,44 @@ def rope_tables(positions: torch.Tensor, head_dim: int, theta: float):
     return emb.cos(), emb.sin()
 
 
+# ------------------------------------------------ q/k head-dim norm + RoPE --
+# Not among the reference's ops: its patcher leaves Qwen3's q_norm / k_norm to
+# transformers (patch.py:104-131 replaces only the layer norms). Restated from
+# transformers' models/qwen3/modeling_qwen3.py as installed here
+# (Qwen3RMSNorm.forward; apply_rotary_pos_emb with rotate_half), the
+# library the reference's model boundary depends on.
+
+
+def qk_norm_rope_forward(x: torch.Tensor, weight: torch.Tensor, eps: float,
+                         cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    """rope(norm(x)) with HF's rounding sequence: the norm in fp32, cast to
+    x's dtype, times the weight; then x * cos + rotate_half(x) * sin with the
+    tables broadcast against x."""
+    xf = x.to(torch.float32)
+    var = xf.pow(2).mean(-1, keepdim=True)
+    n = weight * (xf * torch.rsqrt(var + eps)).to(x.dtype)
+    return n * cos + rotate_half(n) * sin
+
+
+def qk_norm_rope_backward(x: torch.Tensor, weight: torch.Tensor, eps: float,
+                          cos: torch.Tensor, sin: torch.Tensor, grad_out: torch.Tensor):
+    """Exact VJP of qk_norm_rope_forward in fp32 (no intermediate roundings):
+    (dx [..., D], dweight [D]), both fp32. The rotation's transpose maps
+    g * sin = [a, b] to [b, -a]; the norm's is RMSNorm's."""
+    xf, w = x.float(), weight.float()
+    g = grad_out.float()
+    c, s = cos.float(), sin.float()
+    h = x.shape[-1] // 2
+    r = torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)
+    nh = xf * r
+    gs = g * s
+    dn = g * c + torch.cat((gs[..., h:], -gs[..., :h]), dim=-1)
+    gw = dn * w
+    dx = r * (gw - nh * (gw * nh).mean(-1, keepdim=True))
+    dw = (dn * nh).reshape(-1, x.shape[-1]).sum(0)
+    return dx, dw
+
+
 # ----------------------------------------------- fused linear cross-entropy --
 
 

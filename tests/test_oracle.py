@@ -230,6 +230,68 @@ def test_rope_dtype_promotion():
     assert ref.rope_forward(x, cos.bfloat16(), sin.bfloat16()).dtype == torch.bfloat16
 
 
+# ------------------------------------------------ q/k head-dim norm + RoPE --
+
+
+def _hf_qk_norm_rope(x, weight, eps, cos, sin):
+    """transformers' own modules: Qwen3RMSNorm, then apply_rotary_pos_emb."""
+    from transformers.models.qwen3.modeling_qwen3 import Qwen3RMSNorm, apply_rotary_pos_emb
+    norm = Qwen3RMSNorm(x.shape[-1], eps=eps).to(weight.dtype)
+    with torch.no_grad():
+        norm.weight.copy_(weight)
+    n = norm(x)
+    y, _ = apply_rotary_pos_emb(n, n, cos, sin, unsqueeze_dim=1)
+    return y
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_qk_norm_rope_forward_matches_transformers(dtype):
+    B, H, S, D = 2, 3, 17, 64
+    x = randn(B, S, H, D, seed=150, dtype=dtype).transpose(1, 2)     # HF's transposed view
+    w = (1.0 + 0.1 * randn(D, seed=151)).to(dtype)
+    cos, sin = ref.rope_tables(torch.arange(S).unsqueeze(0).expand(B, S), D, 1e6)
+    cos, sin = cos.to(dtype), sin.to(dtype)                           # the rotary module's cast
+    y = ref.qk_norm_rope_forward(x, w, 1e-6, cos.unsqueeze(1), sin.unsqueeze(1))
+    assert y.dtype == dtype
+    assert torch.equal(y, _hf_qk_norm_rope(x, w, 1e-6, cos, sin))
+
+
+def test_qk_norm_rope_backward_vs_fp64_autograd():
+    B, H, S, D = 2, 2, 9, 32
+    x = randn(B, H, S, D, seed=152)
+    w = 1.0 + 0.1 * randn(D, seed=153)
+    # generic tables (halves not duplicated), so both sin halves matter
+    cos, sin = randn(B, 1, S, D, seed=154), randn(B, 1, S, D, seed=155)
+    g = randn(B, H, S, D, seed=156)
+    dx, dw = ref.qk_norm_rope_backward(x, w, 1e-6, cos, sin, g)
+    x64 = x.double().requires_grad_(True)
+    w64 = w.double().requires_grad_(True)
+    ref.qk_norm_rope_forward(x64, w64, 1e-6, cos.double(), sin.double()).backward(g.double())
+    assert close_scaled(dx, x64.grad, 1e-5)
+    assert close_scaled(dw, w64.grad, 1e-5)
+
+
+def test_qk_norm_rope_invariants():
+    S, D = 12, 16
+    x = randn(1, 2, S, D, seed=157).double()
+    w = torch.ones(D, dtype=torch.float64)
+    # identity rotation: y is x / rms(x)
+    y = ref.qk_norm_rope_forward(x, w, 0.0, torch.ones(S, D, dtype=torch.float64),
+                                 torch.zeros(S, D, dtype=torch.float64))
+    assert torch.allclose(y.pow(2).mean(-1), torch.ones(1, 2, S, dtype=torch.float64))
+    # a rotation (duplicated-half tables) keeps each pair's norm
+    ang = torch.arange(S).double().unsqueeze(-1) * ref.rope_inv_freq(D, 1e4).double()
+    emb = torch.cat((ang, ang), -1)
+    y2 = ref.qk_norm_rope_forward(x, w, 0.0, emb.cos(), emb.sin())
+    h = D // 2
+    assert torch.allclose(y2[..., :h] ** 2 + y2[..., h:] ** 2, y[..., :h] ** 2 + y[..., h:] ** 2)
+    # the backward of a pure rotation at unit weight is the inverse rotation
+    # followed by the norm's backward: dx is orthogonal to x
+    dx, _ = ref.qk_norm_rope_backward(x, w, 0.0, emb.cos(), emb.sin(), randn(1, 2, S, D, seed=158))
+    assert torch.allclose((dx.double() * x).sum(-1), torch.zeros(1, 2, S, dtype=torch.float64),
+                          atol=1e-5)
+
+
 # ----------------------------------------------- fused linear cross-entropy --
 
 
@@ -402,6 +464,22 @@ def test_planted_mistakes_fail_the_pins():
     assert torch.allclose(ref.rope_forward(xr, cos, sin).double(), good, atol=1e-5)
     assert not torch.allclose(bad1.double(), good, atol=1e-3)
     assert not torch.allclose(bad2.double(), good, atol=1e-3)
+
+    # q/k norm + RoPE backward: the rotation transposed with the wrong sign
+    xq = randn(1, 2, 5, 8, seed=124)
+    wq = 1.0 + 0.1 * randn(8, seed=125)
+    cq, sq = randn(1, 1, 5, 8, seed=126), randn(1, 1, 5, 8, seed=127)
+    gq = randn(1, 2, 5, 8, seed=128)
+    x64q = xq.double().requires_grad_(True)
+    ref.qk_norm_rope_forward(x64q, wq.double(), 1e-6, cq.double(), sq.double()).backward(gq.double())
+    gs = gq * sq
+    rq = torch.rsqrt(xq.pow(2).mean(-1, keepdim=True) + 1e-6)
+    nq = xq * rq
+    for dn, ok in ((gq * cq + torch.cat((gs[..., 4:], -gs[..., :4]), -1), True),
+                   (gq * cq + torch.cat((-gs[..., 4:], gs[..., :4]), -1), False)):
+        gw = dn * wq
+        dxq = rq * (gw - nq * (gw * nq).mean(-1, keepdim=True))
+        assert close_scaled(dxq, x64q.grad, 1e-5) == ok
 
     # FLCE: forgetting the mask in the mean, or the one-hot subtraction
     hh, ww, lab = flce_inputs(seed=130)

@@ -86,3 +86,70 @@ def test_reference_import_paths():
         assert callable(getattr(metal_liger_ext, f))
     m = torch.nn.Linear(2, 2)
     assert metal_liger.apply_compile(m) is m
+
+
+def apply_rotary_pos_emb(q, k, cos, sin, unsqueeze_dim=1):
+    """Module-level rotary of this test file, for _NoRotaryAttention below."""
+    return q, k
+
+
+class _NoRotaryAttention(torch.nn.Module):
+    """An attention-like module with q_norm / k_norm whose forward never
+    reaches apply_rotary_pos_emb."""
+
+    def __init__(self, d=32):
+        super().__init__()
+        from transformers.models.qwen3.modeling_qwen3 import Qwen3RMSNorm
+        self.q_proj = torch.nn.Linear(d, d)
+        self.q_norm = Qwen3RMSNorm(d)
+        self.k_norm = Qwen3RMSNorm(d)
+        self.head_dim = d
+
+    def forward(self, x):
+        return self.q_norm(self.q_proj(x))
+
+
+def test_qk_norm_rope_patch_defers_norms_to_the_rotary_step(monkeypatch):
+    """fuse_rope routes Qwen3 attention's q_norm / k_norm into the rotary step
+    of the same forward. With the fused op swapped for the oracle on the CPU,
+    the patched model's logits equal the unpatched model's bit for bit, an
+    unpatched instance in the same process keeps transformers' own rotary,
+    and a forward that never reaches the rotary raises."""
+    import copy
+
+    import metal_liger_amd.ops.fused_qk_norm_rope as fq
+    from oracle import reference_ops as ref
+    calls = []
+
+    def oracle_fused(q, k, q_norm, k_norm, cos, sin, unsqueeze_dim=1):
+        calls.append(q.shape)
+        c, s = cos.unsqueeze(unsqueeze_dim), sin.unsqueeze(unsqueeze_dim)
+        return (ref.qk_norm_rope_forward(q, q_norm.weight, q_norm.variance_epsilon, c, s),
+                ref.qk_norm_rope_forward(k, k_norm.weight, k_norm.variance_epsilon, c, s))
+
+    monkeypatch.setattr(fq, "apply_fused_qk_norm_rope", oracle_fused)
+    lm = qwen_tiny.build(seed=5, lora=False, peft_wrap=False)
+    with torch.no_grad():
+        for layer in lm.model.layers:           # non-trivial norm weights
+            layer.self_attn.q_norm.weight.normal_(1.0, 0.1)
+            layer.self_attn.k_norm.weight.normal_(1.0, 0.1)
+    other = copy.deepcopy(lm)
+    ids = torch.randint(0, 512, (2, 24), generator=torch.Generator().manual_seed(2))
+    with torch.no_grad():
+        want = lm(input_ids=ids).logits
+    keys = list(lm.state_dict())
+    assert fq.patch_qk_norm_rope(lm) == 2
+    assert fq.patch_qk_norm_rope(lm) == 0                            # idempotent
+    assert list(lm.state_dict()) == keys
+    with torch.no_grad():
+        got = lm(input_ids=ids).logits
+        got_other = other(input_ids=ids).logits
+    assert calls == [(2, 4, 24, 32)] * 2                             # one call per layer
+    assert torch.equal(got, want)
+    assert torch.equal(got_other, want)
+    assert "q_norm" not in lm.model.layers[0].self_attn.__dict__     # shadow removed
+
+    bad = _NoRotaryAttention()
+    assert fq.patch_qk_norm_rope(bad) == 1
+    with pytest.raises(RuntimeError, match="did not call apply_rotary_pos_emb"):
+        bad(torch.randn(2, 32))
