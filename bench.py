@@ -346,8 +346,10 @@ def pmc_probe(dev):
     1 GiB buffer (the calibration: a plain copy reads and writes exactly
     1 GiB each), then 5 launches each of the SwiGLU backward and forward on
     gate, up, dy [8192, 6144] bf16, RoPE (positions, in-kernel cos/sin) on
-    q [4, 16, 2048, 128], k [4, 8, 2048, 128] bf16, and RMSNorm forward and
-    backward on x [8192, 2048] fp32."""
+    q [4, 16, 2048, 128], k [4, 8, 2048, 128] bf16, RMSNorm forward and
+    backward on x [8192, 2048] fp32, and the fused q/k norm + RoPE forward
+    and backward (with weight gradients) on the same q, k as HF's transposed
+    views with bf16 tables [4, 2048, 128]."""
     import torch
 
     from metal_liger_amd import hip_ops
@@ -364,6 +366,12 @@ def pmc_probe(dev):
     w = 1.0 + 0.1 * gpu_randn((RMS_H,), 41, dev, dtype=torch.float32)
     gx = gpu_randn((RMS_N, RMS_H), 42, dev, dtype=torch.float32)
     _, rrms = hip_ops.rms_norm_fwd(x, w, 1e-6)
+    hq = gpu_randn((RB, RS, RHQ, RD), 60, dev).transpose(1, 2)
+    hk = gpu_randn((RB, RS, RHK, RD), 61, dev).transpose(1, 2)
+    nwq = 1.0 + 0.1 * gpu_randn((RD,), 62, dev)
+    nwk = 1.0 + 0.1 * gpu_randn((RD,), 63, dev)
+    cos = gpu_randn((RB, 1, RS, RD), 64, dev)
+    sin = gpu_randn((RB, 1, RS, RD), 65, dev)
     torch.cuda.synchronize()
     for _ in range(3):
         dst.copy_(src)
@@ -372,12 +380,15 @@ def pmc_probe(dev):
                lambda: hip_ops.swiglu_fwd(gate, up),
                lambda: hip_ops.rope_pos(q, k, pos, inv, 1.0),
                lambda: hip_ops.rms_norm_fwd(x, w, 1e-6),
-               lambda: hip_ops.rms_norm_bwd(x, w, gx, rrms, 1e-6)):
+               lambda: hip_ops.rms_norm_bwd(x, w, gx, rrms, 1e-6),
+               lambda: hip_ops.qk_norm_rope_fwd(hq, hk, nwq, nwk, cos, sin, 1e-6),
+               lambda: hip_ops.qk_norm_rope_bwd(hq, hk, nwq, nwk, cos, sin, 1e-6, q, k)):
         for _ in range(5):
             fn()
         torch.cuda.synchronize()
     print("pmc probe: 3 x 1 GiB copy; 5 x each of swiglu_bwd, swiglu_fwd [8192, 6144] bf16, "
-          "rope_pos q/k bf16, rms_norm fwd, bwd [8192, 2048] fp32", flush=True)
+          "rope_pos q/k bf16, rms_norm fwd, bwd [8192, 2048] fp32, qk_norm_rope fwd, bwd bf16",
+          flush=True)
 
 
 def pmc_mfma_probe(dev):
