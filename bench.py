@@ -284,7 +284,7 @@ def build_train_model(dev, layers=TRAIN_LAYERS):
     lm.to(device=dev, dtype=torch.bfloat16)
     # the patcher wraps norm weights in new (trainable) Parameters, as the
     # reference's MetalLigerRMSNorm does: freeze after patching
-    model = apply_metal_liger_to_qwen3vl(PeftLike(lm), fuse_rope=True)
+    model = apply_metal_liger_to_qwen3vl(PeftLike(lm), fuse_rope=True, fuse_cross_entropy=True)
     for n, p in model.named_parameters():
         p.requires_grad_("lora_" in n)
     return model
@@ -293,29 +293,30 @@ def build_train_model(dev, layers=TRAIN_LAYERS):
 def bench_train_step(dev, steps=5, warmup=2):
     """4-layer Qwen3-style LoRA train step: token ids [4, 2048] uniform in
     [0, 151936), forward through the patched decoder (fused RMSNorm, SwiGLU,
-    LoRA QKV / MLP, q/k norm + RoPE from the rotary module's tables), next-token loss by
-    the chunked fused linear cross-entropy (labels shifted left, the last
-    position of each sequence ignored), backward, AdamW on the adapters.
+    LoRA QKV / MLP, q/k norm + RoPE from the rotary module's tables),
+    next-token loss from model(input_ids, labels=input_ids) by the chunked
+    fused linear cross-entropy (transformers' label shift: the last position
+    of each sequence ignored; no logits formed), backward, AdamW on the
+    adapters.
     Attention is torch's scaled_dot_product_attention restricted to its
     flash / memory-efficient kernels (an unavailable kernel raises instead of
     falling back to the batched-matmul path). tokens/s = 8192 / step time."""
     import torch
     from torch.nn.attention import SDPBackend, sdpa_kernel
 
-    from metal_liger_amd import MetalLigerFusedLinearCrossEntropy
     model = build_train_model(dev)
-    lm = model.base_model.model
-    loss_fn = MetalLigerFusedLinearCrossEntropy(lm.lm_head)
+    model.train()
     params = [p for p in model.parameters() if p.requires_grad]
     opt = torch.optim.AdamW(params, lr=1e-4, foreach=True)
     g = torch.Generator().manual_seed(0)
     ids = torch.randint(0, TRAIN_V, (TRAIN_B, TRAIN_S), generator=g).to(dev)
-    labels = torch.cat([ids[:, 1:], torch.full((TRAIN_B, 1), -100, device=dev)], 1)
 
     def step():
         opt.zero_grad(set_to_none=True)
-        hidden = lm.model(input_ids=ids).last_hidden_state
-        loss = loss_fn(hidden, labels)
+        out = model(input_ids=ids, labels=ids)
+        if out.logits is not None:
+            raise RuntimeError("train step: the fused loss hook did not run")
+        loss = out.loss
         loss.backward()
         opt.step()
         return loss
@@ -337,7 +338,7 @@ def bench_train_step(dev, steps=5, warmup=2):
     return {"layers": TRAIN_LAYERS, "tokens": n_tok, "ms_per_step": round(dt * 1e3, 2),
             "tokens_per_s": round(n_tok / dt, 1), "loss_first": round(first, 4),
             "loss_last": round(last, 4), "steps": steps, "warmup": warmup,
-            "includes": "fwd + FLCE loss + bwd + AdamW on LoRA params",
+            "includes": "fwd + FLCE loss (model(input_ids, labels=input_ids)) + bwd + AdamW on LoRA params",
             "attention": "torch SDPA (flash / mem-efficient)"}
 
 

@@ -5,7 +5,7 @@ The [tokens, vocab] logits never exist. When gradients are needed, the
 forward computes the loss and both gradients in one pass over token chunks,
 with every logit computed once (three MFMA GEMMs in all):
 
-* per chunk, the logits GEMM's epilogue reduces each 128-column slice to
+* per chunk, the logits GEMM's epilogue reduces each 64-column slice to
   per-row (max, sum-exp) partials (the reference's online logsumexp,
   :39-55) and stores exp(z - max) in bf16; a row pass forms lse and the
   masked loss; an elementwise pass turns the stored values into dlogits =
@@ -23,10 +23,20 @@ computed. dW is skipped when the lm_head weight is frozen.
 Semantics kept from the reference: labels are not shifted; ignore_index
 tokens contribute nothing; the mean divides by max(#valid, 1) (all-ignored
 batches give loss 0); the loss is fp32; no bias gradient is returned.
+
+``patch_causal_lm_loss(model)`` goes one step further than the reference
+(whose patcher only logs for ``fuse_cross_entropy``, patch.py:230-232): a
+causal LM called with ``labels`` while training gets its loss from the fused
+op, with transformers' label shift and ``num_items_in_batch`` handling, and
+never forms the logits.
 """
+
+import contextvars
+import inspect
 
 import torch
 import torch.nn as nn
+import torch.nn.functional as F
 
 from metal_liger_amd import hip_ops
 
@@ -99,3 +109,111 @@ class MetalLigerFusedLinearCrossEntropy(nn.Module):
             hidden_flat, self.weight, labels_flat,
             self.bias, self.ignore_index, self.chunk_size
         )
+
+
+# ------------------------------------------------------ causal-LM loss hook --
+
+_LOSS_STATE: contextvars.ContextVar = contextvars.ContextVar("metal_liger_flce_loss", default=None)
+
+
+def _identity(x):
+    return x
+
+
+def causal_lm_loss(hidden_states: torch.Tensor, lm_head: nn.Linear, labels: torch.Tensor,
+                   num_items_in_batch=None, ignore_index: int = -100,
+                   shift_labels: torch.Tensor = None, chunk_size: int = 8192) -> torch.Tensor:
+    """transformers' ForCausalLMLoss over lm_head(hidden_states) without the
+    logits: labels shifted left (the last position ignored) unless
+    shift_labels is given; mean over the valid tokens, or their sum divided
+    by num_items_in_batch when that is given. All-ignored batches give 0 (the
+    reference's clamp) where torch's mean would give NaN."""
+    if shift_labels is None:
+        labels = F.pad(labels, (0, 1), value=ignore_index)
+        shift_labels = labels[..., 1:]
+    h = hidden_states.reshape(-1, hidden_states.shape[-1])
+    y = shift_labels.reshape(-1).to(h.device)
+    if y.shape[0] != h.shape[0]:
+        raise ValueError(f"fused causal-LM loss: {y.shape[0]} labels for {h.shape[0]} positions")
+    loss = _FusedLinearCrossEntropyFunction.apply(h, lm_head.weight, y, lm_head.bias,
+                                                  ignore_index, chunk_size)
+    if num_items_in_batch is not None:
+        n_valid = (y != ignore_index).sum().to(loss.dtype)
+        if torch.is_tensor(num_items_in_batch):
+            num_items_in_batch = num_items_in_batch.to(loss.device)
+        loss = loss * n_valid / num_items_in_batch
+    return loss
+
+
+def _eligible_lm(mod: nn.Module) -> bool:
+    head = getattr(mod, "lm_head", None)
+    cfg = getattr(mod, "config", None)
+    return (isinstance(head, nn.Linear) and hasattr(mod, "loss_function") and
+            getattr(cfg, "final_logit_softcapping", None) is None)
+
+
+def _make_lm_forward(lm: nn.Module, orig_fwd, chunk_size: int):
+    try:
+        sig = inspect.signature(orig_fwd)
+    except (TypeError, ValueError):
+        sig = None
+
+    def labels_of(args, kwargs):
+        if "labels" in kwargs or sig is None:
+            return kwargs.get("labels")
+        try:
+            return sig.bind_partial(*args, **kwargs).arguments.get("labels")
+        except TypeError:
+            return None
+
+    def forward(*args, **kwargs):
+        if not lm.training or labels_of(args, kwargs) is None:
+            return orig_fwd(*args, **kwargs)
+        head = lm.lm_head
+        state = {"used": False}
+
+        def loss_fn(logits, labels, vocab_size=None, **kw):
+            # logits are the final hidden states here (lm_head is shadowed)
+            state["used"] = True
+            return causal_lm_loss(logits, head, labels, kw.get("num_items_in_batch"),
+                                  kw.get("ignore_index", -100), kw.get("shift_labels"), chunk_size)
+
+        token = _LOSS_STATE.set(state)
+        had = "_loss_function" in lm.__dict__
+        prev = lm.__dict__.get("_loss_function")
+        lm.__dict__["lm_head"] = _identity
+        lm.__dict__["_loss_function"] = loss_fn
+        try:
+            out = orig_fwd(*args, **kwargs)
+        finally:
+            lm.__dict__.pop("lm_head", None)
+            if had:
+                lm.__dict__["_loss_function"] = prev
+            else:
+                lm.__dict__.pop("_loss_function", None)
+            _LOSS_STATE.reset(token)
+        if not state["used"]:
+            raise RuntimeError(f"fused causal-LM loss: {type(lm).__name__}.forward did not call "
+                               "loss_function with the labels")
+        if hasattr(out, "logits"):
+            out.logits = None  # the field held the hidden states
+        return out
+
+    return forward
+
+
+def patch_causal_lm_loss(model: nn.Module, chunk_size: int = 8192) -> int:
+    """Routes the training loss of every causal LM in `model` (a module with
+    an nn.Linear ``lm_head``, transformers' ``loss_function`` and no final
+    logit soft-capping) through the fused linear cross-entropy: in training
+    mode with ``labels``, its forward returns the loss with ``logits=None``;
+    otherwise it is unchanged. Modules are not replaced. Returns the number
+    of patched modules."""
+    count = 0
+    for mod in model.modules():
+        if getattr(mod, "_metal_liger_flce_loss", False) or not _eligible_lm(mod):
+            continue
+        mod.forward = _make_lm_forward(mod, mod.forward, chunk_size)
+        mod._metal_liger_flce_loss = True
+        count += 1
+    return count

@@ -14,6 +14,7 @@ import logging
 
 import torch.nn as nn
 
+from metal_liger_amd.ops.fused_linear_cross_entropy import patch_causal_lm_loss
 from metal_liger_amd.ops.fused_lora import patch_fused_lora
 from metal_liger_amd.ops.fused_qk_norm_rope import patch_qk_norm_rope
 from metal_liger_amd.ops.fused_rms_norm import MetalLigerRMSNorm
@@ -125,8 +126,10 @@ def apply_metal_liger_to_qwen3vl(
     head-dim norms and RoPE fused into one launch (ops/fused_qk_norm_rope.py;
     the reference only logs here). Elsewhere RoPE is applied by the caller
     with apply_fused_rotary / apply_fused_rotary_inline, as in the reference.
-    fuse_cross_entropy only logs, as in the reference: the loss is
-    MetalLigerFusedLinearCrossEntropy, called by the trainer.
+    fuse_cross_entropy: the causal LM's training loss (forward with labels in
+    training mode) comes from the fused linear cross-entropy with
+    transformers' label shift, without logits (the reference only logs here;
+    MetalLigerFusedLinearCrossEntropy can still be called directly).
     use_optimized_generator is not part of this build (inference path).
     """
     stats = {}
@@ -154,8 +157,9 @@ def apply_metal_liger_to_qwen3vl(
         logger.info("MetalLiger: fused RoPE — use apply_fused_rotary() / apply_fused_rotary_inline()")
         stats["rope"] = "available"
     if fuse_cross_entropy:
-        logger.info("MetalLiger: fused CE — use MetalLigerFusedLinearCrossEntropy in trainer")
-        stats["cross_entropy"] = "available"
+        n = patch_causal_lm_loss(model)
+        stats["cross_entropy"] = n
+        logger.info(f"MetalLiger: fused linear cross-entropy loss on {n} causal LM heads")
     total = sum(v for v in stats.values() if isinstance(v, int))
     logger.info(f"MetalLiger: {total} total layers patched. Details: {stats}")
     return model

@@ -153,3 +153,51 @@ def test_qk_norm_rope_patch_defers_norms_to_the_rotary_step(monkeypatch):
     assert fq.patch_qk_norm_rope(bad) == 1
     with pytest.raises(RuntimeError, match="did not call apply_rotary_pos_emb"):
         bad(torch.randn(2, 32))
+
+
+class _OracleFLCE:
+    """Stand-in for the fused loss's autograd Function on the CPU: the
+    oracle's chunked CE (mean over valid tokens, 0 when none is valid)."""
+
+    calls = 0
+
+    @staticmethod
+    def apply(h, w, y, b, ignore_index, chunk_size):
+        from oracle import reference_ops as ref
+        _OracleFLCE.calls += 1
+        loss, _, _ = ref.flce_forward(h, w, y, b, ignore_index, chunk_size)
+        return loss
+
+
+def test_causal_lm_loss_hook_matches_transformers(monkeypatch):
+    """fuse_cross_entropy routes a causal LM's training loss through the fused
+    op with transformers' label shift; the logits are not returned; with
+    num_items_in_batch the sum is divided by it; eval mode is unchanged."""
+    import copy
+
+    import metal_liger_amd.ops.fused_linear_cross_entropy as fl
+    monkeypatch.setattr(fl, "_FusedLinearCrossEntropyFunction", _OracleFLCE)
+    lm = qwen_tiny.build(seed=6, lora=False, peft_wrap=False)
+    ref_lm = copy.deepcopy(lm)
+    ids = torch.randint(0, 512, (2, 20), generator=torch.Generator().manual_seed(3))
+    labels = ids.clone()
+    labels[0, :5] = -100
+    lm.train()
+    ref_lm.train()
+    assert fl.patch_causal_lm_loss(lm) == 1
+    assert fl.patch_causal_lm_loss(lm) == 0                          # idempotent
+    with torch.no_grad():
+        want = ref_lm(input_ids=ids, labels=labels)
+        got = lm(input_ids=ids, labels=labels)
+        n_items = torch.tensor(50.0)
+        want_n = ref_lm(input_ids=ids, labels=labels, num_items_in_batch=n_items).loss
+        got_n = lm(input_ids=ids, labels=labels, num_items_in_batch=n_items).loss
+    assert _OracleFLCE.calls == 2 and got.logits is None
+    assert torch.allclose(got.loss, want.loss, rtol=1e-5, atol=1e-6)
+    assert torch.allclose(got_n, want_n, rtol=1e-5, atol=1e-6)
+    assert "lm_head" not in lm.__dict__ and "_loss_function" not in lm.__dict__
+    lm.eval()                                                        # eval: transformers' path
+    with torch.no_grad():
+        ev = lm(input_ids=ids, labels=labels)
+    assert ev.logits is not None and _OracleFLCE.calls == 2
+    assert torch.allclose(ev.loss, want.loss, rtol=1e-5, atol=1e-6)
