@@ -276,6 +276,23 @@ int ml_lora_qkv_bwd(const void* X, int64_t n_tokens, int64_t in_features, const 
                     void* stream);
 
 /*
+ * One projection with LoRA: the "LoRA_W" (output / o_proj) block the
+ * reference announces but never implements (ops/fused_lora.py:26), with the
+ * per-adapter formulas of _LoRA_QKV.backward (:121-171) and _lora_linear's
+ * forward (:69-82): X [n_tokens, in_features], dY [n_tokens, out_features],
+ * W [out, in], A [rank, in], B [out, rank] (bf16), scale a HOST float, XA =
+ * X A^T [n_tokens, rank] from the forward. Outputs: dX bf16 [n, in] =
+ * dY W + s (dY B) A; dA fp32 [rank, in] = s (dY B)^T X; dB fp32 [out, rank]
+ * = s dY^T XA. Same size rules as ml_lora_qkv_bwd.
+ */
+size_t ml_lora_linear_bwd_workspace_bytes(int64_t n_tokens, int64_t in_features,
+                                          int64_t out_features, int64_t rank);
+int ml_lora_linear_bwd(const void* X, int64_t n_tokens, int64_t in_features, const void* dY,
+                       int64_t out_features, const void* W, const void* A, const void* B,
+                       float scale, const void* XA, int64_t rank, void* dX, float* dA, float* dB,
+                       void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * Replaces _LoRA_MLP.backward (ops/fused_lora.py:209-266): SwiGLU MLP with
  * LoRA on gate / up / down. Saved from the forward (bf16): X [n, hidden],
  * gate / up / h [n, intermediate], XA_GU = X [A_G; A_U]^T [n, 2 rank],
@@ -284,7 +301,8 @@ int ml_lora_qkv_bwd(const void* X, int64_t n_tokens, int64_t in_features, const 
  * intermediate], BG, BU [intermediate, rank], BD [hidden, rank]; scale = HOST
  * floats {s_G, s_U, s_D}. Outputs: dX bf16 [n, hidden]; fp32 dA_GU [2 rank,
  * hidden], dA_D [rank, intermediate], dB_G, dB_U [intermediate, rank], dB_D
- * [hidden, rank]. The SwiGLU backward runs in the dH GEMM's epilogue.
+ * [hidden, rank]. dH = dY W_D + s_D (dY B_D) A_D is formed in bf16 and the
+ * SwiGLU backward then runs over it in place.
  */
 size_t ml_lora_mlp_bwd_workspace_bytes(int64_t n_tokens, int64_t hidden, int64_t intermediate,
                                        int64_t rank);

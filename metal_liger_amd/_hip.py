@@ -98,6 +98,11 @@ SIGNATURES: dict[str, tuple] = {
         [_p, _i64, _i64, ctypes.POINTER(_p), _i64p, ctypes.POINTER(_p), _p, ctypes.POINTER(_p),
          ctypes.POINTER(_f32), _p, _i64, _p, _p, ctypes.POINTER(_p), _p, _sz, _p],
     ),
+    "ml_lora_linear_bwd_workspace_bytes": (_sz, [_i64, _i64, _i64, _i64]),
+    "ml_lora_linear_bwd": (
+        _i32,
+        [_p, _i64, _i64, _p, _i64, _p, _p, _p, _f32, _p, _i64, _p, _p, _p, _p, _sz, _p],
+    ),
     "ml_lora_mlp_bwd_workspace_bytes": (_sz, [_i64, _i64, _i64, _i64]),
     "ml_lora_mlp_bwd": (
         _i32,

@@ -543,49 +543,49 @@ static size_t qkv_partial_bytes(int64_t N, int64_t in_f, const int64_t* out_f, i
   return m;
 }
 
-extern "C" size_t ml_lora_qkv_bwd_workspace_bytes(int64_t n_tokens, int64_t in_features,
-                                                  const int64_t* out_features, int64_t rank) {
-  if (n_tokens <= 0 || in_features <= 0 || rank <= 0 || !out_features) return 0;
-  return lora::align256((size_t)(n_tokens * 3 * rank) * 2) +
-         qkv_partial_bytes(n_tokens, in_features, out_features, 3, rank);
+// Backward of nadp (1..3) adapters that share the input X: P_i and dB_i by
+// one pass over each dY_i (rank 16) or split-K skinny products, dA = P^T X,
+// and dX = [dY_1 | ... | P] [W_1; ...; A_stack] as one K-concatenated GEMM.
+static size_t adapters_bwd_ws_bytes(int64_t N, int64_t IN, const int64_t* out_f, int nadp,
+                                    int64_t r) {
+  return lora::align256((size_t)(N * nadp * r) * 2) + qkv_partial_bytes(N, IN, out_f, nadp, r);
 }
 
-extern "C" int ml_lora_qkv_bwd(const void* X, int64_t n_tokens, int64_t in_features,
-                               const void* const* dY, const int64_t* out_features,
-                               const void* const* W, const void* A_stack, const void* const* B,
-                               const float* scale, const void* XA, int64_t rank, void* dX,
-                               float* dA, float* const* dB, void* workspace,
-                               size_t workspace_bytes, void* stream) {
-  const int nadp = 3;
-  ML_CHECK(n_tokens > 0 && in_features > 0 && rank > 0, "lora qkv: bad sizes");
-  ML_CHECK(n_tokens < (1LL << 31) && in_features < (1LL << 31), "lora qkv: sizes too large");
-  ML_CHECK(in_features % 8 == 0 && rank % 8 == 0, "lora qkv: in_features and rank must be multiples of 8");
+static int adapters_bwd(const char* what, int nadp, const void* X, int64_t n_tokens,
+                        int64_t in_features, const void* const* dY, const int64_t* out_features,
+                        const void* const* W, const void* A_stack, const void* const* B,
+                        const float* scale, const void* XA, int64_t rank, void* dX, float* dA,
+                        float* const* dB, void* workspace, size_t workspace_bytes,
+                        hipStream_t st) {
+  ML_CHECK(n_tokens > 0 && in_features > 0 && rank > 0, "%s: bad sizes", what);
+  ML_CHECK(n_tokens < (1LL << 31) && in_features < (1LL << 31), "%s: sizes too large", what);
+  ML_CHECK(in_features % 8 == 0 && rank % 8 == 0,
+           "%s: in_features and rank must be multiples of 8", what);
   ML_CHECK(X && dY && out_features && W && A_stack && B && scale && XA && dX && dA && dB,
-           "lora qkv: null pointer");
+           "%s: null pointer", what);
   for (int i = 0; i < nadp; ++i) {
-    ML_CHECK(dY[i] && W[i] && B[i] && dB[i], "lora qkv: null pointer for adapter %d", i);
+    ML_CHECK(dY[i] && W[i] && B[i] && dB[i], "%s: null pointer for adapter %d", what, i);
     ML_CHECK(out_features[i] > 0 && out_features[i] % 8 == 0 && out_features[i] < (1LL << 31),
-             "lora qkv: out_features[%d] must be a positive multiple of 8", i);
+             "%s: out_features[%d] must be a positive multiple of 8", what, i);
   }
-  const size_t need = ml_lora_qkv_bwd_workspace_bytes(n_tokens, in_features, out_features, rank);
-  ML_CHECK(workspace && workspace_bytes >= need, "lora qkv: workspace too small (%zu < %zu)",
+  const size_t need = adapters_bwd_ws_bytes(n_tokens, in_features, out_features, nadp, rank);
+  ML_CHECK(workspace && workspace_bytes >= need, "%s: workspace too small (%zu < %zu)", what,
            workspace_bytes, need);
-  hipStream_t st = (hipStream_t)stream;
-  const int N = (int)n_tokens, IN = (int)in_features, R = (int)rank, R3 = 3 * (int)rank;
+  const int N = (int)n_tokens, IN = (int)in_features, R = (int)rank, RS = nadp * (int)rank;
   char* ws = static_cast<char*>(workspace);
-  bf16* P = reinterpret_cast<bf16*>(ws);  // [N, 3r], column block i = s_i dY_i B_i
-  float* part = reinterpret_cast<float*>(ws + lora::align256((size_t)N * R3 * 2));
-  const size_t part_bytes = workspace_bytes - lora::align256((size_t)N * R3 * 2);
+  bf16* P = reinterpret_cast<bf16*>(ws);  // [N, nadp r], column block i = s_i dY_i B_i
+  float* part = reinterpret_cast<float*>(ws + lora::align256((size_t)N * RS * 2));
+  const size_t part_bytes = workspace_bytes - lora::align256((size_t)N * RS * 2);
   const bf16* x = static_cast<const bf16*>(X);
   const bf16* xa = static_cast<const bf16*>(XA);
   int rc;
   if (R == lora::kDyRank) {
-    // P_i and dB_i of the three adapters: one pass over each dY_i
+    // P_i and dB_i of every adapter: one pass over each dY_i
     lora::DyJob jobs[3];
     for (int i = 0; i < nadp; ++i)
       jobs[i] = lora::DyJob{static_cast<const bf16*>(dY[i]), out_features[i],
                             (int)out_features[i], static_cast<const bf16*>(B[i]), R, xa + i * R,
-                            R3, scale[i], P + i * R, R3, dB[i], R};
+                            RS, scale[i], P + i * R, RS, dB[i], R};
     rc = lora::dy_pass(N, jobs, nadp, reinterpret_cast<char*>(part), part_bytes, st);
     if (rc) return rc;
   }
@@ -594,35 +594,74 @@ extern "C" int ml_lora_qkv_bwd(const void* X, int64_t n_tokens, int64_t in_featu
     const bf16* dy = static_cast<const bf16*>(dY[i]);
     // P_i = s_i dY_i B_i: A = dY_i [N, out] K-major, B = B_i [out, r] (k = out, n = r) MN-major
     Segment sp{{dy, OUT}, {static_cast<const bf16*>(B[i]), R}, OUT};
-    rc = lora::skinny<TallCfg, kKMajor, kMNMajor, bf16>(N, R, sp, P + i * R, R3, scale[i], part,
+    rc = lora::skinny<TallCfg, kKMajor, kMNMajor, bf16>(N, R, sp, P + i * R, RS, scale[i], part,
                                                          part_bytes, st);
     if (rc) return rc;
-    // dB_i = s_i dY_i^T XA_i: A = dY_i^T (MN-major, ld out), B = XA_i (MN-major, ld 3r)
-    Segment sb{{dy, OUT}, {xa + i * R, R3}, N};
+    // dB_i = s_i dY_i^T XA_i: A = dY_i^T (MN-major, ld out), B = XA_i (MN-major, ld nadp r)
+    Segment sb{{dy, OUT}, {xa + i * R, RS}, N};
     rc = lora::skinny<TallCfg, kMNMajor, kMNMajor, float>(OUT, R, sb, dB[i], R, scale[i], part,
                                                            part_bytes, st);
     if (rc) return rc;
   }
-  // dA_stack = P^T X: A = P^T (MN-major, ld 3r), B = X (MN-major, ld in)
+  // dA_stack = P^T X: A = P^T (MN-major, ld nadp r), B = X (MN-major, ld in)
   if (R == lora::kDyRank) {
-    rc = lora::ptx_pass(N, P, R3, R3, x, IN, IN, dA, IN, reinterpret_cast<char*>(part), part_bytes,
+    rc = lora::ptx_pass(N, P, RS, RS, x, IN, IN, dA, IN, reinterpret_cast<char*>(part), part_bytes,
                         st);
   } else {
-    Segment sa{{P, R3}, {x, IN}, N};
-    rc = lora::skinny<WideCfg, kMNMajor, kMNMajor, float>(R3, IN, sa, dA, IN, 1.0f, part,
+    Segment sa{{P, RS}, {x, IN}, N};
+    rc = lora::skinny<WideCfg, kMNMajor, kMNMajor, float>(RS, IN, sa, dA, IN, 1.0f, part,
                                                            part_bytes, st);
   }
   if (rc) return rc;
-  // dX = [dQ | dK | dV | P] [Wq; Wk; Wv; A_stack]
+  // dX = [dY_1 | ... | dY_nadp | P] [W_1; ...; W_nadp; A_stack]
   Segment segs[4];
   for (int i = 0; i < nadp; ++i)
     segs[i] = Segment{{static_cast<const bf16*>(dY[i]), out_features[i]},
                       {static_cast<const bf16*>(W[i]), IN}, (int)out_features[i]};
-  segs[3] = Segment{{P, R3}, {static_cast<const bf16*>(A_stack), IN}, R3};
+  segs[nadp] = Segment{{P, RS}, {static_cast<const bf16*>(A_stack), IN}, RS};
   Problem pb;
-  rc = make_problem<BigCfg>(pb, N, IN, 4, segs, kKMajor, kMNMajor, 0);
+  rc = make_problem<BigCfg>(pb, N, IN, nadp + 1, segs, kKMajor, kMNMajor, 0);
   if (rc) return rc;
   return launch_store<bf16>(pb, kKMajor, kMNMajor, dX, IN, 1.0f, 0.0f, st);
+}
+
+extern "C" size_t ml_lora_qkv_bwd_workspace_bytes(int64_t n_tokens, int64_t in_features,
+                                                  const int64_t* out_features, int64_t rank) {
+  if (n_tokens <= 0 || in_features <= 0 || rank <= 0 || !out_features) return 0;
+  return adapters_bwd_ws_bytes(n_tokens, in_features, out_features, 3, rank);
+}
+
+extern "C" int ml_lora_qkv_bwd(const void* X, int64_t n_tokens, int64_t in_features,
+                               const void* const* dY, const int64_t* out_features,
+                               const void* const* W, const void* A_stack, const void* const* B,
+                               const float* scale, const void* XA, int64_t rank, void* dX,
+                               float* dA, float* const* dB, void* workspace,
+                               size_t workspace_bytes, void* stream) {
+  return adapters_bwd("lora qkv", 3, X, n_tokens, in_features, dY, out_features, W, A_stack, B,
+                      scale, XA, rank, dX, dA, dB, workspace, workspace_bytes,
+                      (hipStream_t)stream);
+}
+
+// ------------------------------------------------------ single projection --
+
+extern "C" size_t ml_lora_linear_bwd_workspace_bytes(int64_t n_tokens, int64_t in_features,
+                                                     int64_t out_features, int64_t rank) {
+  if (n_tokens <= 0 || in_features <= 0 || rank <= 0 || out_features <= 0) return 0;
+  return adapters_bwd_ws_bytes(n_tokens, in_features, &out_features, 1, rank);
+}
+
+extern "C" int ml_lora_linear_bwd(const void* X, int64_t n_tokens, int64_t in_features,
+                                  const void* dY, int64_t out_features, const void* W,
+                                  const void* A, const void* B, float scale, const void* XA,
+                                  int64_t rank, void* dX, float* dA, float* dB, void* workspace,
+                                  size_t workspace_bytes, void* stream) {
+  const void* dys[1] = {dY};
+  const void* ws_[1] = {W};
+  const void* bs[1] = {B};
+  float* dbs[1] = {dB};
+  return adapters_bwd("lora linear", 1, X, n_tokens, in_features, dys, &out_features, ws_, A, bs,
+                      &scale, XA, rank, dX, dA, dbs, workspace, workspace_bytes,
+                      (hipStream_t)stream);
 }
 
 // ------------------------------------------------------------------- MLP --

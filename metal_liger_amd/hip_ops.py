@@ -674,6 +674,25 @@ def lora_qkv_bwd(x2, dys, ws_, a_stack, bs, scales, xa, rank):
     return dX, dA, dBs
 
 
+def lora_linear_bwd(x2, dy, w, a, b, scale, xa, rank):
+    """One LoRA projection's backward: (dX bf16 [N, in], dA fp32 [r, in],
+    dB fp32 [out, r])."""
+    ensure_rocm_device(x2, dy, w, a, b, xa)
+    N, IN = x2.shape
+    OUT = int(dy.shape[1])
+    dev = x2.device
+    dX = torch.empty(N, IN, dtype=torch.bfloat16, device=dev)
+    dA = torch.empty(rank, IN, dtype=torch.float32, device=dev)
+    dB = torch.empty(OUT, rank, dtype=torch.float32, device=dev)
+    wsb = _hip.query("ml_lora_linear_bwd_workspace_bytes", N, IN, OUT, rank)
+    ws = torch.empty(max(wsb, 16), dtype=torch.uint8, device=dev)
+    call(
+        "ml_lora_linear_bwd", ptr(x2), N, IN, ptr(dy), OUT, ptr(w), ptr(a), ptr(b), float(scale),
+        ptr(xa), rank, ptr(dX), ptr(dA), ptr(dB), ptr(ws), ws.numel(), stream_of(x2),
+    )
+    return dX, dA, dB
+
+
 def lora_mlp_bwd(x2, gate, up, h, dy, wg, wu, wd, a_gu, a_d, bg, bu, bd, scales, xa_gu, ha_d, rank):
     """Returns (dX, dA_GU [2r, H], dA_D [r, I], dB_G [I, r], dB_U [I, r], dB_D [H, r])."""
     ensure_rocm_device(x2, gate, up, h, dy, wg, wu, wd, a_gu, a_d, bg, bu, bd, xa_gu, ha_d)

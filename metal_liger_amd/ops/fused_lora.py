@@ -3,14 +3,17 @@
 X is saved once per fused block (as in the reference), and the backward of
 each block is a single call into the HIP library:
 
-* QKV (`_LoRA_QKV`): the rank-r products P_i = s_i dY_i B_i, dA = P^T X and
-  dB_i = s_i dY_i^T (X A_i^T) run on narrow MFMA tiles with split-K; the
-  shared dX is ONE MFMA GEMM over the K-concatenation
+* QKV (`_LoRA_QKV`): P_i = s_i dY_i B_i and dB_i = s_i dY_i^T (X A_i^T)
+  come from one streaming pass over each dY_i, dA = P^T X from one pass
+  over X (rank 16; other ranks use split-K products on narrow MFMA tiles);
+  the shared dX is ONE MFMA GEMM over the K-concatenation
   [dQ | dK | dV | P] x [Wq; Wk; Wv; A_q; A_k; A_v].
-* MLP (`_LoRA_MLP`): dH = dY W_D + s (dY B_D) A_D comes from one MFMA GEMM
-  whose epilogue applies the SwiGLU backward (sigmoid recomputed), writing
-  d_gate / d_up; then the gate / up adapters as above, and dX as one GEMM
-  over [d_gate | d_up | P] x [W_G; W_U; A_G; A_U].
+* MLP (`_LoRA_MLP`): dH = dY W_D + s (dY B_D) A_D in one MFMA GEMM, the
+  SwiGLU backward over it in place (sigmoid recomputed), writing d_gate /
+  d_up; then the gate / up adapters as above, and dX as one GEMM over
+  [d_gate | d_up | P] x [W_G; W_U; A_G; A_U].
+* One projection (`_LoRA_W`, o_proj): the same backward with one adapter;
+  the patcher routes an attention's o_proj through it when it has LoRA.
 
 The forward passes also run on the MFMA engine: X A^T for the stacked A
 matrices (saved for the backward, where the reference recomputed it) and
@@ -204,6 +207,51 @@ class _LoRA_MLP(torch.autograd.Function):
                 None, dA_D[:r], dB_D[:, :r], None)          # DW, DA, DB, DS
 
 
+class _LoRA_W(torch.autograd.Function):
+    """One projection with LoRA, X W^T + s (X A^T) B^T: the "LoRA_W" block
+    (output / o_proj) the reference announces but does not implement
+    (ops/fused_lora.py:26), with _lora_linear's forward (:69-82) and the
+    per-adapter backward of _LoRA_QKV (:121-171). X A^T is saved from the
+    forward; the backward is one library call (rank-r products and one
+    K-concatenated dX GEMM [dY | P] x [W; A])."""
+
+    @staticmethod
+    def forward(ctx, X, W, A, B, S):
+        _check_bf16(X, "LoRA projection")
+        shape = X.shape
+        Xf = hip_ops._bf16_rows(X.reshape(-1, shape[-1]))
+        r = A.shape[0]
+        rp = _pad_rank(r)
+        a = _stack_a([A], rp)
+        xa = hip_ops.lora_xa(Xf, a)                              # [N, rp], saved
+        Wc = hip_ops._bf16_rows(W.detach())
+        Bp = _pad_b(B, rp)
+        scale = float(S)
+        out = hip_ops.lora_linear_out(Xf, Wc, xa, Bp * scale if scale != 1.0 else Bp)
+        ctx.save_for_backward(Xf, xa, a, Wc, Bp)
+        ctx.scale = scale
+        ctx.rank, ctx.rank_p = r, rp
+        ctx.orig_shape = shape
+        return out.view(*shape[:-1], -1)
+
+    @staticmethod
+    def backward(ctx, dY):
+        Xf, xa, a, Wc, Bp = ctx.saved_tensors
+        r, rp = ctx.rank, ctx.rank_p
+        dy = hip_ops._bf16_rows(dY.reshape(-1, dY.shape[-1]))
+        dX, dA, dB = hip_ops.lora_linear_bwd(Xf, dy, Wc, a, Bp, ctx.scale, xa, rp)
+        return dX.view(*ctx.orig_shape), None, dA[:r], dB[:, :r], None
+
+
+def apply_fused_lora_linear(linear, X: torch.Tensor) -> torch.Tensor:
+    """One LoRA projection (e.g. o_proj) through _LoRA_W; the module's own
+    forward when it has no LoRA adapter."""
+    W, A, B, S = _get_lora_params(linear)
+    if A is None:
+        return linear(X)
+    return _LoRA_W.apply(X, W, A, B, S)
+
+
 def apply_fused_lora_qkv(attn_module, X: torch.Tensor):
     """Fused Q+K+V LoRA projections of an attention module
     (ops/fused_lora.py:269-295); plain module calls when any projection has
@@ -285,23 +333,30 @@ def patch_fused_lora(model: nn.Module) -> int:
 
             if has_q and has_k and has_v:
                 orig_fwd = attn.forward
+                # o_proj with LoRA goes through _LoRA_W (the reference's
+                # patcher leaves it to PEFT)
+                o_proj = getattr(attn, 'o_proj', None)
+                fuse_o = o_proj is not None and _get_lora_params(o_proj)[1] is not None
 
-                def _make_fused_forward(orig_fwd):
+                def _make_fused_forward(orig_fwd, o_proj, fuse_o):
                     def _fused_forward(self_attn, hidden_states, *args, **kwargs):
                         Q, K, V = apply_fused_lora_qkv(self_attn, hidden_states)
                         self_attn.__dict__['q_proj'] = lambda x: Q
                         self_attn.__dict__['k_proj'] = lambda x: K
                         self_attn.__dict__['v_proj'] = lambda x: V
+                        if fuse_o:
+                            self_attn.__dict__['o_proj'] = lambda x: apply_fused_lora_linear(o_proj, x)
                         try:
                             return orig_fwd(hidden_states, *args, **kwargs)
                         finally:
                             self_attn.__dict__.pop('q_proj', None)
                             self_attn.__dict__.pop('k_proj', None)
                             self_attn.__dict__.pop('v_proj', None)
+                            self_attn.__dict__.pop('o_proj', None)
 
                     return _fused_forward
 
-                attn.forward = types.MethodType(_make_fused_forward(orig_fwd), attn)
+                attn.forward = types.MethodType(_make_fused_forward(orig_fwd, o_proj, fuse_o), attn)
                 attn._metal_liger_fused_lora = True
                 patched += 1
 

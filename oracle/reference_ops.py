@@ -256,6 +256,21 @@ def lora_qkv_backward(X, dQ, dK, dV, QW, QA, QB, QS, KW, KA, KB, KS, VW, VA, VB,
     return dX, dQA, dQB, dKA, dKB, dVA, dVB
 
 
+def lora_linear_backward(X, dY, W, A, B, s):
+    """One LoRA projection (the "LoRA_W" block of ops/fused_lora.py:26, which
+    the reference does not implement): the per-adapter terms of
+    _LoRA_QKV.backward (ops/fused_lora.py:121-171) for a single adapter.
+    Returns (dX, dA, dB)."""
+    shp = X.shape
+    Xf = X.reshape(-1, shp[-1])
+    dY = dY.reshape(-1, dY.shape[-1])
+    dt = dY.dtype
+    A_c, B_c = A.to(dt), B.to(dt)
+    dA, dB = _lora_grads(dY, Xf, A_c, B_c, s)
+    dX = torch.mm(dY, W) + torch.mm(torch.mm(dY, B_c), A_c) * s
+    return dX.view(*shp), dA, dB
+
+
 def lora_mlp_forward(X, GW, GA, GB, GS, UW, UA, UB, US, DW, DA, DB, DS):
     """ops/fused_lora.py:183-207. Returns (out, gate, up, h)."""
     shp = X.shape

@@ -236,6 +236,32 @@ def test_lora_mlp_config(dev):
         check(Bd.grad.float(), fdAB[2 * i + 1], rdAB[2 * i + 1], f"mlp dB[{i}] config")
 
 
+@pytest.mark.parametrize("N,IN,OUT,r", [(300, 256, 128, 16), (77, 64, 384, 8), (8192, 2048, 2048, 16)])
+def test_lora_linear_single_projection(dev, N, IN, OUT, r):
+    """_LoRA_W (one projection, e.g. o_proj; the last case is the Qwen3-2B
+    o_proj) against the oracle, forward and backward."""
+    from metal_liger_amd.ops.fused_lora import _LoRA_W
+    X = seeded((N, IN), 3, BF)
+    W, A, B = adapter(OUT, IN, r, 20, b_std=0.05)
+    dY = seeded((N, OUT), 21, BF)
+    Xd = X.to(dev).requires_grad_(True)
+    Ad = A.to(dev).requires_grad_(True)
+    Bd = B.to(dev).requires_grad_(True)
+    out = _LoRA_W.apply(Xd, W.to(dev), Ad, Bd, 2.0)
+    out.backward(dY.to(dev))
+    on = dev if N >= 8192 else torch.device("cpu")
+    Xo, Wo, Ao, Bo, dYo = (t.to(on) for t in (X, W, A, B, dY))
+    rout = ref.lora_linear(Xo, Wo, Ao, Bo, 2.0)
+    fout = ref.lora_linear(Xo.float(), Wo.float(), Ao.float(), Bo.float(), 2.0)
+    rdX, rdA, rdB = ref.lora_linear_backward(Xo, dYo, Wo, Ao, Bo, 2.0)
+    fdX, fdA, fdB = ref.lora_linear_backward(Xo.float(), dYo.float(), Wo.float(), Ao.float(),
+                                             Bo.float(), 2.0)
+    check(out, fout, rout, "out")
+    check(Xd.grad, fdX, rdX, "dX")
+    check(Ad.grad.float(), fdA, rdA, "dA")
+    check(Bd.grad.float(), fdB, rdB, "dB")
+
+
 def test_lora_rejects_fp32(dev):
     from metal_liger_amd.ops.fused_lora import _LoRA_QKV
     X = torch.randn(4, 64, device=dev)

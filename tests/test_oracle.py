@@ -383,6 +383,22 @@ def test_lora_qkv_vs_fp64_autograd():
         assert torch.allclose(dAB[2 * i + 1].double(), B.grad, atol=1e-4, rtol=1e-3)
 
 
+def test_lora_linear_backward_vs_fp64_autograd():
+    X = randn(40, 96, seed=90)
+    W, A, B = lora_params(64, 96, 8, 91, scale_b=0.5)
+    dY = randn(40, 64, seed=92)
+    dX, dA, dB = ref.lora_linear_backward(X, dY, W, A, B, 2.0)
+    X64 = X.double().requires_grad_(True)
+    A64 = A.double().requires_grad_(True)
+    B64 = B.double().requires_grad_(True)
+    out = X64 @ W.double().t() + (X64 @ A64.t()) @ B64.t() * 2.0
+    assert torch.allclose(ref.lora_linear(X, W, A, B, 2.0).double(), out, atol=1e-4, rtol=1e-3)
+    out.backward(dY.double())
+    assert torch.allclose(dX.double(), X64.grad, atol=1e-4, rtol=1e-3)
+    assert torch.allclose(dA.double(), A64.grad, atol=1e-4, rtol=1e-3)
+    assert torch.allclose(dB.double(), B64.grad, atol=1e-4, rtol=1e-3)
+
+
 def test_lora_special_cases():
     X = randn(3, 5, 32, seed=90)
     W, A, B = lora_params(24, 32, 4, 91)
