@@ -556,27 +556,24 @@ def main():
     wall = time.perf_counter() - t0
     gpu_ms_step = e0.elapsed_time(e1) / args.steps
 
-    # Per-kernel launch duration: events on the kernel's stream around a
-    # batch of back-to-back launches of that kernel alone.
+    # Per-kernel launch duration: HIP events on the kernel's stream around
+    # 20 back-to-back launches of that kernel alone, eagerly and replayed
+    # from a captured graph; the smaller of the two is kept (eager launches
+    # of the ~17 us RoPE kernel are timed through each call's host-side
+    # argument marshalling, a graph adds ~1.5 us between its nodes).
     reps = 20
-    per_op = {}
+    per_op, how = {}, {}
     for name, fn in ops.items():
-        fn()
-        a = torch.cuda.Event(enable_timing=True)
-        b = torch.cuda.Event(enable_timing=True)
-        a.record(stream)
-        for _ in range(reps):
-            fn()
-        b.record(stream)
-        torch.cuda.synchronize()
-        per_op[name] = a.elapsed_time(b) / reps
+        eager = time_launches(fn, stream, reps)
+        graph, gh = time_graph(fn, stream, reps)
+        per_op[name], how[name] = (graph, gh) if graph < eager else (eager, "eager launches")
 
     ms_step = wall * 1e3 / args.steps
     value = STEP_BYTES / (wall / args.steps) / 1e9
     op_bytes = {"swiglu_fwd": SWIGLU_FWD_BYTES, "swiglu_bwd": SWIGLU_BWD_BYTES,
                 "rope_fwd": ROPE_DIR_BYTES, "rope_bwd": ROPE_DIR_BYTES}
     breakdown = {n: {"us": round(per_op[n] * 1e3, 2),
-                     "GB/s": round(op_bytes[n] / (per_op[n] * 1e-3) / 1e9, 1)}
+                     "GB/s": round(op_bytes[n] / (per_op[n] * 1e-3) / 1e9, 1), "timing": how[n]}
                  for n in per_op}
     breakdown["gpu_ms_per_step"] = round(gpu_ms_step, 4)
     breakdown["rmsnorm_fp32"] = bench_rmsnorm(dev, stream, reps)
@@ -598,6 +595,7 @@ def main():
         "traffic": load_traffic(),
         "algorithmic_bytes_per_launch": SWIGLU_BWD_BYTES,
         "avg_launch_us": round(dom_ms * 1e3, 2),
+        "timing": how["swiglu_bwd"],
     }
     line = {
         "metric": METRIC,

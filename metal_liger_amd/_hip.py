@@ -168,8 +168,7 @@ def ptr(t: torch.Tensor | None) -> int | None:
 
 
 def geom(vals) -> ctypes.Array:
-    arr = (ctypes.c_int64 * len(vals))(*[int(v) for v in vals])
-    return arr
+    return (ctypes.c_int64 * len(vals))(*vals)
 
 
 def ptrs(vals) -> ctypes.Array:

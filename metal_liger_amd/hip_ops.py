@@ -133,8 +133,7 @@ def _unit_last(t: torch.Tensor) -> torch.Tensor:
 
 
 def _tensor_geom(x4: torch.Tensor, o4: torch.Tensor):
-    return geom([x4.shape[0], x4.shape[1], x4.shape[2], x4.stride(0), x4.stride(1), x4.stride(2),
-                 o4.stride(0), o4.stride(1), o4.stride(2)])
+    return geom([*x4.shape[:3], *x4.stride()[:3], *o4.stride()[:3]])
 
 
 def _table4(t: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
@@ -242,7 +241,9 @@ def rope_pos(q: torch.Tensor, k: torch.Tensor | None, positions: torch.Tensor,
     B, _, S, D = q.shape
     if D % 2 != 0:
         raise ValueError(f"rope: head dim must be even (got {D})")
-    inv = inv_freq.to(device=q.device, dtype=torch.float32).contiguous()
+    inv = inv_freq
+    if inv.device != q.device or inv.dtype != torch.float32 or not inv.is_contiguous():
+        inv = inv.to(device=q.device, dtype=torch.float32).contiguous()
     if inv.numel() != D // 2:
         raise ValueError(f"rope: inv_freq has {inv.numel()} entries, expected {D // 2}")
     p = _positions2d(positions, B, S, q.device)

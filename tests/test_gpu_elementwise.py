@@ -324,6 +324,23 @@ def test_rope_positions_properties_fp32(dev):
     assert torch.equal(y[:, :, 0], q[:, :, 0])
 
 
+def test_rope_positions_large_angles_fp32(dev):
+    """In-kernel cos/sin at positions up to 200,000 (angles up to 2e5 rad)
+    against the rotation by the exact (fp64) cos/sin of the same fp32 angles
+    the HF rotary module forms (fp32 position times fp32 inv_freq), at the
+    fp32 bar."""
+    from metal_liger_amd import hip_ops
+    B, H, S, D = 2, 3, 64, 64
+    x = seeded((B, H, S, D), 47)
+    pos = torch.randint(0, 200_000, (B, S), generator=torch.Generator().manual_seed(48))
+    inv = hip_ops.rope_inv_freq(D, 1e4, dev)
+    y, _ = hip_ops.rope_pos(x.to(dev), None, pos.to(dev), inv, 1.0)
+    ang = (pos.float().unsqueeze(-1) * inv.cpu()).double()          # fp32 angles, exact trig
+    emb = torch.cat((ang, ang), -1).unsqueeze(1)
+    want = ref.rope_forward(x.double(), emb.cos(), emb.sin())
+    assert_close(y, want.float(), "large-angle positions", torch.float32)
+
+
 def test_rope_positions_batched_and_odd_head_dim(dev):
     from metal_liger_amd import hip_ops
     B, H, S, D = 3, 2, 10, 12            # D/2 = 6: scalar path
