@@ -136,6 +136,23 @@ def _tensor_geom(x4: torch.Tensor, o4: torch.Tensor):
     return geom([*x4.shape[:3], *x4.stride()[:3], *o4.stride()[:3]])
 
 
+def rope_out(x: torch.Tensor, out_dtype) -> tuple:
+    """(x4, o4, out) for a RoPE input x: x as a 4-D view with a unit last
+    stride, its output buffer (x's layout where it has one) and the output
+    in x's shape. Shared by the launch and by the fake kernels."""
+    x4 = _unit_last(_as4d(x))
+    o4 = torch.empty_like(x4, dtype=out_dtype)
+    if o4.stride(-1) != 1:
+        o4 = torch.empty(x4.shape, dtype=out_dtype, device=x4.device)
+    return x4, o4, (o4.view(x.shape) if o4.is_contiguous() else o4.reshape(x.shape))
+
+
+def rope_out_dtype(x_dtype, cos_dtype, sin_dtype):
+    """Output dtype of the table-mode rotation: torch's promotion of x and
+    the tables (tables of different dtypes are read as fp32)."""
+    return torch.promote_types(x_dtype, cos_dtype if cos_dtype == sin_dtype else torch.float32)
+
+
 def _table4(t: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
     """cos/sin broadcast to x's shape, as a 4-D view (stride 0 on broadcast dims)."""
     if torch.broadcast_shapes(x.shape, t.shape) != x.shape:
@@ -170,13 +187,10 @@ def rope_table(q: torch.Tensor, k: torch.Tensor | None, cos: torch.Tensor, sin: 
     for x in xs:
         if x.shape[-1] != D:
             raise ValueError("rope: q and k must share the head dimension")
-        x4 = _unit_last(_as4d(x))
-        o4 = torch.empty_like(x4, dtype=out_dtype)
-        if o4.stride(-1) != 1:
-            o4 = torch.empty(x4.shape, dtype=out_dtype, device=x4.device)
+        x4, o4, out = rope_out(x, out_dtype)
         x4s.append(x4)
         o4s.append(o4)
-        outs.append(o4.view(x.shape) if o4.is_contiguous() else o4.reshape(x.shape))
+        outs.append(out)
     c4 = _table4(cos, xs[0])
     s4 = _table4(sin, xs[0])
     joint = k is not None and x4s[0].shape[0] == x4s[1].shape[0] and x4s[0].shape[2] == x4s[1].shape[2]
@@ -249,10 +263,7 @@ def rope_pos(q: torch.Tensor, k: torch.Tensor | None, positions: torch.Tensor,
     p = _positions2d(positions, B, S, q.device)
     x4s, o4s = [], []
     for x in xs:
-        x4 = _unit_last(x)
-        o4 = torch.empty_like(x4)
-        if o4.stride(-1) != 1:
-            o4 = torch.empty(x4.shape, dtype=x4.dtype, device=x4.device)
+        x4, o4, _ = rope_out(x, x.dtype)
         x4s.append(x4)
         o4s.append(o4)
     gq = _tensor_geom(x4s[0], o4s[0])
@@ -616,12 +627,26 @@ def flce_bwd(hidden, weight, labels, bias, ignore_index, lse, n_valid, grad_loss
 
 
 def _bf16_rows(t: torch.Tensor) -> torch.Tensor:
-    """bf16, row-major, 16-byte aligned rows (a copy only when needed)."""
+    """bf16, row-major with row strides in multiples of 8 (a copy only when
+    needed). Shape and stride metadata only, so torch.compile can trace it
+    inside the fused Functions; base-pointer alignment is fixed by the
+    launching wrappers (_al16)."""
     if t.dtype != torch.bfloat16:
         t = t.to(torch.bfloat16)
-    if t.dim() != 2 or t.stride(1) != 1 or t.stride(0) % 8 != 0 or t.data_ptr() % 16 != 0:
+    if t.dim() != 2 or t.stride(1) != 1 or t.stride(0) % 8 != 0:
         t = t.contiguous()
     return t
+
+
+def _al16(*ts):
+    """The tensors with 16-byte aligned base pointers (an aligned copy of any
+    that is not); None passes through."""
+    out = []
+    for t in ts:
+        if t is not None and t.data_ptr() % 16 != 0:
+            t = t.clone(memory_format=torch.contiguous_format)
+        out.append(t)
+    return out if len(out) > 1 else out[0]
 
 
 def _ksplit_for(tiles: int, k: int) -> int:
@@ -642,6 +667,7 @@ def lora_xa(x2: torch.Tensor, a_stack: torch.Tensor) -> torch.Tensor:
 def lora_linear_out(x2: torch.Tensor, w: torch.Tensor, xa: torch.Tensor,
                     sb: torch.Tensor) -> torch.Tensor:
     """X W^T + XA (s B)^T as ONE K-concatenated GEMM -> [N, out] bf16."""
+    x2, w, xa, sb = _al16(x2, w, xa, sb)
     N, K = x2.shape
     out_f = w.shape[0]
     r = xa.shape[1]
@@ -658,6 +684,8 @@ def lora_linear_out(x2: torch.Tensor, w: torch.Tensor, xa: torch.Tensor,
 def lora_qkv_bwd(x2, dys, ws_, a_stack, bs, scales, xa, rank):
     """Returns (dX bf16 [N, in], dA fp32 [3r, in], [dB_i fp32 [out_i, r]])."""
     ensure_rocm_device(x2, *dys, *ws_, a_stack, *bs, xa)
+    x2, a_stack, xa = _al16(x2, a_stack, xa)
+    dys, ws_, bs = [_al16(*t) for t in (dys, ws_, bs)]
     N, IN = x2.shape
     outs = [int(d.shape[1]) for d in dys]
     dev = x2.device
@@ -679,6 +707,7 @@ def lora_linear_bwd(x2, dy, w, a, b, scale, xa, rank):
     """One LoRA projection's backward: (dX bf16 [N, in], dA fp32 [r, in],
     dB fp32 [out, r])."""
     ensure_rocm_device(x2, dy, w, a, b, xa)
+    x2, dy, w, a, b, xa = _al16(x2, dy, w, a, b, xa)
     N, IN = x2.shape
     OUT = int(dy.shape[1])
     dev = x2.device
@@ -697,6 +726,8 @@ def lora_linear_bwd(x2, dy, w, a, b, scale, xa, rank):
 def lora_mlp_bwd(x2, gate, up, h, dy, wg, wu, wd, a_gu, a_d, bg, bu, bd, scales, xa_gu, ha_d, rank):
     """Returns (dX, dA_GU [2r, H], dA_D [r, I], dB_G [I, r], dB_U [I, r], dB_D [H, r])."""
     ensure_rocm_device(x2, gate, up, h, dy, wg, wu, wd, a_gu, a_d, bg, bu, bd, xa_gu, ha_d)
+    (x2, gate, up, h, dy, wg, wu, wd, a_gu, a_d, bg, bu, bd, xa_gu, ha_d) = _al16(
+        x2, gate, up, h, dy, wg, wu, wd, a_gu, a_d, bg, bu, bd, xa_gu, ha_d)
     N, H = x2.shape
     I = gate.shape[1]
     dev = x2.device

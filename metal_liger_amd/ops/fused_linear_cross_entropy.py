@@ -38,7 +38,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from metal_liger_amd import hip_ops
+from metal_liger_amd import _custom_ops as cops
 
 
 class _FusedLinearCrossEntropyFunction(torch.autograd.Function):
@@ -50,31 +50,36 @@ class _FusedLinearCrossEntropyFunction(torch.autograd.Function):
                 labels: torch.Tensor, bias: torch.Tensor = None,
                 ignore_index: int = -100, chunk_size: int = 8192):
         need_h, need_w = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
-        loss, lse, n_valid, dh, dw = hip_ops.flce_fwd_grad(
-            hidden, weight, labels, bias, ignore_index, need_dhidden=need_h, need_dweight=need_w)
-        ctx.save_for_backward(hidden, weight, labels, lse, n_valid, dh, dw)
+        loss, lse, n_valid, dh, dw = cops.flce_fwd_grad(
+            hidden, weight, labels, bias, ignore_index, need_h, need_w)
+        ctx.save_for_backward(hidden, weight, labels, lse, n_valid)
+        # The gradients are handed over (scaled in place) by the first
+        # backward, so they are kept out of the saved tensors, whose versions
+        # a later backward through the same graph checks.
+        ctx.grads = (cops.maybe(dh), cops.maybe(dw))
         ctx.bias = bias
         ctx.ignore_index = ignore_index
         ctx.chunk_size = chunk_size
-        ctx.grads_used = False
         return loss
 
     @staticmethod
     def backward(ctx, grad_output: torch.Tensor):
-        hidden, weight, labels, lse, n_valid, dh, dw = ctx.saved_tensors
+        hidden, weight, labels, lse, n_valid = ctx.saved_tensors
         need_h, need_w = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
-        if not ctx.grads_used:
+        if ctx.grads is not None:
             # gradients from the forward, scaled in place and handed over once
-            ctx.grads_used = True
+            dh, dw = ctx.grads
+            ctx.grads = None
             grad_hidden = dh if need_h else None
             grad_weight = dw if need_w else None
-            hip_ops.flce_scale_grads(grad_output, grad_hidden, grad_weight)
+            cops.flce_scale_grads(grad_output, grad_hidden, grad_weight)
         else:
             # a second backward through the same graph: fresh tensors from the
             # vocabulary-chunked recomputation
-            grad_hidden, grad_weight = hip_ops.flce_bwd(
+            grad_hidden, grad_weight = cops.flce_bwd(
                 hidden, weight, labels, ctx.bias, ctx.ignore_index, lse, n_valid, grad_output,
-                ctx.chunk_size, need_dhidden=need_h, need_dweight=need_w)
+                ctx.chunk_size, need_h, need_w)
+            grad_hidden, grad_weight = cops.maybe(grad_hidden), cops.maybe(grad_weight)
         if grad_hidden is not None and grad_hidden.dtype != hidden.dtype:
             grad_hidden = grad_hidden.to(hidden.dtype)
         if grad_weight is not None and grad_weight.dtype != weight.dtype:

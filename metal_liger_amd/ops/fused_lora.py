@@ -34,6 +34,7 @@ from typing import Any, Optional, Tuple  # noqa: F401
 import torch
 import torch.nn as nn
 
+from metal_liger_amd import _custom_ops as cops
 from metal_liger_amd import hip_ops
 
 logger = logging.getLogger(__name__)
@@ -96,11 +97,11 @@ def _lora_linear(X: torch.Tensor, W: torch.Tensor,
     X2 = hip_ops._bf16_rows(X.reshape(-1, shape[-1]))
     W2 = hip_ops._bf16_rows(W.detach())
     if A is None or B is None:
-        out = hip_ops.matmul(X2, W2, b_t=True, out_dtype=torch.bfloat16)
+        out = cops.linear_bf16(X2, W2)
     else:
         rp = _pad_rank(A.shape[0])
-        xa = hip_ops.lora_xa(X2, _stack_a([A], rp))
-        out = hip_ops.lora_linear_out(X2, W2, xa, _pad_b(B, rp, float(scaling)))
+        xa = cops.lora_xa(X2, _stack_a([A], rp))
+        out = cops.lora_linear_out(X2, W2, xa, _pad_b(B, rp, float(scaling)))
     return out.view(*shape[:-1], -1)
 
 
@@ -123,14 +124,14 @@ class _LoRA_QKV(torch.autograd.Function):
         r = QA.shape[0]
         rp = _pad_rank(r)
         a_stack = _stack_a([QA, KA, VA], rp)
-        xa = hip_ops.lora_xa(Xf, a_stack)                      # [N, 3 rp], saved
+        xa = cops.lora_xa(Xf, a_stack)                         # [N, 3 rp], saved
         Ws = [hip_ops._bf16_rows(W.detach()) for W in (QW, KW, VW)]
         Bs = [_pad_b(B, rp) for B in (QB, KB, VB)]
         scales = [float(QS), float(KS), float(VS)]
         outs = []
         for i in range(3):
             sb = Bs[i] * scales[i] if scales[i] != 1.0 else Bs[i]
-            outs.append(hip_ops.lora_linear_out(Xf, Ws[i], xa[:, i * rp:(i + 1) * rp], sb))
+            outs.append(cops.lora_linear_out(Xf, Ws[i], xa[:, i * rp:(i + 1) * rp], sb))
         ctx.save_for_backward(Xf, xa, a_stack, *Ws, *Bs)
         ctx.scales = scales
         ctx.rank, ctx.rank_p = r, rp
@@ -144,8 +145,8 @@ class _LoRA_QKV(torch.autograd.Function):
         r, rp = ctx.rank, ctx.rank_p
         shape = ctx.orig_shape
         dys = [hip_ops._bf16_rows(d.reshape(-1, d.shape[-1])) for d in (dQ, dK, dV)]
-        dX, dA, dBs = hip_ops.lora_qkv_bwd(Xf, dys, [QW, KW, VW], a_stack, [QB, KB, VB],
-                                           ctx.scales, xa, rp)
+        dX, dA, *dBs = cops.lora_qkv_bwd(Xf, dys, [QW, KW, VW], a_stack, [QB, KB, VB],
+                                         ctx.scales, xa, rp)
         grads = []
         for i in range(3):
             dAi = dA[i * rp:i * rp + r]
@@ -180,12 +181,12 @@ class _LoRA_MLP(torch.autograd.Function):
         a_d = _stack_a([DA], rp)                                 # [rp, inter]
         GWc, UWc, DWc = (hip_ops._bf16_rows(W.detach()) for W in (GW, UW, DW))
         BG, BU, BD = (_pad_b(B, rp) for B in (GB, UB, DB))
-        xa_gu = hip_ops.lora_xa(Xf, a_gu)                         # [N, 2 rp]
-        gate = hip_ops.lora_linear_out(Xf, GWc, xa_gu[:, :rp], BG * scales[0])
-        up = hip_ops.lora_linear_out(Xf, UWc, xa_gu[:, rp:], BU * scales[1])
-        h = hip_ops.swiglu_fwd(gate, up)                          # silu(gate) * up, bf16
-        ha_d = hip_ops.lora_xa(h, a_d)                            # [N, rp]
-        out = hip_ops.lora_linear_out(h, DWc, ha_d, BD * scales[2])
+        xa_gu = cops.lora_xa(Xf, a_gu)                            # [N, 2 rp]
+        gate = cops.lora_linear_out(Xf, GWc, xa_gu[:, :rp], BG * scales[0])
+        up = cops.lora_linear_out(Xf, UWc, xa_gu[:, rp:], BU * scales[1])
+        h = cops.swiglu_fwd(gate, up)                             # silu(gate) * up, bf16
+        ha_d = cops.lora_xa(h, a_d)                               # [N, rp]
+        out = cops.lora_linear_out(h, DWc, ha_d, BD * scales[2])
         ctx.save_for_backward(Xf, gate, up, h, xa_gu, ha_d, a_gu, a_d, GWc, UWc, DWc, BG, BU, BD)
         ctx.scales = scales
         ctx.rank, ctx.rank_p = r, rp
@@ -198,7 +199,7 @@ class _LoRA_MLP(torch.autograd.Function):
         r, rp = ctx.rank, ctx.rank_p
         shape = ctx.orig_shape
         dy = hip_ops._bf16_rows(dY.reshape(-1, dY.shape[-1]))
-        dX, dA_GU, dA_D, dB_G, dB_U, dB_D = hip_ops.lora_mlp_bwd(
+        dX, dA_GU, dA_D, dB_G, dB_U, dB_D = cops.lora_mlp_bwd(
             Xf, gate, up, h, dy, GW, UW, DW, a_gu, a_d, BG, BU, BD, ctx.scales, xa_gu, ha_d, rp)
         dX = dX.view(*shape)
         return (dX,
@@ -223,11 +224,11 @@ class _LoRA_W(torch.autograd.Function):
         r = A.shape[0]
         rp = _pad_rank(r)
         a = _stack_a([A], rp)
-        xa = hip_ops.lora_xa(Xf, a)                              # [N, rp], saved
+        xa = cops.lora_xa(Xf, a)                                 # [N, rp], saved
         Wc = hip_ops._bf16_rows(W.detach())
         Bp = _pad_b(B, rp)
         scale = float(S)
-        out = hip_ops.lora_linear_out(Xf, Wc, xa, Bp * scale if scale != 1.0 else Bp)
+        out = cops.lora_linear_out(Xf, Wc, xa, Bp * scale if scale != 1.0 else Bp)
         ctx.save_for_backward(Xf, xa, a, Wc, Bp)
         ctx.scale = scale
         ctx.rank, ctx.rank_p = r, rp
@@ -239,7 +240,7 @@ class _LoRA_W(torch.autograd.Function):
         Xf, xa, a, Wc, Bp = ctx.saved_tensors
         r, rp = ctx.rank, ctx.rank_p
         dy = hip_ops._bf16_rows(dY.reshape(-1, dY.shape[-1]))
-        dX, dA, dB = hip_ops.lora_linear_bwd(Xf, dy, Wc, a, Bp, ctx.scale, xa, rp)
+        dX, dA, dB = cops.lora_linear_bwd(Xf, dy, Wc, a, Bp, ctx.scale, xa, rp)
         return dX.view(*ctx.orig_shape), None, dA[:r], dB[:, :r], None
 
 

@@ -26,7 +26,7 @@ import logging
 import torch
 import torch.nn as nn
 
-from metal_liger_amd import hip_ops
+from metal_liger_amd import _custom_ops as cops
 
 logger = logging.getLogger(__name__)
 
@@ -38,7 +38,7 @@ class _FusedQKNormRoPEFunction(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, q, k, q_weight, k_weight, cos, sin, eps: float):
-        q_out, k_out = hip_ops.qk_norm_rope_fwd(q, k, q_weight, k_weight, cos, sin, eps)
+        q_out, k_out = cops.qk_norm_rope_fwd(q, k, q_weight, k_weight, cos, sin, eps)
         ctx.save_for_backward(q, k, q_weight, k_weight, cos, sin)
         ctx.eps = eps
         return q_out, k_out
@@ -50,11 +50,11 @@ class _FusedQKNormRoPEFunction(torch.autograd.Function):
             dq_out = torch.zeros_like(q)
         if dk_out is None:
             dk_out = torch.zeros_like(k)
-        dq, dk, dwq, dwk = hip_ops.qk_norm_rope_bwd(
+        dq, dk, dwq, dwk = cops.qk_norm_rope_bwd(
             q, k, q_weight, k_weight, cos, sin, ctx.eps, dq_out, dk_out,
-            need_dq_weight=ctx.needs_input_grad[2], need_dk_weight=ctx.needs_input_grad[3])
+            ctx.needs_input_grad[2], ctx.needs_input_grad[3])
         return (dq if ctx.needs_input_grad[0] else None, dk if ctx.needs_input_grad[1] else None,
-                dwq, dwk, None, None, None)
+                cops.maybe(dwq), cops.maybe(dwk), None, None, None)
 
 
 def _norm_eps(norm: nn.Module) -> float:

@@ -10,7 +10,7 @@ per-row rrms are saved for backward, as in the reference
 import torch
 import torch.nn as nn
 
-from metal_liger_amd import hip_ops
+from metal_liger_amd import _custom_ops as cops
 
 
 class _FusedRMSNormFunction(torch.autograd.Function):
@@ -23,7 +23,7 @@ class _FusedRMSNormFunction(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, x: torch.Tensor, weight: torch.Tensor, eps: float):
-        output, rrms = hip_ops.rms_norm_fwd(x, weight, eps)
+        output, rrms = cops.rms_norm_fwd(x, weight, eps)
         ctx.save_for_backward(x, weight, rrms.unsqueeze(-1))
         ctx.eps = eps
         return output
@@ -31,7 +31,7 @@ class _FusedRMSNormFunction(torch.autograd.Function):
     @staticmethod
     def backward(ctx, grad_output: torch.Tensor):
         x, weight, rrms = ctx.saved_tensors
-        grad_x, grad_weight = hip_ops.rms_norm_bwd(x, weight, grad_output, rrms, ctx.eps)
+        grad_x, grad_weight = cops.rms_norm_bwd(x, weight, grad_output, rrms, ctx.eps)
         return grad_x, grad_weight, None
 
 

@@ -19,6 +19,7 @@ duplicated halves (HF's layout).
 import torch
 import torch.nn as nn
 
+from metal_liger_amd import _custom_ops as cops
 from metal_liger_amd import hip_ops
 
 
@@ -27,7 +28,7 @@ class _FusedRoPEFunction(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor):
-        output, _ = hip_ops.rope_table(x, None, cos, sin, 1.0)
+        output, _ = cops.rope_table(x, None, cos, sin, 1.0)
         ctx.save_for_backward(cos, sin)
         ctx.x_dtype = x.dtype
         return output
@@ -35,7 +36,7 @@ class _FusedRoPEFunction(torch.autograd.Function):
     @staticmethod
     def backward(ctx, grad_output: torch.Tensor):
         cos, sin = ctx.saved_tensors
-        grad_x, _ = hip_ops.rope_table(grad_output, None, cos, sin, -1.0)
+        grad_x, _ = cops.rope_table(grad_output, None, cos, sin, -1.0)
         return grad_x, None, None
 
 
@@ -44,7 +45,7 @@ class _FusedRoPEQKFunction(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, q, k, cos, sin):
-        q_out, k_out = hip_ops.rope_table(q, k, cos, sin, 1.0)
+        q_out, k_out = cops.rope_table(q, k, cos, sin, 1.0)
         ctx.save_for_backward(cos, sin)
         return q_out, k_out
 
@@ -54,10 +55,10 @@ class _FusedRoPEQKFunction(torch.autograd.Function):
         if dq is None and dk is None:
             return None, None, None, None
         if dq is None:
-            return None, hip_ops.rope_table(dk, None, cos, sin, -1.0)[0], None, None
+            return None, cops.rope_table(dk, None, cos, sin, -1.0)[0], None, None
         if dk is None:
-            return hip_ops.rope_table(dq, None, cos, sin, -1.0)[0], None, None, None
-        gq, gk = hip_ops.rope_table(dq, dk, cos, sin, -1.0)
+            return cops.rope_table(dq, None, cos, sin, -1.0)[0], None, None, None
+        gq, gk = cops.rope_table(dq, dk, cos, sin, -1.0)
         return gq, gk, None, None
 
 
@@ -66,10 +67,10 @@ class _FusedRoPEPositionsFunction(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, q, k, positions, inv_freq):
-        q_out, k_out = hip_ops.rope_pos(q, k, positions, inv_freq, 1.0)
+        q_out, k_out = cops.rope_pos(q, k, positions, inv_freq, 1.0)
         ctx.save_for_backward(positions, inv_freq)
         ctx.has_k = k is not None
-        return q_out, k_out
+        return q_out, cops.maybe(k_out)
 
     @staticmethod
     def backward(ctx, dq, dk):
@@ -77,10 +78,10 @@ class _FusedRoPEPositionsFunction(torch.autograd.Function):
         if dq is None and dk is None:
             return None, None, None, None
         if dq is None:
-            return None, hip_ops.rope_pos(dk, None, positions, inv_freq, -1.0)[0], None, None
+            return None, cops.rope_pos(dk, None, positions, inv_freq, -1.0)[0], None, None
         if dk is None:
-            return hip_ops.rope_pos(dq, None, positions, inv_freq, -1.0)[0], None, None, None
-        gq, gk = hip_ops.rope_pos(dq, dk, positions, inv_freq, -1.0)
+            return cops.rope_pos(dq, None, positions, inv_freq, -1.0)[0], None, None, None
+        gq, gk = cops.rope_pos(dq, dk, positions, inv_freq, -1.0)
         return gq, gk, None, None
 
 
@@ -97,7 +98,7 @@ def _rotate_half(x: torch.Tensor) -> torch.Tensor:
 
 def _apply_rotary_fused(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
     """x * cos + rotate_half(x) * sin in one HIP launch (ops/fused_rope.py:67-75)."""
-    return hip_ops.rope_table(x, None, cos, sin, 1.0)[0]
+    return cops.rope_table(x, None, cos, sin, 1.0)[0]
 
 
 class MetalLigerRoPE(nn.Module):

@@ -9,7 +9,7 @@ while the saved tensor cost 4 bytes per element of memory and traffic.
 import torch
 import torch.nn as nn
 
-from metal_liger_amd import hip_ops
+from metal_liger_amd import _custom_ops as cops
 
 
 class _FusedSwiGLUFunction(torch.autograd.Function):
@@ -18,14 +18,14 @@ class _FusedSwiGLUFunction(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, gate: torch.Tensor, up: torch.Tensor):
-        output = hip_ops.swiglu_fwd(gate, up)
+        output = cops.swiglu_fwd(gate, up)
         ctx.save_for_backward(gate, up)
         return output
 
     @staticmethod
     def backward(ctx, grad_output: torch.Tensor):
         gate, up = ctx.saved_tensors
-        grad_gate, grad_up = hip_ops.swiglu_bwd(gate, up, grad_output)
+        grad_gate, grad_up = cops.swiglu_bwd(gate, up, grad_output)
         return grad_gate, grad_up
 
 
