@@ -140,6 +140,33 @@ def bench_rmsnorm(dev, stream, reps):
             "bwd_us": round(b_ms * 1e3, 2), "bwd_GB/s": round(RMS_BWD_BYTES / (b_ms * 1e-3) / 1e9, 1)}
 
 
+ADD_N, ADD_H = 8192, 2048
+ADD_FWD_BYTES = 4 * ADD_N * ADD_H * 2 + ADD_H * 2 + ADD_N * 4      # x, res, w in; sum, y, rrms out
+ADD_BWD_BYTES = 4 * ADD_N * ADD_H * 2 + 2 * ADD_H * 2 + ADD_N * 4  # sum, dy, dsum, w, rrms in; dx, dw out
+
+
+def bench_add_rmsnorm(dev, stream, reps):
+    """Residual add fused into RMSNorm (a decoder layer's post-attention
+    step), bf16 hidden states [8192, 2048], bf16 weight 1 + 0.1 N(0, 1),
+    eps 1e-6; beside it the unfused pair (torch's add, then the fused norm;
+    the norm's backward, then torch's add)."""
+    from metal_liger_amd import hip_ops
+    x = gpu_randn((ADD_N, ADD_H), 45, dev)
+    res = gpu_randn((ADD_N, ADD_H), 46, dev)
+    w = 1.0 + 0.1 * gpu_randn((ADD_H,), 47, dev)
+    dy = gpu_randn((ADD_N, ADD_H), 48, dev)
+    ds = gpu_randn((ADD_N, ADD_H), 49, dev)
+    _, total, rrms = hip_ops.rms_norm_add_fwd(x, res, w, 1e-6)
+    f_ms, how = time_graph(lambda: hip_ops.rms_norm_add_fwd(x, res, w, 1e-6), stream, reps)
+    b_ms, _ = time_graph(lambda: hip_ops.rms_norm_bwd(total, w, dy, rrms, 1e-6, dsum=ds), stream, reps)
+    uf_ms, _ = time_graph(lambda: hip_ops.rms_norm_fwd(x + res, w, 1e-6), stream, reps)
+    ub_ms, _ = time_graph(lambda: hip_ops.rms_norm_bwd(total, w, dy, rrms, 1e-6)[0] + ds, stream, reps)
+    return {"fwd_us": round(f_ms * 1e3, 2), "fwd_GB/s": round(ADD_FWD_BYTES / (f_ms * 1e-3) / 1e9, 1),
+            "bwd_us": round(b_ms * 1e3, 2), "bwd_GB/s": round(ADD_BWD_BYTES / (b_ms * 1e-3) / 1e9, 1),
+            "unfused_fwd_us": round(uf_ms * 1e3, 2), "unfused_bwd_us": round(ub_ms * 1e3, 2),
+            "timing": how}
+
+
 def bench_flce(dev, stream, reps, token_chunk=None):
     """Fused linear cross-entropy fwd + bwd as the autograd Function runs it:
     hidden [8192, 2048], lm_head [151936, 2048] ~N(0, 0.02), no bias, 10% of
@@ -284,7 +311,8 @@ def build_train_model(dev, layers=TRAIN_LAYERS):
     lm.to(device=dev, dtype=torch.bfloat16)
     # the patcher wraps norm weights in new (trainable) Parameters, as the
     # reference's MetalLigerRMSNorm does: freeze after patching
-    model = apply_metal_liger_to_qwen3vl(PeftLike(lm), fuse_rope=True, fuse_cross_entropy=True)
+    model = apply_metal_liger_to_qwen3vl(PeftLike(lm), fuse_rope=True, fuse_cross_entropy=True,
+                                         fuse_residual_norm=True)
     for n, p in model.named_parameters():
         p.requires_grad_("lora_" in n)
     return model
@@ -293,7 +321,8 @@ def build_train_model(dev, layers=TRAIN_LAYERS):
 def bench_train_step(dev, steps=5, warmup=2):
     """4-layer Qwen3-style LoRA train step: token ids [4, 2048] uniform in
     [0, 151936), forward through the patched decoder (fused RMSNorm, SwiGLU,
-    LoRA QKV / MLP, q/k norm + RoPE from the rotary module's tables),
+    LoRA QKV / MLP / o_proj, q/k norm + RoPE from the rotary module's tables,
+    the post-attention residual add fused into its norm),
     next-token loss from model(input_ids, labels=input_ids) by the chunked
     fused linear cross-entropy (transformers' label shift: the last position
     of each sequence ignored; no logits formed), backward, AdamW on the
@@ -350,7 +379,8 @@ def pmc_probe(dev):
     q [4, 16, 2048, 128], k [4, 8, 2048, 128] bf16, RMSNorm forward and
     backward on x [8192, 2048] fp32, and the fused q/k norm + RoPE forward
     and backward (with weight gradients) on the same q, k as HF's transposed
-    views with bf16 tables [4, 2048, 128]."""
+    views with bf16 tables [4, 2048, 128], and the residual add + RMSNorm
+    forward and backward on bf16 [8192, 2048]."""
     import torch
 
     from metal_liger_amd import hip_ops
@@ -373,6 +403,12 @@ def pmc_probe(dev):
     nwk = 1.0 + 0.1 * gpu_randn((RD,), 63, dev)
     cos = gpu_randn((RB, 1, RS, RD), 64, dev)
     sin = gpu_randn((RB, 1, RS, RD), 65, dev)
+    ax = gpu_randn((ADD_N, ADD_H), 45, dev)
+    ares = gpu_randn((ADD_N, ADD_H), 46, dev)
+    aw = 1.0 + 0.1 * gpu_randn((ADD_H,), 47, dev)
+    ady = gpu_randn((ADD_N, ADD_H), 48, dev)
+    ads = gpu_randn((ADD_N, ADD_H), 49, dev)
+    _, atot, arr = hip_ops.rms_norm_add_fwd(ax, ares, aw, 1e-6)
     torch.cuda.synchronize()
     for _ in range(3):
         dst.copy_(src)
@@ -383,13 +419,15 @@ def pmc_probe(dev):
                lambda: hip_ops.rms_norm_fwd(x, w, 1e-6),
                lambda: hip_ops.rms_norm_bwd(x, w, gx, rrms, 1e-6),
                lambda: hip_ops.qk_norm_rope_fwd(hq, hk, nwq, nwk, cos, sin, 1e-6),
-               lambda: hip_ops.qk_norm_rope_bwd(hq, hk, nwq, nwk, cos, sin, 1e-6, q, k)):
+               lambda: hip_ops.qk_norm_rope_bwd(hq, hk, nwq, nwk, cos, sin, 1e-6, q, k),
+               lambda: hip_ops.rms_norm_add_fwd(ax, ares, aw, 1e-6),
+               lambda: hip_ops.rms_norm_bwd(atot, aw, ady, arr, 1e-6, dsum=ads)):
         for _ in range(5):
             fn()
         torch.cuda.synchronize()
     print("pmc probe: 3 x 1 GiB copy; 5 x each of swiglu_bwd, swiglu_fwd [8192, 6144] bf16, "
-          "rope_pos q/k bf16, rms_norm fwd, bwd [8192, 2048] fp32, qk_norm_rope fwd, bwd bf16",
-          flush=True)
+          "rope_pos q/k bf16, rms_norm fwd, bwd [8192, 2048] fp32, qk_norm_rope fwd, bwd bf16, "
+          "rms_norm add fwd, bwd [8192, 2048] bf16", flush=True)
 
 
 def pmc_mfma_probe(dev):
@@ -578,6 +616,7 @@ def main():
     breakdown["gpu_ms_per_step"] = round(gpu_ms_step, 4)
     breakdown["rmsnorm_fp32"] = bench_rmsnorm(dev, stream, reps)
     breakdown["qk_norm_rope_bf16"] = bench_qk_norm_rope(dev, stream, reps)
+    breakdown["add_rmsnorm_bf16"] = bench_add_rmsnorm(dev, stream, reps)
     if not args.no_mfma_ops:
         breakdown["flce_fwd_bwd"] = bench_flce(dev, stream, 5)
         breakdown["lora_bwd_layer"] = bench_lora_bwd(dev, stream, 10)

@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define ML_ABI_VERSION 3
+#define ML_ABI_VERSION 4
 
 /* dtype tags */
 #define ML_F32 0
@@ -85,6 +85,39 @@ int ml_rmsnorm_bwd(const void* x, int64_t ldx, const void* w, const void* dy, in
                    const float* rrms, float eps, void* dx, int64_t lddx, void* dw,
                    void* workspace, size_t workspace_bytes, int64_t rows, int64_t cols,
                    int x_dtype, int w_dtype, void* stream);
+
+/*
+ * Residual add fused into the norm after it: the decoder layer's
+ * `hidden = residual + attn_out; post_attention_layernorm(hidden)`
+ * (transformers modeling_qwen3.py, Qwen3DecoderLayer.forward; the step that
+ * follows the reference's LoRA o_proj, ops/fused_lora.py:26 "LoRA_W").
+ * No single reference function: it fuses torch's add with
+ * _FusedRMSNormFunction.forward (ops/fused_rms_norm.py:31-41).
+ *
+ *   sum[r,c] = x[r,c] + residual[r,c]                  (rounded to x's dtype)
+ *   y, rrms  = ml_rmsnorm_fwd of that rounded sum
+ *
+ * residual shares x's dtype; sum may not alias x or residual.
+ */
+int ml_rmsnorm_add_fwd(const void* x, int64_t ldx, const void* residual, int64_t ldr,
+                       const void* w, void* sum, int64_t lds, void* y, int64_t ldy, float* rrms,
+                       int64_t rows, int64_t cols, float eps, int x_dtype, int w_dtype,
+                       void* stream);
+
+/*
+ * Backward of ml_rmsnorm_add_fwd: the norm's VJP at the saved sum plus the
+ * gradient dsum the sum receives from the residual branch, rounded once:
+ *
+ *   dx = (gw * r - (sum * mean_c(gw * sum)) * r^3) + dsum   (x's dtype)
+ *   dw as ml_rmsnorm_bwd; workspace from ml_rmsnorm_bwd_workspace_bytes.
+ *
+ * dx is the gradient of both x and residual (autograd's add backward gives
+ * each the sum's gradient). dx may not alias sum, dy or dsum.
+ */
+int ml_rmsnorm_add_bwd(const void* sum, int64_t lds, const void* w, const void* dy,
+                       int64_t lddy, const void* dsum, int64_t ldd, const float* rrms, float eps,
+                       void* dx, int64_t lddx, void* dw, void* workspace, size_t workspace_bytes,
+                       int64_t rows, int64_t cols, int x_dtype, int w_dtype, void* stream);
 
 /* ------------------------------------------------------------------- SwiGLU
  * Replaces metal_swiglu_forward (csrc/metal_liger_ops.h:27-30,

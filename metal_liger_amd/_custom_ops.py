@@ -64,6 +64,29 @@ def _(x, weight, dy, rrms, eps):
     return x.new_empty(x.shape), weight.new_empty((x.shape[-1],))
 
 
+@torch.library.custom_op(f"{NS}::rms_norm_add_fwd", mutates_args=(), device_types=_DEV)
+def rms_norm_add_fwd(x: Tensor, residual: Tensor, weight: Tensor,
+                     eps: float) -> tuple[Tensor, Tensor, Tensor]:
+    return hip_ops.rms_norm_add_fwd(x, residual, weight, eps)
+
+
+@rms_norm_add_fwd.register_fake
+def _(x, residual, weight, eps):
+    return (x.new_empty(x.shape), x.new_empty(x.shape),
+            x.new_empty(x.shape[:-1], dtype=torch.float32))
+
+
+@torch.library.custom_op(f"{NS}::rms_norm_add_bwd", mutates_args=(), device_types=_DEV)
+def rms_norm_add_bwd(total: Tensor, weight: Tensor, dy: Tensor, dsum: Tensor, rrms: Tensor,
+                     eps: float) -> tuple[Tensor, Tensor]:
+    return hip_ops.rms_norm_bwd(total, weight, dy, rrms, eps, dsum=dsum)
+
+
+@rms_norm_add_bwd.register_fake
+def _(total, weight, dy, dsum, rrms, eps):
+    return total.new_empty(total.shape), weight.new_empty((total.shape[-1],))
+
+
 # ------------------------------------------------------------------- SwiGLU --
 
 @torch.library.custom_op(f"{NS}::swiglu_fwd", mutates_args=(), device_types=_DEV)

@@ -39,6 +39,14 @@ SIGNATURES: dict[str, tuple] = {
         _i32,
         [_p, _i64, _p, _p, _i64, _p, _f32, _p, _i64, _p, _p, _sz, _i64, _i64, _i32, _i32, _p],
     ),
+    "ml_rmsnorm_add_fwd": (
+        _i32, [_p, _i64, _p, _i64, _p, _p, _i64, _p, _i64, _p, _i64, _i64, _f32, _i32, _i32, _p],
+    ),
+    "ml_rmsnorm_add_bwd": (
+        _i32,
+        [_p, _i64, _p, _p, _i64, _p, _i64, _p, _f32, _p, _i64, _p, _p, _sz, _i64, _i64, _i32, _i32,
+         _p],
+    ),
     "ml_swiglu_fwd": (_i32, [_p, _p, _p, _i64, _i32, _p]),
     "ml_swiglu_bwd": (_i32, [_p, _p, _p, _p, _p, _i64, _i32, _p]),
     "ml_rope_table": (
@@ -111,7 +119,7 @@ SIGNATURES: dict[str, tuple] = {
     ),
 }
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 _lib = None
 _lock = threading.Lock()

@@ -13,6 +13,15 @@
 //    partial rows in fixed order. No atomics, bit-reproducible run to run.
 //  * generic path (any width, stride or alignment): one 256-thread block per
 //    row with scalar accesses.
+//  * residual form (Qwen3's `h = residual + attn_out; post_attention_layernorm(h)`):
+//    the forward reads x and the residual, stores s = x + residual rounded
+//    to x's dtype (what the separate add produces) and normalises that s;
+//    the backward adds the gradient the sum receives from the residual
+//    branch into dx before its one rounding. One pass each instead of an
+//    add kernel plus a norm kernel (forward) and a norm kernel plus an add
+//    (backward).
+#include <initializer_list>
+
 #include "common.h"
 
 // Evaluate every product and sum exactly as written (one rounding each), as
@@ -43,10 +52,12 @@ __device__ __forceinline__ float block_sum_256(float v, float* red /* [4] */) {
 }
 
 // ------------------------------------------------------------ fast forward
-template <typename TX, typename TW, int ITERS>
+// ADD: x <- round(x + res) first (stored to sum), as the residual form does.
+template <typename TX, typename TW, int ITERS, bool ADD>
 __global__ __launch_bounds__(64 * kFwdWaves) void rms_fwd_reg(
-    const TX* __restrict__ x, int64_t ldx, const TW* __restrict__ w, TX* __restrict__ y,
-    int64_t ldy, float* __restrict__ rrms, int64_t rows, int cols, float eps) {
+    const TX* __restrict__ x, int64_t ldx, const TX* __restrict__ res, int64_t ldr,
+    TX* __restrict__ sum, int64_t lds, const TW* __restrict__ w, TX* __restrict__ y, int64_t ldy,
+    float* __restrict__ rrms, int64_t rows, int cols, float eps) {
   constexpr int VEC = vec16<TX>();
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * kFwdWaves + (threadIdx.x >> 6);
@@ -58,6 +69,20 @@ __global__ __launch_bounds__(64 * kFwdWaves) void rms_fwd_reg(
   float v[ITERS][VEC];
 #pragma unroll
   for (int it = 0; it < ITERS; ++it) load_n<TX, VEC>(xr + clamp_col(it, lane, cols, VEC), v[it]);
+  if constexpr (ADD) {
+    const TX* rr = res + row * ldr;
+    float rv[ITERS][VEC];
+#pragma unroll
+    for (int it = 0; it < ITERS; ++it) load_n<TX, VEC>(rr + clamp_col(it, lane, cols, VEC), rv[it]);
+    TX* sr = sum + row * lds;
+#pragma unroll
+    for (int it = 0; it < ITERS; ++it) {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) v[it][e] = to_f32(from_f32<TX>(v[it][e] + rv[it][e]));
+      const int c = (it * 64 + lane) * VEC;
+      if (c < cols) store_n<TX, VEC>(sr + c, v[it]);
+    }
+  }
 #pragma unroll
   for (int it = 0; it < ITERS; ++it) {
     if ((it * 64 + lane) * VEC >= cols) {
@@ -89,16 +114,25 @@ __global__ __launch_bounds__(64 * kFwdWaves) void rms_fwd_reg(
 }
 
 // --------------------------------------------------------- generic forward
+// res == nullptr: plain norm of x. Otherwise each thread stores
+// round(x + res) for its columns and normalises that.
 template <typename TX, typename TW>
 __global__ __launch_bounds__(kGenericThreads) void rms_fwd_generic(
-    const TX* __restrict__ x, int64_t ldx, const TW* __restrict__ w, TX* __restrict__ y,
-    int64_t ldy, float* __restrict__ rrms, int64_t rows, int64_t cols, float eps) {
+    const TX* __restrict__ x, int64_t ldx, const TX* __restrict__ res, int64_t ldr,
+    TX* __restrict__ sum, int64_t lds, const TW* __restrict__ w, TX* __restrict__ y, int64_t ldy,
+    float* __restrict__ rrms, int64_t rows, int64_t cols, float eps) {
   __shared__ float red[4];
   const int64_t row = blockIdx.x;
   const TX* xr = x + row * ldx;
+  const TX* rr = res == nullptr ? nullptr : res + row * ldr;
+  TX* sr = res == nullptr ? nullptr : sum + row * lds;
+  auto value = [&](int64_t c) -> float {
+    return rr == nullptr ? to_f32(xr[c]) : to_f32(from_f32<TX>(to_f32(xr[c]) + to_f32(rr[c])));
+  };
   float ss = 0.f;
   for (int64_t c = threadIdx.x; c < cols; c += kGenericThreads) {
-    const float xv = to_f32(xr[c]);
+    const float xv = value(c);
+    if (sr != nullptr) sr[c] = from_f32<TX>(xv);
     ss += xv * xv;
   }
   ss = block_sum_256(ss, red);
@@ -106,15 +140,17 @@ __global__ __launch_bounds__(kGenericThreads) void rms_fwd_generic(
   if (rrms != nullptr && threadIdx.x == 0) rrms[row] = r;
   TX* yr = y + row * ldy;
   for (int64_t c = threadIdx.x; c < cols; c += kGenericThreads)
-    yr[c] = from_f32<TX>((to_f32(xr[c]) * r) * to_f32(w[c]));
+    yr[c] = from_f32<TX>((value(c) * r) * to_f32(w[c]));
 }
 
 // ------------------------------------------------------------ fast backward
-template <typename TX, typename TW, int ITERS, bool HAS_RRMS>
+// HAS_DRES: dx += dres (the residual form's second gradient) before rounding.
+template <typename TX, typename TW, int ITERS, bool HAS_RRMS, bool HAS_DRES>
 __global__ __launch_bounds__(64 * kBwdWaves) void rms_bwd_reg(
     const TX* __restrict__ x, int64_t ldx, const TW* __restrict__ w, const TX* __restrict__ dy,
-    int64_t lddy, const float* __restrict__ rrms, float eps, TX* __restrict__ dx, int64_t lddx,
-    float* __restrict__ partial, int64_t rows, int cols) {
+    int64_t lddy, const TX* __restrict__ dres, int64_t ldd, const float* __restrict__ rrms,
+    float eps, TX* __restrict__ dx, int64_t lddx, float* __restrict__ partial, int64_t rows,
+    int cols) {
   constexpr int VEC = vec16<TX>();
   extern __shared__ float smem[];  // [kBwdWaves/2][cols]
   const int lane = threadIdx.x & 63;
@@ -143,12 +179,14 @@ __global__ __launch_bounds__(64 * kBwdWaves) void rms_bwd_reg(
        row += (int64_t)gridDim.x * kBwdWaves) {
     const TX* xr = x + row * ldx;
     const TX* gr = dy + row * lddy;
-    float xv[ITERS][VEC], gv[ITERS][VEC];
+    float xv[ITERS][VEC], gv[ITERS][VEC], dv[HAS_DRES ? ITERS : 1][VEC];
 #pragma unroll
     for (int it = 0; it < ITERS; ++it) {
       const int c = clamp_col(it, lane, cols, VEC);
       load_n<TX, VEC>(xr + c, xv[it]);
       load_n<TX, VEC>(gr + c, gv[it]);
+      // (the tail chunk reads the last valid chunk; its result is not stored)
+      if constexpr (HAS_DRES) load_n<TX, VEC>(dres + row * ldd + c, dv[it]);
     }
 #pragma unroll
     for (int it = 0; it < ITERS; ++it) {
@@ -197,6 +235,10 @@ __global__ __launch_bounds__(64 * kBwdWaves) void rms_bwd_reg(
       float o[VEC];
 #pragma unroll
       for (int e = 0; e < VEC; ++e) o[e] = gv[it][e] * r - (xv[it][e] * mean) * r3;
+      if constexpr (HAS_DRES) {
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) o[e] = o[e] + dv[HAS_DRES ? it : 0][e];
+      }
       if (c < cols) store_n_nt<TX, VEC>(dxr + c, o);
     }
   }
@@ -245,8 +287,9 @@ __global__ __launch_bounds__(64 * kBwdWaves) void rms_bwd_reg(
 template <typename TX, typename TW, bool HAS_RRMS>
 __global__ __launch_bounds__(kGenericThreads) void rms_bwd_generic(
     const TX* __restrict__ x, int64_t ldx, const TW* __restrict__ w, const TX* __restrict__ dy,
-    int64_t lddy, const float* __restrict__ rrms, float eps, TX* __restrict__ dx, int64_t lddx,
-    float* __restrict__ partial, int64_t rows, int64_t cols) {
+    int64_t lddy, const TX* __restrict__ dres, int64_t ldd, const float* __restrict__ rrms,
+    float eps, TX* __restrict__ dx, int64_t lddx, float* __restrict__ partial, int64_t rows,
+    int64_t cols) {
   __shared__ float red[4];
   float* pr = partial + (int64_t)blockIdx.x * cols;
   for (int64_t c = threadIdx.x; c < cols; c += kGenericThreads) pr[c] = 0.f;
@@ -273,7 +316,9 @@ __global__ __launch_bounds__(kGenericThreads) void rms_bwd_generic(
     for (int64_t c = threadIdx.x; c < cols; c += kGenericThreads) {
       const float xv = to_f32(xr[c]);
       const float gv = to_f32(gr[c]);
-      dxr[c] = from_f32<TX>((gv * to_f32(w[c])) * r - (xv * mean) * r3);
+      float o = (gv * to_f32(w[c])) * r - (xv * mean) * r3;
+      if (dres != nullptr) o = o + to_f32(dres[row * ldd + c]);
+      dxr[c] = from_f32<TX>(o);
       pr[c] += gv * (xv * r);
     }
   }
@@ -357,43 +402,60 @@ int pick_iters(int64_t cols, bool backward) {
   return 0;
 }
 
+// A row operand: base pointer and row stride in elements (ptr may be null:
+// an absent optional operand).
+struct RowOp {
+  const void* ptr;
+  int64_t ld;
+};
+
 template <typename TX, typename TW>
-bool fast_path_ok(bool backward, const void* x, int64_t ldx, const void* y, int64_t ldy,
-                  const void* w, int64_t cols, const void* extra = nullptr, int64_t ld_extra = 0) {
+bool fast_path_ok(bool backward, const void* w, int64_t cols, std::initializer_list<RowOp> ops) {
   constexpr int VEC = vec16<TX>();
   if (cols % VEC != 0 || pick_iters<TX>(cols, backward) == 0) return false;
-  if (!aligned16(x) || !aligned16(y) || !aligned16(w)) return false;
-  if ((ldx * (int64_t)sizeof(TX)) % 16 != 0 || (ldy * (int64_t)sizeof(TX)) % 16 != 0) return false;
-  if (extra != nullptr &&
-      (!aligned16(extra) || (ld_extra * (int64_t)sizeof(TX)) % 16 != 0))
-    return false;
+  if (!aligned16(w)) return false;
+  for (const RowOp& o : ops)
+    if (o.ptr != nullptr && (!aligned16(o.ptr) || (o.ld * (int64_t)sizeof(TX)) % 16 != 0))
+      return false;
   return true;
 }
 
+// res / sum: the residual form (both given) or the plain norm (both null).
 template <typename TX, typename TW>
-int launch_fwd(const void* x, int64_t ldx, const void* w, void* y, int64_t ldy, float* rrms,
-               int64_t rows, int64_t cols, float eps, hipStream_t st) {
+int launch_fwd(const void* x, int64_t ldx, const void* res, int64_t ldr, void* sum, int64_t lds,
+               const void* w, void* y, int64_t ldy, float* rrms, int64_t rows, int64_t cols,
+               float eps, hipStream_t st) {
   if (rows == 0) return ML_OK;
   const TX* xp = static_cast<const TX*>(x);
+  const TX* rp = static_cast<const TX*>(res);
+  TX* sp = static_cast<TX*>(sum);
   const TW* wp = static_cast<const TW*>(w);
   TX* yp = static_cast<TX*>(y);
-  if (fast_path_ok<TX, TW>(false, x, ldx, y, ldy, w, cols)) {
+  if (fast_path_ok<TX, TW>(false, w, cols, {{x, ldx}, {y, ldy}, {res, ldr}, {sum, lds}})) {
     const dim3 grid((unsigned)((rows + kFwdWaves - 1) / kFwdWaves));
     const int it = pick_iters<TX>(cols, false);
-#define ML_FWD(I) \
-  rms_fwd_reg<TX, TW, I><<<grid, 64 * kFwdWaves, 0, st>>>(xp, ldx, wp, yp, ldy, rrms, rows, (int)cols, eps)
+#define ML_FWD(I, A)                                                                         \
+  rms_fwd_reg<TX, TW, I, A><<<grid, 64 * kFwdWaves, 0, st>>>(xp, ldx, rp, ldr, sp, lds, wp, yp, \
+                                                             ldy, rrms, rows, (int)cols, eps)
+#define ML_FWD_A(I)  \
+  if (rp) {          \
+    ML_FWD(I, true); \
+  } else {           \
+    ML_FWD(I, false); \
+  }
     switch (it) {
-      case 1: ML_FWD(1); break;
-      case 2: ML_FWD(2); break;
-      case 4: ML_FWD(4); break;
-      default: ML_FWD(8); break;
+      case 1: ML_FWD_A(1); break;
+      case 2: ML_FWD_A(2); break;
+      case 4: ML_FWD_A(4); break;
+      default: ML_FWD_A(8); break;
     }
+#undef ML_FWD_A
 #undef ML_FWD
   } else {
     ML_CHECK(rows <= 0x7fffffffLL, "rmsnorm: too many rows for the generic path (%lld)",
              (long long)rows);
     rms_fwd_generic<TX, TW><<<dim3((unsigned)rows), kGenericThreads, 0, st>>>(
-        xp, ldx, wp, yp, ldy, rrms, rows, cols, eps);
+        xp, ldx, rp, ldr, sp, lds, wp, yp, ldy, rrms, rows, cols, eps);
   }
   ML_LAUNCH_CHECK();
   return ML_OK;
@@ -405,19 +467,23 @@ int64_t bwd_blocks_fast(int64_t rows) {
 }
 int64_t bwd_blocks_generic(int64_t rows) { return rows < kMaxBwdBlocks ? rows : kMaxBwdBlocks; }
 
+// dres: the residual form's second gradient of the sum (null: plain norm).
 template <typename TX, typename TW>
 int launch_bwd(const void* x, int64_t ldx, const void* w, const void* dy, int64_t lddy,
-               const float* rrms, float eps, void* dx, int64_t lddx, void* dw, void* ws,
-               size_t ws_bytes, int64_t rows, int64_t cols, hipStream_t st) {
+               const void* dres, int64_t ldd, const float* rrms, float eps, void* dx,
+               int64_t lddx, void* dw, void* ws, size_t ws_bytes, int64_t rows, int64_t cols,
+               hipStream_t st) {
   const TX* xp = static_cast<const TX*>(x);
   const TW* wp = static_cast<const TW*>(w);
   const TX* gp = static_cast<const TX*>(dy);
+  const TX* dp = static_cast<const TX*>(dres);
   TX* dxp = static_cast<TX*>(dx);
   TW* dwp = static_cast<TW*>(dw);
   float* part = static_cast<float*>(ws);
   const int64_t lds_bytes = (int64_t)(kBwdWaves / 2) * cols * (int64_t)sizeof(float);
-  const bool fast = fast_path_ok<TX, TW>(true, x, ldx, dx, lddx, w, cols, dy, lddy) &&
-                    lds_bytes <= 64 * 1024;
+  const bool fast =
+      fast_path_ok<TX, TW>(true, w, cols, {{x, ldx}, {dx, lddx}, {dy, lddy}, {dres, ldd}}) &&
+      lds_bytes <= 64 * 1024;
   const int64_t G = rows == 0 ? 0 : (fast ? bwd_blocks_fast(rows) : bwd_blocks_generic(rows));
   ML_CHECK(ws_bytes >= (size_t)(G * cols * (int64_t)sizeof(float)),
            "rmsnorm backward: workspace too small (%zu < %lld bytes)", ws_bytes,
@@ -425,14 +491,18 @@ int launch_bwd(const void* x, int64_t ldx, const void* w, const void* dy, int64_
   if (G > 0) {
     if (fast) {
       const int it = pick_iters<TX>(cols, true);
-#define ML_BWD(I, R)                                                                           \
-  rms_bwd_reg<TX, TW, I, R><<<dim3((unsigned)G), 64 * kBwdWaves, (size_t)lds_bytes, st>>>( \
-      xp, ldx, wp, gp, lddy, rrms, eps, dxp, lddx, part, rows, (int)cols)
-#define ML_BWD_R(I) \
-  if (rrms) {       \
-    ML_BWD(I, true); \
-  } else {          \
-    ML_BWD(I, false); \
+#define ML_BWD(I, R, D)                                                                           \
+  rms_bwd_reg<TX, TW, I, R, D><<<dim3((unsigned)G), 64 * kBwdWaves, (size_t)lds_bytes, st>>>( \
+      xp, ldx, wp, gp, lddy, dp, ldd, rrms, eps, dxp, lddx, part, rows, (int)cols)
+#define ML_BWD_R(I)          \
+  if (rrms && dp) {          \
+    ML_BWD(I, true, true);   \
+  } else if (rrms) {         \
+    ML_BWD(I, true, false);  \
+  } else if (dp) {           \
+    ML_BWD(I, false, true);  \
+  } else {                   \
+    ML_BWD(I, false, false); \
   }
       switch (it) {
         case 1: ML_BWD_R(1); break;
@@ -449,10 +519,10 @@ int launch_bwd(const void* x, int64_t ldx, const void* w, const void* dy, int64_
     } else {
       if (rrms)
         rms_bwd_generic<TX, TW, true><<<dim3((unsigned)G), kGenericThreads, 0, st>>>(
-            xp, ldx, wp, gp, lddy, rrms, eps, dxp, lddx, part, rows, cols);
+            xp, ldx, wp, gp, lddy, dp, ldd, rrms, eps, dxp, lddx, part, rows, cols);
       else
         rms_bwd_generic<TX, TW, false><<<dim3((unsigned)G), kGenericThreads, 0, st>>>(
-            xp, ldx, wp, gp, lddy, rrms, eps, dxp, lddx, part, rows, cols);
+            xp, ldx, wp, gp, lddy, dp, ldd, rrms, eps, dxp, lddx, part, rows, cols);
     }
     ML_LAUNCH_CHECK();
   }
@@ -500,8 +570,23 @@ extern "C" int ml_rmsnorm_fwd(const void* x, int64_t ldx, const void* w, void* y
   ML_CHECK(rows == 0 || (x && w && y), "rmsnorm: null pointer");
   ML_CHECK(ldx >= cols && ldy >= cols, "rmsnorm: row stride smaller than cols");
   return dispatch_xw(x_dtype, w_dtype, [&](auto tx, auto tw) -> int {
-    return launch_fwd<decltype(tx), decltype(tw)>(x, ldx, w, y, ldy, rrms, rows, cols, eps,
-                                                  (hipStream_t)stream);
+    return launch_fwd<decltype(tx), decltype(tw)>(x, ldx, nullptr, 0, nullptr, 0, w, y, ldy, rrms,
+                                                  rows, cols, eps, (hipStream_t)stream);
+  });
+}
+
+extern "C" int ml_rmsnorm_add_fwd(const void* x, int64_t ldx, const void* residual, int64_t ldr,
+                                  const void* w, void* sum, int64_t lds, void* y, int64_t ldy,
+                                  float* rrms, int64_t rows, int64_t cols, float eps, int x_dtype,
+                                  int w_dtype, void* stream) {
+  ML_CHECK(rows >= 0 && cols > 0, "rmsnorm add: bad shape rows=%lld cols=%lld", (long long)rows,
+           (long long)cols);
+  ML_CHECK(rows == 0 || (x && residual && w && sum && y), "rmsnorm add: null pointer");
+  ML_CHECK(ldx >= cols && ldr >= cols && lds >= cols && ldy >= cols,
+           "rmsnorm add: row stride smaller than cols");
+  return dispatch_xw(x_dtype, w_dtype, [&](auto tx, auto tw) -> int {
+    return launch_fwd<decltype(tx), decltype(tw)>(x, ldx, residual, ldr, sum, lds, w, y, ldy,
+                                                  rrms, rows, cols, eps, (hipStream_t)stream);
   });
 }
 
@@ -511,19 +596,38 @@ extern "C" size_t ml_rmsnorm_bwd_workspace_bytes(int64_t rows, int64_t cols) {
   return (size_t)(g * cols * (int64_t)sizeof(float));
 }
 
-extern "C" int ml_rmsnorm_bwd(const void* x, int64_t ldx, const void* w, const void* dy,
-                              int64_t lddy, const float* rrms, float eps, void* dx, int64_t lddx,
-                              void* dw, void* workspace, size_t workspace_bytes, int64_t rows,
-                              int64_t cols, int x_dtype, int w_dtype, void* stream) {
+static int rmsnorm_bwd_checked(const void* x, int64_t ldx, const void* w, const void* dy,
+                               int64_t lddy, const void* dres, int64_t ldd, const float* rrms,
+                               float eps, void* dx, int64_t lddx, void* dw, void* workspace,
+                               size_t workspace_bytes, int64_t rows, int64_t cols, int x_dtype,
+                               int w_dtype, void* stream) {
   ML_CHECK(rows >= 0 && cols > 0, "rmsnorm backward: bad shape rows=%lld cols=%lld",
            (long long)rows, (long long)cols);
   ML_CHECK(w && dw, "rmsnorm backward: null weight / dw pointer");
   ML_CHECK(rows == 0 || (x && dy && dx && workspace), "rmsnorm backward: null pointer");
-  ML_CHECK(ldx >= cols && lddy >= cols && lddx >= cols,
+  ML_CHECK(ldx >= cols && lddy >= cols && lddx >= cols && (dres == nullptr || ldd >= cols),
            "rmsnorm backward: row stride smaller than cols");
   return dispatch_xw(x_dtype, w_dtype, [&](auto tx, auto tw) -> int {
-    return launch_bwd<decltype(tx), decltype(tw)>(x, ldx, w, dy, lddy, rrms, eps, dx, lddx, dw,
-                                                  workspace, workspace_bytes, rows, cols,
+    return launch_bwd<decltype(tx), decltype(tw)>(x, ldx, w, dy, lddy, dres, ldd, rrms, eps, dx,
+                                                  lddx, dw, workspace, workspace_bytes, rows, cols,
                                                   (hipStream_t)stream);
   });
+}
+
+extern "C" int ml_rmsnorm_bwd(const void* x, int64_t ldx, const void* w, const void* dy,
+                              int64_t lddy, const float* rrms, float eps, void* dx, int64_t lddx,
+                              void* dw, void* workspace, size_t workspace_bytes, int64_t rows,
+                              int64_t cols, int x_dtype, int w_dtype, void* stream) {
+  return rmsnorm_bwd_checked(x, ldx, w, dy, lddy, nullptr, 0, rrms, eps, dx, lddx, dw, workspace,
+                             workspace_bytes, rows, cols, x_dtype, w_dtype, stream);
+}
+
+extern "C" int ml_rmsnorm_add_bwd(const void* sum, int64_t lds, const void* w, const void* dy,
+                                  int64_t lddy, const void* dsum, int64_t ldd, const float* rrms,
+                                  float eps, void* dx, int64_t lddx, void* dw, void* workspace,
+                                  size_t workspace_bytes, int64_t rows, int64_t cols, int x_dtype,
+                                  int w_dtype, void* stream) {
+  ML_CHECK(rows == 0 || dsum, "rmsnorm add backward: null sum gradient");
+  return rmsnorm_bwd_checked(sum, lds, w, dy, lddy, dsum, ldd, rrms, eps, dx, lddx, dw, workspace,
+                             workspace_bytes, rows, cols, x_dtype, w_dtype, stream);
 }

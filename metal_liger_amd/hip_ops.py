@@ -44,12 +44,42 @@ def rms_norm_fwd(x: torch.Tensor, weight: torch.Tensor, eps: float):
     return y, rrms
 
 
+def rms_norm_add_fwd(x: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor, eps: float):
+    """Residual add fused with the norm after it: returns (y, sum, rrms) with
+    sum = x + residual (x's dtype, contiguous) and y, rrms the norm of sum."""
+    ensure_rocm_device(x, residual, weight)
+    if x.dim() < 1:
+        raise ValueError("rms_norm add: input must have at least one dimension")
+    if residual.shape != x.shape or residual.dtype != x.dtype:
+        raise ValueError(f"rms_norm add: residual {tuple(residual.shape)} {residual.dtype} does not "
+                         f"match x {tuple(x.shape)} {x.dtype}")
+    cols = x.shape[-1]
+    x2 = rows_view(x)
+    r2 = rows_view(residual)
+    w = _norm_weight(x, weight)
+    y = torch.empty(x.shape, dtype=x.dtype, device=x.device)
+    total = torch.empty(x.shape, dtype=x.dtype, device=x.device)
+    rrms = torch.empty(x.shape[:-1], dtype=torch.float32, device=x.device)
+    rows = x2.shape[0]
+    if rows > 0:
+        call(
+            "ml_rmsnorm_add_fwd", ptr(x2), row_stride(x2), ptr(r2), row_stride(r2), ptr(w),
+            ptr(total), cols, ptr(y), cols, ptr(rrms), rows, cols, float(eps), dtype_tag(x, "x"),
+            dtype_tag(w, "weight"), stream_of(x),
+        )
+    return y, total, rrms
+
+
 def rms_norm_bwd(x: torch.Tensor, weight: torch.Tensor, dy: torch.Tensor,
-                 rrms: torch.Tensor | None, eps: float):
-    """Returns (dx, dweight); rrms may be None (recomputed from x and eps)."""
-    ensure_rocm_device(x, weight, dy, rrms)
+                 rrms: torch.Tensor | None, eps: float, dsum: torch.Tensor | None = None):
+    """Returns (dx, dweight); rrms may be None (recomputed from x and eps).
+    dsum (the residual form): a second gradient of x added into dx."""
+    ensure_rocm_device(x, weight, dy, rrms, dsum)
     if dy.shape != x.shape:
         raise ValueError(f"rms_norm backward: grad shape {tuple(dy.shape)} != input {tuple(x.shape)}")
+    if dsum is not None and dsum.shape != x.shape:
+        raise ValueError(f"rms_norm backward: sum grad shape {tuple(dsum.shape)} != input "
+                         f"{tuple(x.shape)}")
     cols = x.shape[-1]
     if dy.dtype != x.dtype:
         dy = dy.to(x.dtype)
@@ -67,11 +97,15 @@ def rms_norm_bwd(x: torch.Tensor, weight: torch.Tensor, dy: torch.Tensor,
         r = r.contiguous()
     ws_bytes = _hip.query("ml_rmsnorm_bwd_workspace_bytes", rows, cols)
     ws = torch.empty(max(1, (ws_bytes + 3) // 4), dtype=torch.float32, device=x.device)
-    call(
-        "ml_rmsnorm_bwd", ptr(x2), row_stride(x2), ptr(w), ptr(g2), row_stride(g2), ptr(r),
-        float(eps), ptr(dx), cols, ptr(dw), ptr(ws), ws.numel() * 4, rows, cols,
-        dtype_tag(x, "x"), dtype_tag(w, "weight"), stream_of(x),
-    )
+    tail = (float(eps), ptr(dx), cols, ptr(dw), ptr(ws), ws.numel() * 4, rows, cols,
+            dtype_tag(x, "x"), dtype_tag(w, "weight"), stream_of(x))
+    if dsum is None:
+        call("ml_rmsnorm_bwd", ptr(x2), row_stride(x2), ptr(w), ptr(g2), row_stride(g2), ptr(r),
+             *tail)
+    else:
+        d2 = rows_view(dsum if dsum.dtype == x.dtype else dsum.to(x.dtype))
+        call("ml_rmsnorm_add_bwd", ptr(x2), row_stride(x2), ptr(w), ptr(g2), row_stride(g2),
+             ptr(d2), row_stride(d2), ptr(r), *tail)
     if dw.dtype != weight.dtype:
         dw = dw.to(weight.dtype)
     return dx, dw

@@ -14,6 +14,7 @@ import logging
 
 import torch.nn as nn
 
+from metal_liger_amd.ops.fused_add_rms_norm import patch_residual_add_norm
 from metal_liger_amd.ops.fused_linear_cross_entropy import patch_causal_lm_loss
 from metal_liger_amd.ops.fused_lora import patch_fused_lora
 from metal_liger_amd.ops.fused_qk_norm_rope import patch_qk_norm_rope
@@ -118,6 +119,7 @@ def apply_metal_liger_to_qwen3vl(
     fuse_cross_entropy: bool = False,
     fuse_lora: bool = True,
     use_optimized_generator: bool = False,
+    fuse_residual_norm: bool = False,
 ) -> nn.Module:
     """Apply the fused operations to a Qwen3 / Qwen3-VL model in place and
     return it (patch.py:181-240).
@@ -130,6 +132,10 @@ def apply_metal_liger_to_qwen3vl(
     training mode) comes from the fused linear cross-entropy with
     transformers' label shift, without logits (the reference only logs here;
     MetalLigerFusedLinearCrossEntropy can still be called directly).
+    fuse_residual_norm (not in the reference): each decoder layer's
+    post-attention residual add runs in the same launch as its
+    post_attention_layernorm (ops/fused_add_rms_norm.py); needs
+    fuse_rms_norm, whose norm it extends.
     use_optimized_generator is not part of this build (inference path).
     """
     stats = {}
@@ -141,6 +147,10 @@ def apply_metal_liger_to_qwen3vl(
         n = _replace_mlps(model)
         stats["swiglu"] = n
         logger.info(f"MetalLiger: replaced {n} MLP layers with fused SwiGLU")
+    if fuse_residual_norm:
+        n = patch_residual_add_norm(model)
+        stats["residual_add_norm"] = n
+        logger.info(f"MetalLiger: fused residual add + RMSNorm in {n} decoder layers")
     if fuse_rope:
         # before the LoRA patch, which wraps whatever attention forward it finds
         n = patch_qk_norm_rope(model)

@@ -46,6 +46,31 @@ def rms_norm_backward(x: torch.Tensor, weight: torch.Tensor, rrms: torch.Tensor,
     return dx, dw
 
 
+# ---------------------------------------------------- residual add + RMSNorm --
+# Not a reference op: torch's add in a Qwen3 decoder layer (transformers'
+# modeling_qwen3.py, Qwen3DecoderLayer.forward: `residual + hidden_states`,
+# then post_attention_layernorm) followed by the reference's fused norm.
+
+
+def add_rms_norm_forward(x: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor,
+                         eps: float):
+    """(y, sum, rrms): sum = x + residual in x's dtype (torch's add rounds
+    the exact sum once), then rms_norm_forward of that sum."""
+    total = x + residual
+    y, rrms = rms_norm_forward(total, weight, eps)
+    return y, total, rrms
+
+
+def add_rms_norm_backward(total: torch.Tensor, weight: torch.Tensor, rrms: torch.Tensor,
+                          grad_out: torch.Tensor, grad_sum: torch.Tensor):
+    """Gradient of x (equal to that of residual): the norm's dx at the sum in
+    fp32 plus grad_sum, rounded once to the sum's dtype; dw as
+    rms_norm_backward."""
+    dxf, dw = rms_norm_backward(total.float(), weight.float(), rrms, grad_out.float())
+    dx = (dxf + grad_sum.float()).to(total.dtype)
+    return dx, dw.to(weight.dtype)
+
+
 # ------------------------------------------------------------------- SwiGLU --
 
 

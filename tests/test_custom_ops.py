@@ -26,6 +26,10 @@ def test_fake_kernels_elementwise_rope_qkn(ops):
         assert y.shape == (4, 8, 256) and r.shape == (4, 8) and r.dtype == F32
         dx, dw = ops.rms_norm_bwd(e(32, 64), e(64, dtype=F32), e(32, 64), None, 1e-6)
         assert dx.dtype == BF and dw.shape == (64,) and dw.dtype == F32
+        y, total, r = ops.rms_norm_add_fwd(e(2, 5, 64), e(2, 5, 64), e(64, dtype=F32), 1e-6)
+        assert y.shape == total.shape == (2, 5, 64) and total.dtype == BF and r.shape == (2, 5)
+        dx, dw = ops.rms_norm_add_bwd(total, e(64, dtype=F32), y, y, r, 1e-6)
+        assert dx.shape == (2, 5, 64) and dx.dtype == BF and dw.dtype == F32
         assert ops.swiglu_fwd(e(8, 96), e(8, 96)).shape == (8, 96)
         q = e(2, 33, 4, 64).transpose(1, 2)                  # HF's transposed view
         qo, ko = ops.rope_table(q, None, e(33, 64, dtype=F32), e(33, 64, dtype=F32), 1.0)

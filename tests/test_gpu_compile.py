@@ -35,6 +35,11 @@ def test_opcheck_elementwise_ops(dev):
     y, rrms = ops.rms_norm_fwd(x, w, 1e-6)
     torch.library.opcheck(ops.rms_norm_fwd.default, (x, w, 1e-6), test_utils=CHECKS)
     torch.library.opcheck(ops.rms_norm_bwd.default, (x, w, x.clone(), rrms, 1e-6), test_utils=CHECKS)
+    r = seeded((64, 256), 5).to(dev)
+    torch.library.opcheck(ops.rms_norm_add_fwd.default, (x, r, w, 1e-6), test_utils=CHECKS)
+    _, total, rrms2 = ops.rms_norm_add_fwd(x, r, w, 1e-6)
+    torch.library.opcheck(ops.rms_norm_add_bwd.default, (total, w, x.clone(), r.clone(), rrms2, 1e-6),
+                          test_utils=CHECKS)
     g, u = _bf((32, 512), 3, dev), _bf((32, 512), 4, dev)
     torch.library.opcheck(ops.swiglu_fwd.default, (g, u), test_utils=CHECKS)
     torch.library.opcheck(ops.swiglu_bwd.default, (g, u, g.clone()), test_utils=CHECKS)
@@ -144,6 +149,7 @@ def _compiled_matches_eager(fn, leaves):
 
 def test_compile_elementwise_and_rope(dev):
     from metal_liger_amd import MetalLigerRMSNorm
+    from metal_liger_amd.ops.fused_add_rms_norm import fused_add_rms_norm
     from metal_liger_amd.ops.fused_qk_norm_rope import _FusedQKNormRoPEFunction
     from metal_liger_amd.ops.fused_rope import apply_fused_rotary, apply_fused_rotary_inline
     from metal_liger_amd.ops.fused_swiglu import fused_swiglu
@@ -158,7 +164,8 @@ def test_compile_elementwise_and_rope(dev):
     wk = seeded((64,), 67, BF, 0.1, 1.0).to(dev).requires_grad_(True)
 
     def f(x, g, q, k, wq, wk):
-        y = fused_swiglu(norm(x).float().to(BF), g)
+        y, total = fused_add_rms_norm(norm(x), g, norm)
+        y = fused_swiglu(y, total)
         qa, ka = apply_fused_rotary(q, k, cos, sin)
         qb, kb = apply_fused_rotary_inline(qa, ka, pos, theta=1e4)
         qc, kc = _FusedQKNormRoPEFunction.apply(qb, kb, wq, wk, cos, sin, 1e-6)

@@ -115,6 +115,42 @@ def test_rmsnorm_bf16_dtypes():
     assert y.dtype == dx.dtype == dw.dtype == torch.bfloat16 and r.dtype == torch.float32
 
 
+# ---------------------------------------------------- residual add + RMSNorm --
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_add_rms_norm_forward_vs_library_routines(dtype):
+    # the sum is the exact sum rounded once to the input dtype (torch's add);
+    # the norm of that sum is F.rms_norm evaluated in fp64
+    x = randn(6, 96, seed=15, dtype=dtype)
+    r = randn(6, 96, seed=16, dtype=dtype)
+    w = 1.0 + 0.1 * randn(96, seed=17)
+    y, s, rrms = ref.add_rms_norm_forward(x, r, w, 1e-6)
+    assert s.dtype == y.dtype == dtype and rrms.dtype == torch.float32
+    assert torch.equal(s, (x.double() + r.double()).to(dtype))
+    want = F.rms_norm(s.double(), (96,), w.double(), 1e-6)
+    assert close_scaled(y, want, 1e-5 if dtype == torch.float32 else 8e-3)
+
+
+def test_add_rms_norm_backward_vs_fp64_autograd():
+    """Both outputs receive a gradient (the norm's and the residual
+    branch's); x and residual get the same total. A dropped residual-branch
+    gradient fails the check."""
+    eps = 1e-6
+    x, r = randn(5, 64, seed=18), randn(5, 64, seed=19)
+    w = 1.0 + 0.1 * randn(64, seed=20)
+    gy, gs = randn(5, 64, seed=21), randn(5, 64, seed=22)
+    x64, r64, w64 = (t.double().requires_grad_(True) for t in (x, r, w))
+    s64 = x64 + r64
+    ((rms64(s64, w64, eps) * gy.double()).sum() + (s64 * gs.double()).sum()).backward()
+    _, s, rrms = ref.add_rms_norm_forward(x, r, w, eps)
+    dx, dw = ref.add_rms_norm_backward(s, w, rrms, gy, gs)
+    assert close_scaled(dx, x64.grad, 1e-5) and close_scaled(dx, r64.grad, 1e-5)
+    assert close_scaled(dw, w64.grad, 1e-5)
+    dropped = ref.rms_norm_backward(s, w, rrms, gy)[0]       # planted: grad_sum left out
+    assert not close_scaled(dropped, x64.grad, 1e-2)
+
+
 # ------------------------------------------------------------------- SwiGLU --
 
 

@@ -155,6 +155,83 @@ def test_qk_norm_rope_patch_defers_norms_to_the_rotary_step(monkeypatch):
         bad(torch.randn(2, 32))
 
 
+class _OracleAddNorm:
+    """Stand-in for the fused residual add + norm Function on the CPU."""
+
+    calls = 0
+
+    @staticmethod
+    def apply(x, residual, weight, eps):
+        from oracle import reference_ops as ref
+        _OracleAddNorm.calls += 1
+        y, total, _ = ref.add_rms_norm_forward(x, residual, weight, eps)
+        return y, total
+
+
+class _ExtraAddLayer(torch.nn.Module):
+    """Has the four parts of a decoder layer but a third addition: not the
+    structure the fused forward reproduces, so it must stay unpatched."""
+
+    def __init__(self):
+        super().__init__()
+        from metal_liger_amd.ops.fused_rms_norm import MetalLigerRMSNorm
+        self.input_layernorm = MetalLigerRMSNorm(8)
+        self.self_attn = torch.nn.Identity()
+        self.post_attention_layernorm = MetalLigerRMSNorm(8)
+        self.mlp = torch.nn.Identity()
+
+    def forward(self, hidden_states):
+        residual = hidden_states
+        h = self.self_attn(self.input_layernorm(hidden_states))
+        h = residual + h + 1.0
+        residual = h
+        h = self.mlp(self.post_attention_layernorm(h))
+        return residual + h
+
+
+def test_residual_add_norm_patch_matches_unfused(monkeypatch):
+    """fuse_residual_norm swaps each Qwen3 decoder layer's forward for one
+    that fuses the post-attention add into post_attention_layernorm. With the
+    fused norms swapped for the oracle on the CPU, logits and gradients equal
+    the unfused model's bit for bit (every argument reaches the attention as
+    before); layers of another structure, or whose norm is not the fused
+    norm, are left alone."""
+    import copy
+
+    import metal_liger_amd.ops.fused_add_rms_norm as fa
+    from metal_liger_amd.ops.fused_rms_norm import MetalLigerRMSNorm
+    from metal_liger_amd.patch import apply_metal_liger_to_qwen3vl
+    from oracle import reference_ops as ref
+
+    monkeypatch.setattr(MetalLigerRMSNorm, "forward",
+                        lambda self, x: ref.rms_norm_forward(x, self.weight, self.eps)[0])
+    monkeypatch.setattr(fa, "_FusedAddRMSNormFunction", _OracleAddNorm)
+    base = qwen_tiny.build(seed=6, lora=False, peft_wrap=False)
+    assert fa.patch_residual_add_norm(base) == 0                    # HF norms: not eligible
+    kw = dict(fuse_swiglu=False, fuse_lora=False)
+    unfused = apply_metal_liger_to_qwen3vl(copy.deepcopy(base), **kw)
+    fused = apply_metal_liger_to_qwen3vl(copy.deepcopy(base), fuse_residual_norm=True, **kw)
+    assert all(getattr(layer, "_metal_liger_add_norm", False) for layer in fused.model.layers)
+    assert list(fused.state_dict()) == list(unfused.state_dict())
+    assert fa.patch_residual_add_norm(fused) == 0                   # idempotent
+
+    ids = torch.randint(0, 512, (2, 20), generator=torch.Generator().manual_seed(3))
+    outs = []
+    for m in (unfused, fused):
+        m.zero_grad()
+        logits = m(input_ids=ids).logits
+        logits.float().square().mean().backward()
+        outs.append((logits.detach(), {n: p.grad.clone() for n, p in m.named_parameters()}))
+    assert _OracleAddNorm.calls == 2                                # one per layer
+    assert torch.equal(outs[0][0], outs[1][0])
+    for n, g in outs[0][1].items():
+        assert torch.equal(outs[1][1][n], g), n
+
+    assert fa.patch_residual_add_norm(_ExtraAddLayer()) == 0
+    from transformers.models.qwen3_vl.modeling_qwen3_vl import Qwen3VLTextDecoderLayer
+    assert fa._structure(Qwen3VLTextDecoderLayer.forward) == (fa._LAYER_PARTS, 2)
+
+
 class _OracleFLCE:
     """Stand-in for the fused loss's autograd Function on the CPU: the
     oracle's chunked CE (mean over valid tokens, 0 when none is valid)."""
