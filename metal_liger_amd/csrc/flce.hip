@@ -209,44 +209,46 @@ __global__ __launch_bounds__(1024) void count_valid_kernel(const int64_t* __rest
 // 16-byte vector; 8 divides the 64-column partial block).
 constexpr int kDlogitUnroll = 4;
 
-__global__ __launch_bounds__(256) void dlogit_pass_kernel(bf16* __restrict__ E, int64_t ldE, int rows,
-                                                          int V, const float* __restrict__ pmax,
-                                                          int nblk, const float* __restrict__ lse,
-                                                          const int64_t* __restrict__ labels,
-                                                          int64_t ignore,
-                                                          const float* __restrict__ n_valid) {
-  // Consecutive lanes take consecutive 16-byte vectors (whole cache lines
-  // per instruction); each thread holds kDlogitUnroll vectors, one grid
-  // stride apart, with every load issued before the first store.
-  const int vpr = V / 8;  // vectors per row
-  const int64_t total = (int64_t)rows * vpr;
-  const int64_t stride = (int64_t)gridDim.x * 256;
-  const float inv = 1.0f / fmaxf(n_valid[0], 1.0f);
-  for (int64_t q0 = (int64_t)blockIdx.x * 256 + threadIdx.x; q0 < total;
-       q0 += kDlogitUnroll * stride) {
-    float e[kDlogitUnroll][8], f[kDlogitUnroll], sc[kDlogitUnroll];
-    int v0[kDlogitUnroll];
-    int64_t lab[kDlogitUnroll];
-    bf16* p[kDlogitUnroll];
+__global__ __launch_bounds__(256) void dlogit_pass_kernel(
+    bf16* __restrict__ E, int64_t ldE, int rows, int V, const float* __restrict__ pmax, int nblk,
+    const float* __restrict__ lse, const int64_t* __restrict__ labels, int64_t ignore,
+    const float* __restrict__ n_valid) {
+  // Block (x, y) rewrites 256 * kDlogitUnroll consecutive 16-byte vectors of
+  // row y (consecutive lanes, consecutive vectors: whole cache lines per
+  // instruction), every load issued before the first store. The row's
+  // label, scale and lse are uniform (scalar loads); the one-hot term is a
+  // branch only the lane holding the label column takes. Rows past
+  // gridDim.y (at most 65535) are taken in turn.
+  for (int row = blockIdx.y; row < rows; row += gridDim.y) {
+    const int vpr = V / 8;  // vectors per row
+    const int64_t lab = labels[row];
+    const float sc = lab != ignore ? 1.0f / fmaxf(n_valid[0], 1.0f) : 0.f;
+    const float lse_r = lse[row];
+    const float* pm = pmax + (int64_t)row * nblk;
+    bf16* er = E + (int64_t)row * ldE;
+    const int j0 = blockIdx.x * (256 * kDlogitUnroll) + threadIdx.x;
+    float e[kDlogitUnroll][8], f[kDlogitUnroll];
 #pragma unroll
     for (int u = 0; u < kDlogitUnroll; ++u) {
-      const int64_t q = q0 + u * stride;
-      p[u] = nullptr;
-      if (q >= total) continue;
-      const int r = (int)(q / vpr);
-      v0[u] = (int)(q - (int64_t)r * vpr) * 8;
-      lab[u] = labels[r];
-      sc[u] = lab[u] != ignore ? inv : 0.f;
-      f[u] = exp_f(pmax[(int64_t)r * nblk + v0[u] / kColBlock] - lse[r]) * sc[u];
-      p[u] = E + (int64_t)r * ldE + v0[u];
-      load_n<bf16, 8>(p[u], e[u]);
+      const int j = j0 + u * 256;
+      if (j < vpr) {
+        f[u] = exp_f(pm[(j * 8) / kColBlock] - lse_r) * sc;
+        load_n<bf16, 8>(er + j * 8, e[u]);
+      }
     }
 #pragma unroll
     for (int u = 0; u < kDlogitUnroll; ++u) {
-      if (p[u] == nullptr) continue;
+      const int j = j0 + u * 256;
+      if (j >= vpr) continue;
 #pragma unroll
-      for (int k = 0; k < 8; ++k) e[u][k] = e[u][k] * f[u] - (v0[u] + k == lab[u] ? sc[u] : 0.f);
-      store_n<bf16, 8>(p[u], e[u]);
+      for (int k = 0; k < 8; ++k) e[u][k] = e[u][k] * f[u];
+      const int64_t d = lab - (int64_t)j * 8;
+      if (d >= 0 && d < 8) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+          if (k == (int)d) e[u][k] = e[u][k] - sc;
+      }
+      store_n<bf16, 8>(er + j * 8, e[u]);
     }
   }
 }
@@ -591,11 +593,10 @@ int fwd_grad_impl(const bf16* hidden, int64_t ldh, const bf16* weight, int64_t l
     ML_LAUNCH_CHECK();
     if (!grads) continue;
     {  // 3. dlogits in place
-      const int64_t vec = (int64_t)Tc * (V / 8);
-      int64_t blocks = (vec + 256 * kDlogitUnroll - 1) / (256 * kDlogitUnroll);
-      blocks = blocks < 8192 ? blocks : 8192;
-      dlogit_pass_kernel<<<dim3((unsigned)blocks), 256, 0, st>>>(w.E, V, Tc, V, w.pmax, nblk,
-                                                                 lse + t0, lc, ignore, n_valid);
+      const int segs = (int)((V / 8 + 256 * kDlogitUnroll - 1) / (256 * kDlogitUnroll));
+      const int ys = Tc < 65535 ? Tc : 65535;
+      dlogit_pass_kernel<<<dim3((unsigned)segs, (unsigned)ys), 256, 0, st>>>(
+          w.E, V, Tc, (int)V, w.pmax, nblk, lse + t0, lc, ignore, n_valid);
       ML_LAUNCH_CHECK();
     }
     if (d_hidden) {  // 4. dH_c = D W (split-K over the vocabulary)
