@@ -384,7 +384,6 @@ int launch_qkn(QknArgs& a, int64_t B, int64_t D, const DwReduceArgs* red, hipStr
 template <typename F>
 int dispatch_qkn(int x_dtype, int w_dtype, F&& f) {
   return dispatch_dtype(x_dtype, [&](auto tx) -> int {
-    using TX = decltype(tx);
     if (w_dtype == ML_F32) return f(tx, float{});
     ML_CHECK(w_dtype == x_dtype, "qk_norm_rope: weight dtype %d must be fp32 or x's dtype %d",
              w_dtype, x_dtype);
