@@ -63,3 +63,27 @@ def register_fp32_attention(name="ml_fp32_eager"):
 
     AttentionInterface.register(name, attn)
     return name
+
+
+def build_vl(seed=0, attn="eager", dtype=torch.float32):
+    """A tiny Qwen3-VL (text stack as tiny_config, interleaved M-RoPE; a
+    one-block vision tower), norm weights 1 + 0.1 N(0, 1)."""
+    from transformers import Qwen3VLConfig, Qwen3VLForConditionalGeneration
+    cfg = Qwen3VLConfig(
+        text_config=dict(vocab_size=512, hidden_size=128, intermediate_size=256,
+                         num_hidden_layers=2, num_attention_heads=4, num_key_value_heads=2,
+                         head_dim=32, rms_norm_eps=1e-6, rope_theta=1e6,
+                         max_position_embeddings=256,
+                         rope_scaling={"rope_type": "default", "mrope_section": [8, 4, 4],
+                                       "mrope_interleaved": True}),
+        vision_config=dict(depth=1, hidden_size=64, intermediate_size=128, num_heads=2,
+                           out_hidden_size=128, deepstack_visual_indexes=[]))
+    cfg._attn_implementation = attn
+    cfg.text_config._attn_implementation = attn
+    torch.manual_seed(seed)
+    model = Qwen3VLForConditionalGeneration(cfg)
+    with torch.no_grad():
+        for n, p in model.named_parameters():
+            if n.endswith("norm.weight"):
+                p.normal_(1.0, 0.1)
+    return model.to(dtype)

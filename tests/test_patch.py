@@ -278,3 +278,72 @@ def test_causal_lm_loss_hook_matches_transformers(monkeypatch):
         ev = lm(input_ids=ids, labels=labels)
     assert ev.logits is not None and _OracleFLCE.calls == 2
     assert torch.allclose(ev.loss, want.loss, rtol=1e-5, atol=1e-6)
+
+
+class _OracleSwiGLU:
+    """Stand-in for the fused SwiGLU Function on the CPU."""
+
+    @staticmethod
+    def apply(gate, up):
+        from oracle import reference_ops as ref
+        return ref.swiglu_forward(gate, up)[0]
+
+
+def test_qwen3_vl_text_stack_patched(monkeypatch):
+    """apply_metal_liger_to_qwen3vl on a Qwen3-VL model (the reference's
+    target, patch.py:181-240): the language model's layer and final norms,
+    MLPs, q/k norms + RoPE, post-attention add + norm and the training loss
+    are routed, the vision tower is left alone, state_dict keys are
+    unchanged; with every fused op swapped for the oracle on the CPU, the
+    loss and all gradients match the unpatched model (fp32 bar: the fused
+    loss is the chunked CE, SwiGLU the reference's sigmoid form)."""
+    import copy
+
+    import metal_liger_amd.ops.fused_add_rms_norm as fa
+    import metal_liger_amd.ops.fused_linear_cross_entropy as fl
+    import metal_liger_amd.ops.fused_qk_norm_rope as fq
+    import metal_liger_amd.ops.fused_swiglu as fs
+    from metal_liger_amd import MetalLigerRMSNorm, MetalLigerSwiGLU, apply_metal_liger_to_qwen3vl
+    from oracle import reference_ops as ref
+
+    def oracle_qkn(q, k, q_norm, k_norm, cos, sin, unsqueeze_dim=1):
+        c, s = cos.unsqueeze(unsqueeze_dim), sin.unsqueeze(unsqueeze_dim)
+        return (ref.qk_norm_rope_forward(q, q_norm.weight, q_norm.variance_epsilon, c, s),
+                ref.qk_norm_rope_forward(k, k_norm.weight, k_norm.variance_epsilon, c, s))
+
+    monkeypatch.setattr(MetalLigerRMSNorm, "forward",
+                        lambda self, x: ref.rms_norm_forward(x, self.weight, self.eps)[0])
+    monkeypatch.setattr(fs, "_FusedSwiGLUFunction", _OracleSwiGLU)
+    monkeypatch.setattr(fq, "apply_fused_qk_norm_rope", oracle_qkn)
+    monkeypatch.setattr(fa, "_FusedAddRMSNormFunction", _OracleAddNorm)
+    monkeypatch.setattr(fl, "_FusedLinearCrossEntropyFunction", _OracleFLCE)
+
+    base = qwen_tiny.build_vl(seed=8)
+    keys = list(base.state_dict())
+    patched = apply_metal_liger_to_qwen3vl(copy.deepcopy(base), fuse_rope=True,
+                                           fuse_cross_entropy=True, fuse_residual_norm=True)
+    lm = patched.model.language_model
+    assert sum(isinstance(m, MetalLigerRMSNorm) for m in patched.modules()) == 2 * 2 + 1
+    assert all(isinstance(layer.mlp, MetalLigerSwiGLU) for layer in lm.layers)
+    assert all(getattr(layer.self_attn, "_metal_liger_qk_norm_rope", False) for layer in lm.layers)
+    assert all(getattr(layer, "_metal_liger_add_norm", False) for layer in lm.layers)
+    assert getattr(patched, "_metal_liger_flce_loss", False)
+    assert not any(isinstance(m, (MetalLigerRMSNorm, MetalLigerSwiGLU))
+                   for m in patched.model.visual.modules())
+    assert list(patched.state_dict()) == keys
+
+    ids = torch.randint(0, 512, (2, 24), generator=torch.Generator().manual_seed(4))
+    results = []
+    for m in (base, patched):
+        m.train()
+        m.zero_grad()
+        out = m(input_ids=ids, labels=ids)
+        out.loss.backward()
+        results.append((out.loss.detach(), {n: p.grad for n, p in m.named_parameters()
+                                            if p.grad is not None}))
+    (l0, g0), (l1, g1) = results
+    assert torch.allclose(l1, l0, rtol=1e-5, atol=1e-6), (l1, l0)
+    assert set(g1) == set(g0) and len(g0) > 0
+    for n, g in g0.items():
+        err = (g1[n].double() - g.double()).abs().max()
+        assert err <= 1e-4 * g.double().abs().max() + 1e-7, n
