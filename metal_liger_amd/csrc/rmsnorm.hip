@@ -325,52 +325,42 @@ __global__ __launch_bounds__(kGenericThreads) void rms_bwd_generic(
 }
 
 // Sums G partial rows in a fixed order.
-// Vector form (cols % 4 == 0): a block covers 16 columns as 4 vectors of 4
-// floats x 64 row slices; thread (slice r, vector cv) sums rows r, r + 64,
-// ... with 16-byte loads (unrolled, so several are in flight), then the 64
-// slices are added in a fixed binary tree through LDS.
-// Scalar form (any cols): 32 columns x 8 row slices per block.
-constexpr int kRedVec = 4;      // column vectors per block (vector form)
-constexpr int kRedSlices = 64;  // row slices per block (vector form)
+// Wave form (cols % 4 == 0, G <= 256): one wave per 4-column vector, lane l
+// summing partial rows l, l + 64, ... (16-byte loads, all in flight
+// together), then a fixed-order wave reduction. No LDS and no barrier: the
+// reduction is one L2 round trip.
+constexpr int kRedWaveRows = 4;  // partial rows per lane (G <= 64 * kRedWaveRows)
 
 template <typename TW>
-__global__ __launch_bounds__(256) void rms_dw_reduce_vec(const float* __restrict__ partial, int G,
-                                                          int64_t cols, TW* __restrict__ dw) {
-  __shared__ float sm[kRedSlices][kRedVec * 4 + 1];
-  const int cv = threadIdx.x % kRedVec;
-  const int r = threadIdx.x / kRedVec;
-  const int64_t c = ((int64_t)blockIdx.x * kRedVec + cv) * 4;
-  float s[4] = {0.f, 0.f, 0.f, 0.f};
-  if (c < cols) {
-    int g = r;
-#pragma unroll 4
-    for (; g < G; g += kRedSlices) {
-      float v[4];
-      load_n<float, 4>(partial + (int64_t)g * cols + c, v);
+__global__ __launch_bounds__(256) void rms_dw_reduce_wave(const float* __restrict__ partial, int G,
+                                                           int64_t cols, TW* __restrict__ dw) {
+  const int lane = threadIdx.x & 63;
+  const int64_t c = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * 4;
+  if (c >= cols) return;
+  float v[kRedWaveRows][4];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) s[e] += v[e];
+  for (int i = 0; i < kRedWaveRows; ++i) {
+    const int g = lane + 64 * i;
+    if (g < G) {
+      load_n<float, 4>(partial + (int64_t)g * cols + c, v[i]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[i][e] = 0.f;
     }
   }
+  float o[4];
 #pragma unroll
-  for (int e = 0; e < 4; ++e) sm[r][cv * 4 + e] = s[e];
-  __syncthreads();
-#pragma unroll
-  for (int half = kRedSlices / 2; half >= 1; half >>= 1) {
-    if (r < half) {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) sm[r][cv * 4 + e] += sm[r + half][cv * 4 + e];
-    }
-    __syncthreads();
+  for (int e = 0; e < 4; ++e) {
+    float t = (v[0][e] + v[1][e]) + (v[2][e] + v[3][e]);
+    o[e] = wave_sum(t);
   }
-  if (r == 0 && c < cols) {
-    float o[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) o[e] = sm[0][cv * 4 + e];
+  if (lane == 0) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) dw[c + e] = from_f32<TW>(o[e]);
   }
 }
 
+// Scalar form (any cols): 32 columns x 8 row slices per block.
 template <typename TW>
 __global__ __launch_bounds__(256) void rms_dw_reduce(const float* __restrict__ partial, int G,
                                                       int64_t cols, TW* __restrict__ dw) {
@@ -527,9 +517,10 @@ int launch_bwd(const void* x, int64_t ldx, const void* w, const void* dy, int64_
     ML_LAUNCH_CHECK();
   }
   if (cols > 0) {
+    static_assert(kMaxBwdBlocks <= 64 * kRedWaveRows, "wave reduction covers every partial row");
     if (cols % 4 == 0)
-      rms_dw_reduce_vec<TW><<<dim3((unsigned)((cols + 4 * kRedVec - 1) / (4 * kRedVec))), 256, 0,
-                              st>>>(part, (int)G, cols, dwp);
+      rms_dw_reduce_wave<TW><<<dim3((unsigned)((cols / 4 + 3) / 4)), 256, 0, st>>>(part, (int)G,
+                                                                                  cols, dwp);
     else
       rms_dw_reduce<TW><<<dim3((unsigned)((cols + 31) / 32)), 256, 0, st>>>(part, (int)G, cols,
                                                                              dwp);
