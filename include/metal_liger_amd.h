@@ -201,7 +201,8 @@ int ml_rope_pos(const void* q, void* q_out, const int64_t* q_geom, const void* k
  *
  * geom (9 int64 per tensor): {B, H, S, x_sb, x_sh, x_ss, y_sb, y_sh, y_ss}.
  * cs_geom (6 int64): {cos_sb, cos_sh, cos_ss, sin_sb, sin_sh, sin_ss}, 0 on
- * broadcast dimensions. k may be NULL (q only).
+ * broadcast dimensions. k may be NULL (q only); a NULL k whose k_geom
+ * describes no elements is an empty k (its weight gradient is zero).
  */
 int ml_qk_norm_rope_fwd(const void* q, void* q_out, const int64_t* q_geom, const void* q_weight,
                         const void* k, void* k_out, const int64_t* k_geom, const void* k_weight,

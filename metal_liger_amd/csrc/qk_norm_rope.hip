@@ -391,6 +391,13 @@ int dispatch_qkn(int x_dtype, int w_dtype, F&& f) {
   });
 }
 
+// k is given when its pointer is, or when its geometry describes no
+// elements (an empty tensor's pointer may be null); NULL k with no geometry
+// or a non-empty one means q only.
+bool k_given(const void* k, const int64_t* k_geom) {
+  return k != nullptr || (k_geom != nullptr && k_geom[0] * k_geom[1] * k_geom[2] == 0);
+}
+
 int setup_qkn(QknArgs& a, int64_t& B, const int64_t* q_geom, const int64_t* k_geom, bool has_k,
               int64_t D, float eps, const void* cos, const void* sin, const int64_t* cs_geom,
               bool bwd) {
@@ -445,7 +452,7 @@ extern "C" int ml_qk_norm_rope_fwd(const void* q, void* q_out, const int64_t* q_
                                    void* stream) {
   QknArgs a;
   int64_t B = 0;
-  int rc = setup_qkn(a, B, q_geom, k_geom, k != nullptr, D, eps, cos, sin, cs_geom, false);
+  int rc = setup_qkn(a, B, q_geom, k_geom, k_given(k, k_geom), D, eps, cos, sin, cs_geom, false);
   if (rc) return rc;
   const void* xs[2] = {q, k};
   void* outs[2] = {q_out, k_out};
@@ -488,7 +495,7 @@ extern "C" int ml_qk_norm_rope_bwd(const void* q, const void* dq_out, void* dq,
                                    void* workspace, size_t workspace_bytes, void* stream) {
   QknArgs a;
   int64_t B = 0;
-  int rc = setup_qkn(a, B, q_geom, k_geom, k != nullptr, D, eps, cos, sin, cs_geom, true);
+  int rc = setup_qkn(a, B, q_geom, k_geom, k_given(k, k_geom), D, eps, cos, sin, cs_geom, true);
   if (rc) return rc;
   const void* xs[2] = {q, k};
   const void* dys[2] = {dq_out, dk_out};
@@ -506,7 +513,7 @@ extern "C" int ml_qk_norm_rope_bwd(const void* q, const void* dq_out, void* dq,
   float* part = static_cast<float*>(workspace);
   for (int i = 0; i < 2; ++i) {
     QknTensor& t = a.t[i];
-    if (dws[i] != nullptr && (i == 0 || k != nullptr)) {
+    if (dws[i] != nullptr && (i == 0 || k_given(k, k_geom))) {
       // part stays null for a tensor without rows (its reduction reads none)
       t.part = t.items > 0 ? part + (i ? a.t[0].blocks * D : 0) : nullptr;
       red.part[i] = t.part;

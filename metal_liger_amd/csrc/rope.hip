@@ -319,7 +319,8 @@ extern "C" int ml_rope_table(const void* q, void* q_out, const int64_t* q_geom, 
   RopeArgs a;
   int rc = setup_common(a, q, q_out, q_geom, k, k_out, k_geom, D, sgn);
   if (rc) return rc;
-  ML_CHECK(cos && sin && cs_geom, "rope: null cos/sin");
+  const bool empty = a.B * a.S * (a.t[0].H + a.t[1].H) == 0;  // nothing is read
+  ML_CHECK(cs_geom && (empty || (cos && sin)), "rope: null cos/sin");
   a.cos = cos;
   a.sin = sin;
   a.csb = cs_geom[0];
@@ -355,7 +356,8 @@ extern "C" int ml_rope_pos(const void* q, void* q_out, const int64_t* q_geom, co
   RopeArgs a;
   int rc = setup_common(a, q, q_out, q_geom, k, k_out, k_geom, D, sgn);
   if (rc) return rc;
-  ML_CHECK(positions && inv_freq, "rope: null positions / inv_freq");
+  const bool empty = a.B * a.S * (a.t[0].H + a.t[1].H) == 0;  // nothing is read
+  ML_CHECK(empty || (positions && inv_freq), "rope: null positions / inv_freq");
   a.pos = positions;
   a.psb = pos_sb;
   a.pss = pos_ss;

@@ -510,6 +510,10 @@ def matmul(a: torch.Tensor, b: torch.Tensor, *, a_t: bool = False, b_t: bool = F
         beta = 0.0
     elif out.shape != (M, N) or out.stride(1) != 1:
         raise ValueError("gemm: out must be a row-major [M, N] tensor")
+    if M == 0 or N == 0:
+        return out
+    if K == 0:   # an empty sum: alpha * 0 + beta * out
+        return out.mul_(beta) if beta != 0.0 else out.zero_()
     if tile_cfg == 0 and ksplit == 1:
         call(
             "ml_gemm_bf16", M, N, K, ptr(a), a.stride(0), 1 if a_t else 0, ptr(b), b.stride(0),
@@ -706,6 +710,8 @@ def lora_linear_out(x2: torch.Tensor, w: torch.Tensor, xa: torch.Tensor,
     out_f = w.shape[0]
     r = xa.shape[1]
     out = torch.empty(N, out_f, dtype=torch.bfloat16, device=x2.device)
+    if N == 0:
+        return out
     call(
         "ml_gemm_bf16_segments", N, out_f, 2, geom([K, r]), _hip.ptrs([x2.data_ptr(), xa.data_ptr()]),
         geom([x2.stride(0), xa.stride(0)]), _hip.ptrs([w.data_ptr(), sb.data_ptr()]),
@@ -726,6 +732,8 @@ def lora_qkv_bwd(x2, dys, ws_, a_stack, bs, scales, xa, rank):
     dX = torch.empty(N, IN, dtype=torch.bfloat16, device=dev)
     dA = torch.empty(3 * rank, IN, dtype=torch.float32, device=dev)
     dBs = [torch.empty(o, rank, dtype=torch.float32, device=dev) for o in outs]
+    if N == 0:   # no tokens: the adapter gradients are empty sums
+        return dX, dA.zero_(), [d.zero_() for d in dBs]
     wsb = _hip.query("ml_lora_qkv_bwd_workspace_bytes", N, IN, geom(outs), rank)
     ws = torch.empty(max(wsb, 16), dtype=torch.uint8, device=dev)
     call(
@@ -748,6 +756,8 @@ def lora_linear_bwd(x2, dy, w, a, b, scale, xa, rank):
     dX = torch.empty(N, IN, dtype=torch.bfloat16, device=dev)
     dA = torch.empty(rank, IN, dtype=torch.float32, device=dev)
     dB = torch.empty(OUT, rank, dtype=torch.float32, device=dev)
+    if N == 0:
+        return dX, dA.zero_(), dB.zero_()
     wsb = _hip.query("ml_lora_linear_bwd_workspace_bytes", N, IN, OUT, rank)
     ws = torch.empty(max(wsb, 16), dtype=torch.uint8, device=dev)
     call(
@@ -772,6 +782,8 @@ def lora_mlp_bwd(x2, gate, up, h, dy, wg, wu, wd, a_gu, a_d, bg, bu, bd, scales,
     dB_G = torch.empty(I, rank, dtype=f32, device=dev)
     dB_U = torch.empty(I, rank, dtype=f32, device=dev)
     dB_D = torch.empty(H, rank, dtype=f32, device=dev)
+    if N == 0:
+        return (dX, dA_GU.zero_(), dA_D.zero_(), dB_G.zero_(), dB_U.zero_(), dB_D.zero_())
     wsb = _hip.query("ml_lora_mlp_bwd_workspace_bytes", N, H, I, rank)
     ws = torch.empty(max(wsb, 16), dtype=torch.uint8, device=dev)
     call(

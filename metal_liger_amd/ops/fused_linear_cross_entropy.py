@@ -108,7 +108,7 @@ class MetalLigerFusedLinearCrossEntropy(nn.Module):
                 labels: torch.Tensor) -> torch.Tensor:
         batch_seq = (hidden_states.shape[0] * hidden_states.shape[1]
                      if hidden_states.ndim == 3 else hidden_states.shape[0])
-        hidden_flat = hidden_states.reshape(batch_seq, -1)
+        hidden_flat = hidden_states.reshape(batch_seq, hidden_states.shape[-1])
         labels_flat = labels.reshape(-1)
         return _FusedLinearCrossEntropyFunction.apply(
             hidden_flat, self.weight, labels_flat,

@@ -102,7 +102,7 @@ def _lora_linear(X: torch.Tensor, W: torch.Tensor,
         rp = _pad_rank(A.shape[0])
         xa = cops.lora_xa(X2, _stack_a([A], rp))
         out = cops.lora_linear_out(X2, W2, xa, _pad_b(B, rp, float(scaling)))
-    return out.view(*shape[:-1], -1)
+    return out.view(*shape[:-1], out.shape[-1])
 
 
 class _LoRA_QKV(torch.autograd.Function):
@@ -137,7 +137,7 @@ class _LoRA_QKV(torch.autograd.Function):
         ctx.rank, ctx.rank_p = r, rp
         ctx.orig_shape = shape
         ctx.param_dtypes = [(A.dtype, B.dtype) for A, B in ((QA, QB), (KA, KB), (VA, VB))]
-        return tuple(o.view(*shape[:-1], -1) for o in outs)
+        return tuple(o.view(*shape[:-1], o.shape[-1]) for o in outs)
 
     @staticmethod
     def backward(ctx, dQ, dK, dV):
@@ -233,7 +233,7 @@ class _LoRA_W(torch.autograd.Function):
         ctx.scale = scale
         ctx.rank, ctx.rank_p = r, rp
         ctx.orig_shape = shape
-        return out.view(*shape[:-1], -1)
+        return out.view(*shape[:-1], out.shape[-1])
 
     @staticmethod
     def backward(ctx, dY):
