@@ -64,6 +64,23 @@ def test_flce_small(dev, N, H, V, chunk):
     check_grads(dh, dw, rdh, rdw, f"N={N} V={V}")
 
 
+def test_flce_token_chunk_over_65535_rows(dev):
+    """A small vocabulary lets the whole batch be one token chunk: 70000
+    rows, more than a grid dimension's 65535 blocks, so the dlogit pass
+    walks its rows in two rounds; the rows past 65535 are checked alone."""
+    from metal_liger_amd import hip_ops
+    N, H, V = 70000, 64, 512
+    assert hip_ops.flce_token_chunk(N, V) == N
+    h, w, lab = make_inputs(N, H, V, seed=77, w_scale=0.3)
+    loss, dh, dw = run_ours(dev, h, w, lab)
+    rl, lse, mask = ref.flce_forward(h, w, lab, None, -100, 8192)
+    rdh, rdw = ref.flce_backward(h, w, lab, lse, mask, torch.tensor(1.0), None, 8192)
+    assert abs(loss.item() - rl.item()) <= 1e-3 * abs(rl.item())
+    check_grads(dh, dw, rdh, rdw, "N=70000")
+    assert_close(dh[65535:], rdh[65535:], "dH rows past 65535")
+    assert rel_fro(dh[65535:], rdh[65535:]) <= 2e-2
+
+
 def test_flce_lse_matches_oracle(dev):
     from metal_liger_amd import hip_ops
     h, w, lab = make_inputs(256, 128, 3000, seed=5, w_scale=0.3)
