@@ -3,8 +3,8 @@
 A restatement, in plain torch on the CPU, of the reference's pure-torch fused
 ops (krrish-v/metal_liger, ops/*.py). Each function follows the cited lines
 op for op, including where the reference casts between dtypes, so that it
-reproduces the reference's rounding sequence on the same inputs. It is the
-checker for the HIP path: only tests/, __graft_entry__.smoke() and
+reproduces the reference's rounding sequence on the same inputs. The HIP
+path is tested against it: only tests/, __graft_entry__.smoke() and
 bench.py's cpu_baseline leg use it, and never as a product code path.
 
 Pinning (what checks this oracle independently of its own formulas) lives in
