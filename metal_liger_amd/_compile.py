@@ -2,7 +2,7 @@
 
 The reference's apply_compile (_compile.py:369-379) is a deprecated no-op
 that logs and returns the model; the rest of that module is an MPS
-graph-capture helper that is not part of this build (the fused ops are
+graph-capture helper that metal_liger_amd does not include (the fused ops are
 ahead-of-time HIP kernels and need no tracing compiler).
 """
 

@@ -136,7 +136,7 @@ def apply_metal_liger_to_qwen3vl(
     post-attention residual add runs in the same launch as its
     post_attention_layernorm (ops/fused_add_rms_norm.py); needs
     fuse_rms_norm, whose norm it extends.
-    use_optimized_generator is not part of this build (inference path).
+    use_optimized_generator is not part of metal_liger_amd (inference path).
     """
     stats = {}
     if fuse_rms_norm:
@@ -161,7 +161,7 @@ def apply_metal_liger_to_qwen3vl(
         stats["fused_lora"] = n
         logger.info(f"MetalLiger: fused LoRA QKV+MLP marked {n} modules")
     if use_optimized_generator:
-        logger.warning("MetalLiger: the optimized generator is not part of this build; skipped")
+        logger.warning("MetalLiger: the optimized generator is not part of metal_liger_amd; skipped")
         stats["generator"] = "unavailable"
     if fuse_rope:
         logger.info("MetalLiger: fused RoPE — use apply_fused_rotary() / apply_fused_rotary_inline()")
