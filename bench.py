@@ -280,41 +280,18 @@ def bench_lora_bwd(dev, stream, reps):
             "tokens_per_s": round(N / (tot * 1e-3), 1)}
 
 
-TRAIN_LAYERS, TRAIN_B, TRAIN_S, TRAIN_V = 4, 4, 2048, 151936
-
-
-def build_train_model(dev, layers=TRAIN_LAYERS):
-    """Qwen3-style decoder (hidden 2048, 16 q / 8 kv heads, head_dim 128, MLP
-    6144, eps 1e-6, theta 1e6, vocab 151936, tied embeddings, HF's random
-    init) with rank-16 alpha-32 LoRA on q, k, v, o, gate, up, down in PEFT's
-    layout, bf16, every fused op patched in. Only the adapters train."""
-    import torch
-    from transformers import Qwen3Config, Qwen3ForCausalLM
-
+def build_train_model(dev, layers=None):
+    """The 4-layer Qwen3-style LoRA train-step model (tests/qwen_tiny.py,
+    build_train_config: hidden 2048, 16 q / 8 kv heads, head_dim 128, MLP
+    6144, vocab 151936, tied embeddings, rank-16 LoRA on q, k, v, o, gate,
+    up, down, bf16) with every fused op patched in; only the adapters
+    train."""
     from metal_liger_amd import apply_metal_liger_to_qwen3vl
-    from tests.peft_shim import LoraLinear, init_lora, wrap_lora
-    from tests.qwen_tiny import PeftLike
-    cfg = Qwen3Config(vocab_size=TRAIN_V, hidden_size=LORA_H, intermediate_size=LORA_I,
-                      num_hidden_layers=layers, num_attention_heads=16, num_key_value_heads=8,
-                      head_dim=128, rms_norm_eps=1e-6, rope_theta=THETA,
-                      max_position_embeddings=TRAIN_S, tie_word_embeddings=True)
-    cfg._attn_implementation = "sdpa"
-    torch.manual_seed(0)
-    with torch.device(dev):
-        lm = Qwen3ForCausalLM(cfg)
-    for i, layer in enumerate(lm.model.layers):
-        wrap_lora(layer.self_attn, ["q_proj", "k_proj", "v_proj", "o_proj"], r=LORA_R, alpha=32)
-        wrap_lora(layer.mlp, ["gate_proj", "up_proj", "down_proj"], r=LORA_R, alpha=32)
-        for j, m in enumerate(list(layer.self_attn.children()) + list(layer.mlp.children())):
-            if isinstance(m, LoraLinear):
-                init_lora(m, 10 * i + j)
-    lm.to(device=dev, dtype=torch.bfloat16)
-    # the patcher wraps norm weights in new (trainable) Parameters, as the
-    # reference's MetalLigerRMSNorm does: freeze after patching
-    model = apply_metal_liger_to_qwen3vl(PeftLike(lm), fuse_rope=True, fuse_cross_entropy=True,
+    from tests import qwen_tiny
+    model = qwen_tiny.build_train_config(dev, layers or qwen_tiny.TRAIN_LAYERS)
+    model = apply_metal_liger_to_qwen3vl(model, fuse_qk_norm_rope=True, fuse_lm_loss=True,
                                          fuse_residual_norm=True)
-    for n, p in model.named_parameters():
-        p.requires_grad_("lora_" in n)
+    qwen_tiny.freeze_all_but_lora(model)
     return model
 
 
@@ -333,12 +310,12 @@ def bench_train_step(dev, steps=5, warmup=2):
     import torch
     from torch.nn.attention import SDPBackend, sdpa_kernel
 
+    from tests import qwen_tiny
     model = build_train_model(dev)
     model.train()
     params = [p for p in model.parameters() if p.requires_grad]
     opt = torch.optim.AdamW(params, lr=1e-4, foreach=True)
-    g = torch.Generator().manual_seed(0)
-    ids = torch.randint(0, TRAIN_V, (TRAIN_B, TRAIN_S), generator=g).to(dev)
+    ids = qwen_tiny.train_ids(dev)
 
     def step():
         opt.zero_grad(set_to_none=True)
@@ -363,8 +340,8 @@ def bench_train_step(dev, steps=5, warmup=2):
     last = loss.item()
     if not (math.isfinite(first) and math.isfinite(last)):
         raise RuntimeError(f"train step: non-finite loss {first} -> {last}")
-    n_tok = TRAIN_B * TRAIN_S
-    return {"layers": TRAIN_LAYERS, "tokens": n_tok, "ms_per_step": round(dt * 1e3, 2),
+    n_tok = qwen_tiny.TRAIN_B * qwen_tiny.TRAIN_S
+    return {"layers": qwen_tiny.TRAIN_LAYERS, "tokens": n_tok, "ms_per_step": round(dt * 1e3, 2),
             "tokens_per_s": round(n_tok / dt, 1), "loss_first": round(first, 4),
             "loss_last": round(last, 4), "steps": steps, "warmup": warmup,
             "includes": "fwd + FLCE loss (model(input_ids, labels=input_ids)) + bwd + AdamW on LoRA params",

@@ -933,16 +933,6 @@ __device__ __forceinline__ void big_mainloop(const Problem& pb, int tm, int tn, 
         acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(f.a[i], f.b[j], acc[i][j], 0, 0, 0);
     big_barrier();
   };
-#ifdef ML_BIG_ROLLED
-  // k-tile t reads stage t % STAGES and loads stage (t + DIST) % STAGES.
-  uint32_t rd = 0, wr = big::DIST * big::STAGE_BYTES;
-  constexpr uint32_t kWrap = big::STAGES * big::STAGE_BYTES;
-  for (int t = 0; t < nk; ++t) {
-    iteration(lds + rd, lds + wr);
-    rd = rd + big::STAGE_BYTES == kWrap ? 0u : rd + big::STAGE_BYTES;
-    wr = wr + big::STAGE_BYTES == kWrap ? 0u : wr + big::STAGE_BYTES;
-  }
-#else
   // The body runs the stages in turn; the k-tile count is rounded up to a
   // multiple of STAGES (the extra k-tiles are zeros and add nothing).
   for (int t = 0; t < nk; t += big::STAGES) {
@@ -951,7 +941,6 @@ __device__ __forceinline__ void big_mainloop(const Problem& pb, int tm, int tn, 
       iteration(lds + j * big::STAGE_BYTES, lds + ((j + big::DIST) % big::STAGES) * big::STAGE_BYTES);
     });
   }
-#endif
   if (grp == 0) big_barrier();
   __builtin_amdgcn_s_waitcnt(big::kWaitVm0);
   __syncthreads();  // loads past the end have landed; the epilogue may reuse the LDS

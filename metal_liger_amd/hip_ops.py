@@ -671,7 +671,7 @@ def _bf16_rows(t: torch.Tensor) -> torch.Tensor:
     launching wrappers (_al16)."""
     if t.dtype != torch.bfloat16:
         t = t.to(torch.bfloat16)
-    if t.dim() != 2 or t.stride(1) != 1 or t.stride(0) % 8 != 0:
+    if t.dim() != 2 or t.stride(1) != 1 or t.stride(0) % 8 != 0 or t.stride(0) < t.shape[1]:
         t = t.contiguous()
     return t
 
@@ -682,6 +682,19 @@ def _al16(*ts):
     out = []
     for t in ts:
         if t is not None and t.data_ptr() % 16 != 0:
+            t = t.clone(memory_format=torch.contiguous_format)
+        out.append(t)
+    return out if len(out) > 1 else out[0]
+
+
+def _dense16(*ts):
+    """The tensors as dense row-major 2-D blocks (row stride == width) with
+    16-byte aligned bases, copying any that is not: the LoRA backward entry
+    points take no leading dimensions. None passes through."""
+    out = []
+    for t in ts:
+        if t is not None and (t.stride(-1) != 1 or t.stride(0) != t.shape[-1]
+                              or t.data_ptr() % 16 != 0):
             t = t.clone(memory_format=torch.contiguous_format)
         out.append(t)
     return out if len(out) > 1 else out[0]
@@ -724,8 +737,8 @@ def lora_linear_out(x2: torch.Tensor, w: torch.Tensor, xa: torch.Tensor,
 def lora_qkv_bwd(x2, dys, ws_, a_stack, bs, scales, xa, rank):
     """Returns (dX bf16 [N, in], dA fp32 [3r, in], [dB_i fp32 [out_i, r]])."""
     ensure_rocm_device(x2, *dys, *ws_, a_stack, *bs, xa)
-    x2, a_stack, xa = _al16(x2, a_stack, xa)
-    dys, ws_, bs = [_al16(*t) for t in (dys, ws_, bs)]
+    x2, a_stack, xa = _dense16(x2, a_stack, xa)
+    dys, ws_, bs = [list(_dense16(*t, None))[:-1] for t in (dys, ws_, bs)]
     N, IN = x2.shape
     outs = [int(d.shape[1]) for d in dys]
     dev = x2.device
@@ -749,7 +762,7 @@ def lora_linear_bwd(x2, dy, w, a, b, scale, xa, rank):
     """One LoRA projection's backward: (dX bf16 [N, in], dA fp32 [r, in],
     dB fp32 [out, r])."""
     ensure_rocm_device(x2, dy, w, a, b, xa)
-    x2, dy, w, a, b, xa = _al16(x2, dy, w, a, b, xa)
+    x2, dy, w, a, b, xa = _dense16(x2, dy, w, a, b, xa)
     N, IN = x2.shape
     OUT = int(dy.shape[1])
     dev = x2.device
@@ -770,7 +783,7 @@ def lora_linear_bwd(x2, dy, w, a, b, scale, xa, rank):
 def lora_mlp_bwd(x2, gate, up, h, dy, wg, wu, wd, a_gu, a_d, bg, bu, bd, scales, xa_gu, ha_d, rank):
     """Returns (dX, dA_GU [2r, H], dA_D [r, I], dB_G [I, r], dB_U [I, r], dB_D [H, r])."""
     ensure_rocm_device(x2, gate, up, h, dy, wg, wu, wd, a_gu, a_d, bg, bu, bd, xa_gu, ha_d)
-    (x2, gate, up, h, dy, wg, wu, wd, a_gu, a_d, bg, bu, bd, xa_gu, ha_d) = _al16(
+    (x2, gate, up, h, dy, wg, wu, wd, a_gu, a_d, bg, bu, bd, xa_gu, ha_d) = _dense16(
         x2, gate, up, h, dy, wg, wu, wd, a_gu, a_d, bg, bu, bd, xa_gu, ha_d)
     N, H = x2.shape
     I = gate.shape[1]

@@ -77,16 +77,30 @@ def fused_add_rms_norm(x: torch.Tensor, residual: torch.Tensor, norm: nn.Module)
 _LAYER_PARTS = ("input_layernorm", "self_attn", "post_attention_layernorm", "mlp")
 
 
+_CONTAINER_OPS = ("BUILD_TUPLE", "BUILD_LIST", "LIST_APPEND", "LIST_EXTEND", "LIST_TO_TUPLE")
+
+
 def _structure(fn) -> tuple:
-    """(attribute loads of the layer parts in order, number of additions) of
-    a forward's bytecode."""
-    parts, adds = [], 0
+    """(attribute loads of the layer parts in order, number of additions
+    (in-place ones included), whether every return hands back one local
+    variable and no tuple or list is built) of a forward's bytecode. The
+    fused forward returns one tensor, so a layer that returns an outputs
+    tuple (older transformers: ``outputs = (hidden_states,)`` with attention
+    weights appended by ``+=``) does not match."""
+    parts, adds, single = [], 0, True
+    prev = None
     for ins in dis.get_instructions(fn):
         if ins.opname in ("LOAD_ATTR", "LOAD_METHOD") and ins.argval in _LAYER_PARTS:
             parts.append(ins.argval)
-        elif ins.opname == "BINARY_ADD" or (ins.opname == "BINARY_OP" and ins.argrepr == "+"):
+        elif ins.opname in ("BINARY_ADD", "INPLACE_ADD") or (
+                ins.opname == "BINARY_OP" and ins.argrepr in ("+", "+=")):
             adds += 1
-    return tuple(parts), adds
+        elif ins.opname in _CONTAINER_OPS:
+            single = False
+        elif ins.opname == "RETURN_VALUE" and (prev is None or prev.opname != "LOAD_FAST"):
+            single = False
+        prev = ins
+    return tuple(parts), adds, single
 
 
 def _eligible(layer: nn.Module) -> bool:
@@ -99,7 +113,7 @@ def _eligible(layer: nn.Module) -> bool:
         params = inspect.signature(fwd).parameters
     except (TypeError, ValueError):
         return False
-    return "hidden_states" in params and _structure(fwd) == (_LAYER_PARTS, 2)
+    return "hidden_states" in params and _structure(fwd) == (_LAYER_PARTS, 2, True)
 
 
 def _make_forward(layer: nn.Module, orig_fwd):

@@ -24,8 +24,9 @@ Semantics kept from the reference: labels are not shifted; ignore_index
 tokens contribute nothing; the mean divides by max(#valid, 1) (all-ignored
 batches give loss 0); the loss is fp32; no bias gradient is returned.
 
-``patch_causal_lm_loss(model)`` goes one step further than the reference
-(whose patcher only logs for ``fuse_cross_entropy``, patch.py:230-232): a
+``patch_causal_lm_loss(model)`` (``apply_metal_liger_to_qwen3vl(...,
+fuse_lm_loss=True)``) goes one step further than the reference, whose
+patcher only logs for ``fuse_cross_entropy`` (patch.py:230-232): a
 causal LM called with ``labels`` while training gets its loss from the fused
 op, with transformers' label shift and ``num_items_in_batch`` handling, and
 never forms the logits.
@@ -39,6 +40,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from metal_liger_amd import _custom_ops as cops
+from metal_liger_amd._model_walk import shadowed
 
 
 class _FusedLinearCrossEntropyFunction(torch.autograd.Function):
@@ -184,18 +186,10 @@ def _make_lm_forward(lm: nn.Module, orig_fwd, chunk_size: int):
                                   kw.get("ignore_index", -100), kw.get("shift_labels"), chunk_size)
 
         token = _LOSS_STATE.set(state)
-        had = "_loss_function" in lm.__dict__
-        prev = lm.__dict__.get("_loss_function")
-        lm.__dict__["lm_head"] = _identity
-        lm.__dict__["_loss_function"] = loss_fn
         try:
-            out = orig_fwd(*args, **kwargs)
+            with shadowed(lm, lm_head=_identity, _loss_function=loss_fn):
+                out = orig_fwd(*args, **kwargs)
         finally:
-            lm.__dict__.pop("lm_head", None)
-            if had:
-                lm.__dict__["_loss_function"] = prev
-            else:
-                lm.__dict__.pop("_loss_function", None)
             _LOSS_STATE.reset(token)
         if not state["used"]:
             raise RuntimeError(f"fused causal-LM loss: {type(lm).__name__}.forward did not call "

@@ -28,14 +28,13 @@ activation dtypes raise.
 """
 
 import logging
-import types
-from typing import Any, Optional, Tuple  # noqa: F401
 
 import torch
 import torch.nn as nn
 
 from metal_liger_amd import _custom_ops as cops
 from metal_liger_amd import hip_ops
+from metal_liger_amd._model_walk import find_layers, shadowed
 
 logger = logging.getLogger(__name__)
 
@@ -293,88 +292,87 @@ def apply_fused_lora_mlp(mlp_module, X: torch.Tensor) -> torch.Tensor:
     )
 
 
+_QKV_PROJ = ("q_proj", "k_proj", "v_proj")
+_MLP_PROJ = ("gate_proj", "up_proj", "down_proj")
+
+
+def _all_lora(module: nn.Module, names) -> bool:
+    """Every projection in `names` exists on module and carries a LoRA adapter."""
+    return all(_get_lora_params(getattr(module, n, None))[1] is not None for n in names)
+
+
+class _Returns:
+    """Stands in for a projection whose output is already computed."""
+
+    __slots__ = ("value",)
+
+    def __init__(self, value):
+        self.value = value
+
+    def __call__(self, *_args, **_kwargs):
+        return self.value
+
+
+class _FusedAttentionForward:
+    """Forward of an attention module whose q/k/v projections all carry
+    LoRA: q, k and v come from one _LoRA_QKV call on the hidden states, and
+    the module's own forward then runs with q/k/v_proj shadowed by those
+    results (o_proj by _LoRA_W when it carries LoRA too, which the
+    reference's patcher leaves to PEFT)."""
+
+    def __init__(self, attn: nn.Module, original):
+        self.attn = attn
+        self.original = original
+        o_proj = getattr(attn, "o_proj", None)
+        self.o_proj = o_proj if _all_lora(attn, ("o_proj",)) else None
+
+    def __call__(self, hidden_states, *args, **kwargs):
+        q, k, v = apply_fused_lora_qkv(self.attn, hidden_states)
+        subs = dict(zip(_QKV_PROJ, (_Returns(q), _Returns(k), _Returns(v))))
+        if self.o_proj is not None:
+            o_proj = self.o_proj
+            subs["o_proj"] = lambda x: apply_fused_lora_linear(o_proj, x)
+        with shadowed(self.attn, **subs):
+            return self.original(hidden_states, *args, **kwargs)
+
+
+class _FusedMLPForward:
+    """Forward of an MLP whose gate/up/down projections all carry LoRA: the
+    whole block is one _LoRA_MLP call."""
+
+    def __init__(self, mlp: nn.Module):
+        self.mlp = mlp
+
+    def __call__(self, x):
+        return apply_fused_lora_mlp(self.mlp, x)
+
+
 def patch_fused_lora(model: nn.Module) -> int:
-    """Routes every attention / MLP with LoRA on all three projections through
-    the fused functions (ops/fused_lora.py:323-421). Modules are not
-    replaced: attention forwards shadow q/k/v_proj in the instance __dict__
-    with the precomputed fused results for the duration of the call, so
-    state_dict keys stay unchanged. Returns the number of patched modules.
+    """Routes every decoder layer's attention and MLP whose three
+    projections all carry LoRA through _LoRA_QKV / _LoRA_MLP and returns how
+    many modules were routed (ops/fused_lora.py:323-421).
 
-    The layer search starts at PEFT's ``base_model.model``; a bare HF model's
-    ``base_model`` (its decoder, which has no ``.model``) is searched as is,
-    where the reference raises AttributeError."""
-    base = getattr(model, 'base_model', model)
-    base = getattr(base, 'model', base)
-
-    def _find_layers_list(m, depth=0):
-        if depth > 6:
-            return None
-        for name, child in m.named_children():
-            if name == 'layers' and len(list(child.children())) > 0:
-                return child
-            result = _find_layers_list(child, depth + 1)
-            if result is not None:
-                return result
-        return None
-
-    layers = _find_layers_list(base)
+    Only the instances' ``forward`` attributes change (no module is replaced
+    and q/k/v_proj are shadowed only while an attention forward runs), so
+    state_dict keys and checkpoints are unaffected. The decoder layers are
+    found as the model patcher finds them (PEFT's base_model.model, a bare
+    HF model or decoder, Qwen3-VL's language_model); modules already routed
+    are left as they are, so a second call returns 0."""
+    layers = find_layers(model)
     if layers is None:
         logger.warning("MetalLiger fused LoRA: could not find transformer layers")
         return 0
-
-    patched = 0
+    routed = 0
     for layer in layers:
-        attn = getattr(layer, 'self_attn', None)
-        mlp = getattr(layer, 'mlp', None)
-
-        if attn is not None:
-            has_q = hasattr(attn, 'q_proj') and _get_lora_params(attn.q_proj)[1] is not None
-            has_k = hasattr(attn, 'k_proj') and _get_lora_params(attn.k_proj)[1] is not None
-            has_v = hasattr(attn, 'v_proj') and _get_lora_params(attn.v_proj)[1] is not None
-
-            if has_q and has_k and has_v:
-                orig_fwd = attn.forward
-                # o_proj with LoRA goes through _LoRA_W (the reference's
-                # patcher leaves it to PEFT)
-                o_proj = getattr(attn, 'o_proj', None)
-                fuse_o = o_proj is not None and _get_lora_params(o_proj)[1] is not None
-
-                def _make_fused_forward(orig_fwd, o_proj, fuse_o):
-                    def _fused_forward(self_attn, hidden_states, *args, **kwargs):
-                        Q, K, V = apply_fused_lora_qkv(self_attn, hidden_states)
-                        self_attn.__dict__['q_proj'] = lambda x: Q
-                        self_attn.__dict__['k_proj'] = lambda x: K
-                        self_attn.__dict__['v_proj'] = lambda x: V
-                        if fuse_o:
-                            self_attn.__dict__['o_proj'] = lambda x: apply_fused_lora_linear(o_proj, x)
-                        try:
-                            return orig_fwd(hidden_states, *args, **kwargs)
-                        finally:
-                            self_attn.__dict__.pop('q_proj', None)
-                            self_attn.__dict__.pop('k_proj', None)
-                            self_attn.__dict__.pop('v_proj', None)
-                            self_attn.__dict__.pop('o_proj', None)
-
-                    return _fused_forward
-
-                attn.forward = types.MethodType(_make_fused_forward(orig_fwd, o_proj, fuse_o), attn)
-                attn._metal_liger_fused_lora = True
-                patched += 1
-
-        if mlp is not None:
-            has_gate = hasattr(mlp, 'gate_proj') and _get_lora_params(mlp.gate_proj)[1] is not None
-            has_up = hasattr(mlp, 'up_proj') and _get_lora_params(mlp.up_proj)[1] is not None
-            has_down = hasattr(mlp, 'down_proj') and _get_lora_params(mlp.down_proj)[1] is not None
-
-            if has_gate and has_up and has_down:
-                def _make_fused_mlp_forward(mlp_instance):
-                    def _fused_mlp_forward(self, x):
-                        return apply_fused_lora_mlp(self, x)
-                    return _fused_mlp_forward.__get__(mlp_instance, type(mlp_instance))
-
-                mlp.forward = _make_fused_mlp_forward(mlp)
-                mlp._metal_liger_fused_lora = True
-                patched += 1
-
-    logger.info(f"MetalLiger fused LoRA: activated on {patched} modules.")
-    return patched
+        for attr, names, make in (("self_attn", _QKV_PROJ, lambda m: _FusedAttentionForward(m, m.forward)),
+                                  ("mlp", _MLP_PROJ, _FusedMLPForward)):
+            mod = getattr(layer, attr, None)
+            if mod is None or getattr(mod, "_metal_liger_fused_lora", False):
+                continue
+            if not _all_lora(mod, names):
+                continue
+            mod.forward = make(mod)
+            mod._metal_liger_fused_lora = True
+            routed += 1
+    logger.info(f"MetalLiger fused LoRA: activated on {routed} modules.")
+    return routed

@@ -27,6 +27,7 @@ import torch
 import torch.nn as nn
 
 from metal_liger_amd import _custom_ops as cops
+from metal_liger_amd._model_walk import shadowed
 
 logger = logging.getLogger(__name__)
 
@@ -147,13 +148,10 @@ def _make_forward(attn: nn.Module, orig_fwd):
     def forward(hidden_states, *args, **kwargs):
         st = _Deferred(attn.q_norm, attn.k_norm)
         token = _ACTIVE.set(st)
-        attn.__dict__["q_norm"] = _identity
-        attn.__dict__["k_norm"] = _identity
         try:
-            out = orig_fwd(hidden_states, *args, **kwargs)
+            with shadowed(attn, q_norm=_identity, k_norm=_identity):
+                out = orig_fwd(hidden_states, *args, **kwargs)
         finally:
-            attn.__dict__.pop("q_norm", None)
-            attn.__dict__.pop("k_norm", None)
             _ACTIVE.reset(token)
         if not st.used:
             raise RuntimeError(

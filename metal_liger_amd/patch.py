@@ -14,6 +14,7 @@ import logging
 
 import torch.nn as nn
 
+from metal_liger_amd._model_walk import find_final_norm, find_layers
 from metal_liger_amd.ops.fused_add_rms_norm import patch_residual_add_norm
 from metal_liger_amd.ops.fused_linear_cross_entropy import patch_causal_lm_loss
 from metal_liger_amd.ops.fused_lora import patch_fused_lora
@@ -23,54 +24,11 @@ from metal_liger_amd.ops.fused_swiglu import MetalLigerSwiGLU
 
 logger = logging.getLogger(__name__)
 
-# Attribute paths to the decoder-layer list, most specific first
-# (patch.py:36-54 of the reference).
-_LAYER_PATHS = (
-    ("base_model", "model", "model", "language_model", "layers"),  # PEFT + Qwen3-VL
-    ("base_model", "model", "model", "layers"),                    # PEFT
-    ("model", "language_model", "layers"),                         # Qwen3-VL
-    ("model", "layers"),                                           # HF causal LM
-    ("layers",),                                                   # bare decoder
-    ("module", "model", "layers"),                                 # accelerate wrapper
-)
-
-# Attribute paths to the final norm's parent (patch.py:69-81).
-_NORM_PARENT_PATHS = (
-    ("base_model", "model", "model", "language_model"),
-    ("model", "language_model"),
-    ("base_model", "model", "model"),
-    ("model",),
-)
-
-
-def _resolve(obj, path):
-    for name in path:
-        obj = getattr(obj, name, None)
-        if obj is None:
-            return None
-    return obj
-
-
-def _find_layers(model: nn.Module):
-    """First non-empty decoder-layer list along _LAYER_PATHS, else None."""
-    for path in _LAYER_PATHS:
-        try:
-            layers = _resolve(model, path)
-            if layers is not None and len(layers) > 0:
-                return layers
-        except (AttributeError, TypeError):
-            continue
-    return None
-
-
-def _find_final_norm(model: nn.Module):
-    """(norm module, parent) of the final norm, or (None, None)."""
-    for path in _NORM_PARENT_PATHS:
-        parent = _resolve(model, path)
-        norm = getattr(parent, "norm", None) if parent is not None else None
-        if norm is not None and hasattr(norm, "weight"):
-            return norm, parent
-    return None, None
+# The decoder layers and the final norm are found along the wrapping layouts
+# the reference's patch.py:27-89 walks (bare HF, PEFT, Qwen3-VL's nested
+# language_model, accelerate); the path tables live in _model_walk.
+_find_layers = find_layers
+_find_final_norm = find_final_norm
 
 
 def _fused_norm_like(old: nn.Module) -> MetalLigerRMSNorm:
@@ -120,22 +78,28 @@ def apply_metal_liger_to_qwen3vl(
     fuse_lora: bool = True,
     use_optimized_generator: bool = False,
     fuse_residual_norm: bool = False,
+    fuse_qk_norm_rope: bool = False,
+    fuse_lm_loss: bool = False,
 ) -> nn.Module:
     """Apply the fused operations to a Qwen3 / Qwen3-VL model in place and
     return it (patch.py:181-240).
 
-    fuse_rope: attention modules with q_norm / k_norm (Qwen3) get their
-    head-dim norms and RoPE fused into one launch (ops/fused_qk_norm_rope.py;
-    the reference only logs here). Elsewhere RoPE is applied by the caller
-    with apply_fused_rotary / apply_fused_rotary_inline, as in the reference.
-    fuse_cross_entropy: the causal LM's training loss (forward with labels in
+    The reference's flags keep their meaning: fuse_rms_norm, fuse_swiglu
+    and fuse_lora patch the model; fuse_rope and fuse_cross_entropy only
+    record that the ops are available (RoPE is applied by the caller with
+    apply_fused_rotary / apply_fused_rotary_inline, the fused cross-entropy
+    through MetalLigerFusedLinearCrossEntropy in the training loop).
+
+    Fusions the reference does not have, off by default:
+    fuse_residual_norm: each decoder layer's post-attention residual add runs
+    in the same launch as its post_attention_layernorm
+    (ops/fused_add_rms_norm.py); needs fuse_rms_norm, whose norm it extends.
+    fuse_qk_norm_rope: attention modules with q_norm / k_norm (Qwen3) get
+    their head-dim norms and RoPE in one launch (ops/fused_qk_norm_rope.py).
+    fuse_lm_loss: the causal LM's training loss (forward with labels in
     training mode) comes from the fused linear cross-entropy with
-    transformers' label shift, without logits (the reference only logs here;
-    MetalLigerFusedLinearCrossEntropy can still be called directly).
-    fuse_residual_norm (not in the reference): each decoder layer's
-    post-attention residual add runs in the same launch as its
-    post_attention_layernorm (ops/fused_add_rms_norm.py); needs
-    fuse_rms_norm, whose norm it extends.
+    transformers' label shift, and the output's logits are None
+    (ops/fused_linear_cross_entropy.py, patch_causal_lm_loss).
     use_optimized_generator is not part of metal_liger_amd (inference path).
     """
     stats = {}
@@ -151,7 +115,7 @@ def apply_metal_liger_to_qwen3vl(
         n = patch_residual_add_norm(model)
         stats["residual_add_norm"] = n
         logger.info(f"MetalLiger: fused residual add + RMSNorm in {n} decoder layers")
-    if fuse_rope:
+    if fuse_qk_norm_rope:
         # before the LoRA patch, which wraps whatever attention forward it finds
         n = patch_qk_norm_rope(model)
         stats["qk_norm_rope"] = n
@@ -160,16 +124,21 @@ def apply_metal_liger_to_qwen3vl(
         n = patch_fused_lora(model)
         stats["fused_lora"] = n
         logger.info(f"MetalLiger: fused LoRA QKV+MLP marked {n} modules")
+    if fuse_lm_loss:
+        n = patch_causal_lm_loss(model)
+        stats["lm_loss"] = n
+        logger.info(f"MetalLiger: fused linear cross-entropy loss on {n} causal LM heads")
     if use_optimized_generator:
         logger.warning("MetalLiger: the optimized generator is not part of metal_liger_amd; skipped")
         stats["generator"] = "unavailable"
     if fuse_rope:
-        logger.info("MetalLiger: fused RoPE — use apply_fused_rotary() / apply_fused_rotary_inline()")
+        logger.info("MetalLiger: fused RoPE available — use apply_fused_rotary() / "
+                    "apply_fused_rotary_inline()")
         stats["rope"] = "available"
     if fuse_cross_entropy:
-        n = patch_causal_lm_loss(model)
-        stats["cross_entropy"] = n
-        logger.info(f"MetalLiger: fused linear cross-entropy loss on {n} causal LM heads")
+        logger.info("MetalLiger: fused CE available — use MetalLigerFusedLinearCrossEntropy in the "
+                    "training loop")
+        stats["cross_entropy"] = "available"
     total = sum(v for v in stats.values() if isinstance(v, int))
     logger.info(f"MetalLiger: {total} total layers patched. Details: {stats}")
     return model

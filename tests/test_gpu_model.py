@@ -33,11 +33,11 @@ def train_step(model, ids):
     return out.loss.detach().float(), lora_grads(model)
 
 
-@pytest.mark.parametrize("fuse_rope,fuse_ce,fuse_res", [(False, False, False), (True, False, False),
-                                                         (False, False, True), (True, True, True)])
-def test_patched_qwen3_lora_train_step(dev, fuse_rope, fuse_ce, fuse_res):
-    """fuse_rope=True also routes q_norm / k_norm + RoPE through the fused
-    kernel; fuse_cross_entropy=True computes the model's training loss (from
+@pytest.mark.parametrize("fuse_qkn,fuse_ce,fuse_res", [(False, False, False), (True, False, False),
+                                                        (False, False, True), (True, True, True)])
+def test_patched_qwen3_lora_train_step(dev, fuse_qkn, fuse_ce, fuse_res):
+    """fuse_qk_norm_rope=True routes q_norm / k_norm + RoPE through the fused
+    kernel; fuse_lm_loss=True computes the model's training loss (from
     labels) with the fused linear cross-entropy instead of logits;
     fuse_residual_norm=True fuses each layer's post-attention residual add
     into its norm."""
@@ -47,11 +47,11 @@ def test_patched_qwen3_lora_train_step(dev, fuse_rope, fuse_ce, fuse_res):
     for n, p in base.named_parameters():
         p.requires_grad_("lora_" in n)
     exact = copy.deepcopy(base).float()
-    patched = apply_metal_liger_to_qwen3vl(copy.deepcopy(base), fuse_rope=fuse_rope,
-                                           fuse_cross_entropy=fuse_ce, fuse_residual_norm=fuse_res)
+    patched = apply_metal_liger_to_qwen3vl(copy.deepcopy(base), fuse_qk_norm_rope=fuse_qkn,
+                                           fuse_lm_loss=fuse_ce, fuse_residual_norm=fuse_res)
     lm = patched.base_model.model
     qkn = [getattr(l.self_attn, "_metal_liger_qk_norm_rope", False) for l in lm.model.layers]
-    assert qkn == [fuse_rope] * 2
+    assert qkn == [fuse_qkn] * 2
     assert getattr(lm, "_metal_liger_flce_loss", False) == fuse_ce
     assert [getattr(l, "_metal_liger_add_norm", False) for l in lm.model.layers] == [fuse_res] * 2
     g = torch.Generator().manual_seed(7)
@@ -101,8 +101,8 @@ def test_patched_qwen3_vl_train_step(dev):
     attn = qwen_tiny.register_fp32_attention()
     base = qwen_tiny.build_vl(seed=9, attn=attn, dtype=torch.bfloat16).to(dev)
     exact = copy.deepcopy(base).float()
-    patched = apply_metal_liger_to_qwen3vl(copy.deepcopy(base), fuse_rope=True,
-                                           fuse_cross_entropy=True, fuse_residual_norm=True)
+    patched = apply_metal_liger_to_qwen3vl(copy.deepcopy(base), fuse_qk_norm_rope=True,
+                                           fuse_lm_loss=True, fuse_residual_norm=True)
     layers = patched.model.language_model.layers
     assert all(getattr(l.self_attn, "_metal_liger_qk_norm_rope", False) for l in layers)
     assert all(getattr(l, "_metal_liger_add_norm", False) for l in layers)

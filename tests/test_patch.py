@@ -34,9 +34,16 @@ def test_patch_bare_model_and_flags():
     from metal_liger_amd import apply_metal_liger_to_qwen3vl
     from metal_liger_amd.ops.fused_lora import patch_fused_lora
     lm = qwen_tiny.build(lora=False, peft_wrap=False)
+    keys = list(lm.state_dict())
     apply_metal_liger_to_qwen3vl(lm, fuse_swiglu=False, fuse_lora=True, fuse_rope=True,
                                  fuse_cross_entropy=True)
     assert type(lm.model.layers[0].mlp).__name__ == "Qwen3MLP"      # swiglu not fused
+    # fuse_rope / fuse_cross_entropy only log, as in the reference (patch.py:226-232)
+    attn = lm.model.layers[0].self_attn
+    assert not getattr(attn, "_metal_liger_qk_norm_rope", False)
+    assert not getattr(lm, "_metal_liger_flce_loss", False)
+    assert "forward" not in lm.__dict__ and "forward" not in attn.__dict__
+    assert list(lm.state_dict()) == keys
     assert patch_fused_lora(lm) == 0                                 # no LoRA adapters
     assert patch_fused_lora(torch.nn.Linear(4, 4)) == 0              # no layers at all
 
@@ -49,9 +56,53 @@ def test_patch_lora_routing_without_replacement():
     W, A, B, s = _get_lora_params(q)
     assert W is q.base_layer.weight and A.shape == (16, 128) and B.shape == (128, 16) and s == 2.0
     assert _get_lora_params(torch.nn.Linear(3, 3)) == (None, None, None, None)
+    keys = list(model.state_dict())
     n = patch_fused_lora(model)
     assert n == 4
+    assert patch_fused_lora(model) == 0                              # already routed
     assert lm.model.layers[0].self_attn.q_proj is q                  # module not replaced
+    assert list(model.state_dict()) == keys
+
+
+class _Block(torch.nn.Module):
+    def __init__(self):
+        super().__init__()
+        self.self_attn = torch.nn.Module()
+        self.mlp = torch.nn.Module()
+
+
+def test_layer_search_paths_and_fallback():
+    """The decoder layers are found along the wrapping layouts (bare decoder,
+    causal LM, PEFT, Qwen3-VL) and, for any other wrapper, as the first
+    non-empty ModuleList named ``layers``."""
+    from metal_liger_amd._model_walk import find_layers
+    model = qwen_tiny.build()
+    assert find_layers(model) is model.base_model.model.model.layers
+    assert find_layers(model.base_model.model) is model.base_model.model.model.layers
+    assert find_layers(model.base_model.model.model) is model.base_model.model.model.layers
+    outer = torch.nn.Module()
+    outer.wrapped = torch.nn.Module()
+    outer.wrapped.inner = torch.nn.Module()
+    outer.wrapped.inner.layers = torch.nn.ModuleList([_Block(), _Block()])
+    assert find_layers(outer) is outer.wrapped.inner.layers
+    outer.wrapped.inner.layers = torch.nn.ModuleList()
+    assert find_layers(outer) is None
+
+
+def test_shadowed_restores_instance_dict():
+    """shadowed() hides submodules for the duration of a block only, and puts
+    back an instance attribute that was there before, also on an error."""
+    from metal_liger_amd._model_walk import shadowed
+    m = torch.nn.Module()
+    m.proj = torch.nn.Linear(2, 2)
+    m.__dict__["tag"] = "old"
+    with shadowed(m, proj="p", tag="new"):
+        assert m.proj == "p" and m.tag == "new"
+    assert isinstance(m.proj, torch.nn.Linear) and m.tag == "old"
+    with pytest.raises(KeyError):
+        with shadowed(m, proj="p"):
+            raise KeyError("x")
+    assert isinstance(m.proj, torch.nn.Linear) and "proj" not in m.__dict__
 
 
 def test_fused_ops_refuse_cpu_tensors():
@@ -110,7 +161,7 @@ class _NoRotaryAttention(torch.nn.Module):
 
 
 def test_qk_norm_rope_patch_defers_norms_to_the_rotary_step(monkeypatch):
-    """fuse_rope routes Qwen3 attention's q_norm / k_norm into the rotary step
+    """fuse_qk_norm_rope routes Qwen3 attention's q_norm / k_norm into the rotary step
     of the same forward. With the fused op swapped for the oracle on the CPU,
     the patched model's logits equal the unpatched model's bit for bit, an
     unpatched instance in the same process keeps transformers' own rotary,
@@ -189,6 +240,33 @@ class _ExtraAddLayer(torch.nn.Module):
         return residual + h
 
 
+class _TupleReturnLayer(_ExtraAddLayer):
+    """transformers' older decoder-layer form: returns an outputs tuple and
+    appends to it with +=."""
+
+    def forward(self, hidden_states, output_attentions=False):
+        residual = hidden_states
+        h = self.self_attn(self.input_layernorm(hidden_states))
+        h = residual + h
+        residual = h
+        h = self.mlp(self.post_attention_layernorm(h))
+        h = residual + h
+        outputs = (h,)
+        if output_attentions:
+            outputs += (None,)
+        return outputs
+
+
+class _BareTupleLayer(_ExtraAddLayer):
+    def forward(self, hidden_states):
+        residual = hidden_states
+        h = self.self_attn(self.input_layernorm(hidden_states))
+        h = residual + h
+        residual = h
+        h = self.mlp(self.post_attention_layernorm(h))
+        return (residual + h,)
+
+
 def test_residual_add_norm_patch_matches_unfused(monkeypatch):
     """fuse_residual_norm swaps each Qwen3 decoder layer's forward for one
     that fuses the post-attention add into post_attention_layernorm. With the
@@ -228,8 +306,12 @@ def test_residual_add_norm_patch_matches_unfused(monkeypatch):
         assert torch.equal(outs[1][1][n], g), n
 
     assert fa.patch_residual_add_norm(_ExtraAddLayer()) == 0
+    assert fa.patch_residual_add_norm(_TupleReturnLayer()) == 0      # returns a tuple
+    assert fa.patch_residual_add_norm(_BareTupleLayer()) == 0
+    from transformers.models.qwen3.modeling_qwen3 import Qwen3DecoderLayer
     from transformers.models.qwen3_vl.modeling_qwen3_vl import Qwen3VLTextDecoderLayer
-    assert fa._structure(Qwen3VLTextDecoderLayer.forward) == (fa._LAYER_PARTS, 2)
+    for cls in (Qwen3DecoderLayer, Qwen3VLTextDecoderLayer):
+        assert fa._structure(cls.forward) == (fa._LAYER_PARTS, 2, True)
 
 
 class _OracleFLCE:
@@ -247,7 +329,7 @@ class _OracleFLCE:
 
 
 def test_causal_lm_loss_hook_matches_transformers(monkeypatch):
-    """fuse_cross_entropy routes a causal LM's training loss through the fused
+    """fuse_lm_loss routes a causal LM's training loss through the fused
     op with transformers' label shift; the logits are not returned; with
     num_items_in_batch the sum is divided by it; eval mode is unchanged."""
     import copy
@@ -320,8 +402,8 @@ def test_qwen3_vl_text_stack_patched(monkeypatch):
 
     base = qwen_tiny.build_vl(seed=8)
     keys = list(base.state_dict())
-    patched = apply_metal_liger_to_qwen3vl(copy.deepcopy(base), fuse_rope=True,
-                                           fuse_cross_entropy=True, fuse_residual_norm=True)
+    patched = apply_metal_liger_to_qwen3vl(copy.deepcopy(base), fuse_qk_norm_rope=True,
+                                           fuse_lm_loss=True, fuse_residual_norm=True)
     lm = patched.model.language_model
     assert sum(isinstance(m, MetalLigerRMSNorm) for m in patched.modules()) == 2 * 2 + 1
     assert all(isinstance(layer.mlp, MetalLigerSwiGLU) for layer in lm.layers)
