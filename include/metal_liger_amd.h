@@ -87,6 +87,22 @@ int ml_rmsnorm_bwd(const void* x, int64_t ldx, const void* w, const void* dy, in
                    int x_dtype, int w_dtype, void* stream);
 
 /*
+ * ml_rmsnorm_bwd without a workspace argument: no counterpart in the
+ * reference. For callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc). The
+ * dW partials live in the library's own 8 MiB device array, one per GPU,
+ * held until the process ends; min(rows, 256) * cols * 4 must not exceed
+ * it (cols <= 8192 once rows >= 256), else the call fails with an error
+ * and launches nothing. Calls allocate nothing.
+ * Calls that overlap on one GPU share the array and race; the stream must
+ * belong to the current device.
+ */
+int ml_rmsnorm_bwd_noalloc(const void* x, int64_t ldx, const void* w, const void* dy,
+                           int64_t lddy, const float* rrms, float eps, void* dx, int64_t lddx,
+                           void* dw, int64_t rows, int64_t cols, int x_dtype, int w_dtype,
+                           void* stream);
+
+/*
  * Residual add fused into the norm after it: the decoder layer's
  * `hidden = residual + attn_out; post_attention_layernorm(hidden)`
  * (transformers modeling_qwen3.py, Qwen3DecoderLayer.forward; the step that

@@ -39,6 +39,9 @@ SIGNATURES: dict[str, tuple] = {
         _i32,
         [_p, _i64, _p, _p, _i64, _p, _f32, _p, _i64, _p, _p, _sz, _i64, _i64, _i32, _i32, _p],
     ),
+    "ml_rmsnorm_bwd_noalloc": (
+        _i32, [_p, _i64, _p, _p, _i64, _p, _f32, _p, _i64, _p, _i64, _i64, _i32, _i32, _p],
+    ),
     "ml_rmsnorm_add_fwd": (
         _i32, [_p, _i64, _p, _i64, _p, _p, _i64, _p, _i64, _p, _i64, _i64, _f32, _i32, _i32, _p],
     ),

@@ -22,6 +22,8 @@
 //    (backward).
 #include <initializer_list>
 
+#include <mutex>
+
 #include "common.h"
 
 // Evaluate every product and sum exactly as written (one rounding each), as
@@ -611,6 +613,73 @@ extern "C" int ml_rmsnorm_bwd(const void* x, int64_t ldx, const void* w, const v
                               int64_t cols, int x_dtype, int w_dtype, void* stream) {
   return rmsnorm_bwd_checked(x, ldx, w, dy, lddy, nullptr, 0, rrms, eps, dx, lddx, dw, workspace,
                              workspace_bytes, rows, cols, x_dtype, w_dtype, stream);
+}
+
+// ------------------------------------------------ allocation-free backward --
+// ml_rmsnorm_bwd_noalloc keeps the dW partial rows (min(rows, 256) x cols
+// fp32) in this file-scope device array instead of a caller workspace. Each
+// GPU holds its own copy for the life of the process. The array's name is a
+// host-side stand-in: host code uses only the per-device address that
+// hipGetSymbolAddress returns (looked up once per device, on the first call
+// made with that device current). Every backward block writes its whole
+// partial row before the reduction reads it, so the array needs no clearing;
+// calls that overlap on one GPU share it and race.
+namespace {
+constexpr size_t kNoAllocScratchBytes = size_t(8) << 20;
+constexpr int kScratchDevices = 64;
+void* g_scratch[kScratchDevices] = {};
+hipError_t g_scratch_status[kScratchDevices] = {};
+std::once_flag g_scratch_once[kScratchDevices];
+}  // namespace
+
+static __device__ __align__(256) char scratch[kNoAllocScratchBytes];
+
+// The current device's address of `scratch`; the stream must belong to
+// that device.
+static int scratch_address(hipStream_t st, void** out) {
+  int dev = 0;
+  ML_HIP_CHECK(hipGetDevice(&dev));
+  ML_CHECK(dev >= 0 && dev < kScratchDevices, "rmsnorm backward (no-alloc): device %d out of range",
+           dev);
+  if (st != nullptr) {
+    hipDevice_t sdev = 0;
+    ML_HIP_CHECK(hipStreamGetDevice(st, &sdev));
+    ML_CHECK(sdev == dev,
+             "rmsnorm backward (no-alloc): the stream belongs to device %d, the current device is %d",
+             (int)sdev, dev);
+  }
+  std::call_once(g_scratch_once[dev], [dev]() {
+    void* p = nullptr;
+    g_scratch_status[dev] = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    g_scratch[dev] = p;
+  });
+  if (g_scratch_status[dev] != hipSuccess || g_scratch[dev] == nullptr) {
+    set_error("rmsnorm backward (no-alloc): hipGetSymbolAddress failed on device %d: %s", dev,
+              hipGetErrorString(g_scratch_status[dev]));
+    return ML_ERR_HIP;
+  }
+  *out = g_scratch[dev];
+  return ML_OK;
+}
+
+extern "C" int ml_rmsnorm_bwd_noalloc(const void* x, int64_t ldx, const void* w, const void* dy,
+                                      int64_t lddy, const float* rrms, float eps, void* dx,
+                                      int64_t lddx, void* dw, int64_t rows, int64_t cols,
+                                      int x_dtype, int w_dtype, void* stream) {
+  ML_CHECK(rows >= 0 && cols > 0, "rmsnorm backward: bad shape rows=%lld cols=%lld",
+           (long long)rows, (long long)cols);
+  const size_t need = ml_rmsnorm_bwd_workspace_bytes(rows, cols);
+  ML_CHECK(need <= kNoAllocScratchBytes,
+           "rmsnorm backward (no-alloc): min(rows, 256) x cols x 4 = %zu bytes of dW partials "
+           "exceed its %zu-byte scratch (cols <= %zu at 256 or more rows)",
+           need, kNoAllocScratchBytes, kNoAllocScratchBytes / (256 * sizeof(float)));
+  void* ws = nullptr;
+  if (need > 0) {
+    const int rc = scratch_address((hipStream_t)stream, &ws);
+    if (rc != ML_OK) return rc;
+  }
+  return rmsnorm_bwd_checked(x, ldx, w, dy, lddy, nullptr, 0, rrms, eps, dx, lddx, dw, ws,
+                             kNoAllocScratchBytes, rows, cols, x_dtype, w_dtype, stream);
 }
 
 extern "C" int ml_rmsnorm_add_bwd(const void* sum, int64_t lds, const void* w, const void* dy,
