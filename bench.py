@@ -11,19 +11,23 @@ count each input read once and each output written once:
   SwiGLU fwd 3*N*I*2 + bwd 5*N*I*2 = 805,306,368 B
   RoPE   fwd (read + write q, k) + bwd (same) = 201,326,592 B
 roofline: the dominant kernel (SwiGLU backward, 503,316,480 B per launch),
-its average launch duration from HIP events on its stream around 20
-back-to-back launches, against 8 TB/s.
+its launch duration measured cold (MALL and L2 flushed by a 512 MB write
+before each of 25 reps, median, HIP events on its stream), against 8 TB/s.
 cpu_baseline: the oracle (a CPU restatement of the reference's torch ops)
-on a bounded sample of the same workload, on the host's cores.
-breakdown: each op's average launch time; plus, outside the step, chunked
-FLCE fwd+bwd (hidden [8192, 2048], lm_head [151936, 2048], chunk 8192:
-15.29 TFLOP) and the fused LoRA backward of a Qwen3-style 2B layer (QKV +
-MLP, rank 16: 774.2 GFLOP), as TFLOP/s against the 2.5 PFLOP/s bf16 peak;
-and the 4-layer Qwen3-style LoRA train step (batch 4 x 2048 tokens, every
-fused op patched in, FLCE loss, AdamW on the adapters) in tokens/s.
+on a bounded sample of the same workload, on the host's cores;
+cpu_baselines: the same per config (RMSNorm, SwiGLU, RoPE, LoRA backward,
+FLCE, train step) on bounded samples; --cpu-full runs them at full shape.
+breakdown: each op's cold median (and warm back-to-back) launch time; plus,
+outside the step, RMSNorm fp32, the residual add + RMSNorm and the q/k norm
++ RoPE (all cold); chunked FLCE fwd+bwd (hidden [8192, 2048], lm_head
+[151936, 2048], chunk 8192: 15.29 TFLOP, with its peak extra memory) and
+the fused LoRA backward of a Qwen3-style 2B layer (QKV + MLP, rank 16:
+774.2 GFLOP), as TFLOP/s against the 2.5 PFLOP/s bf16 peak (medians of 20
+reps); and the 4-layer Qwen3-style LoRA train step (batch 4 x 2048 tokens,
+every fused op patched in, FLCE loss, AdamW on the adapters) in tokens/s.
 
-Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline] [--no-mfma-ops] [--no-train-step]
-       [--train-step-only] [--pmc-probe] [--pmc-mfma-probe]
+Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline] [--no-mfma-ops]
+       [--no-train-step] [--train-step-only] [--cpu-full] [--pmc-probe] [--pmc-mfma-probe]
 """
 
 from __future__ import annotations
@@ -74,7 +78,8 @@ def gpu_randn(shape, seed, dev, scale=1.0, dtype=None):
 
 def time_launches(fn, stream, reps):
     """Average milliseconds per call over `reps` back-to-back calls (events on
-    the stream the kernels are launched on)."""
+    the stream the kernels are launched on): the warm rate, operands partly
+    resident in the MALL / L2 when they fit there."""
     import torch
     fn()
     a = torch.cuda.Event(enable_timing=True)
@@ -87,36 +92,124 @@ def time_launches(fn, stream, reps):
     return a.elapsed_time(b) / reps
 
 
-def time_graph(fn, stream, reps):
-    """Average milliseconds per call of fn replayed from one captured HIP
-    graph of `reps` calls: the launches' own GPU time, without the host-side
-    argument marshalling of each call. Falls back to time_launches (and says
-    so) when the capture fails."""
-    import torch
-    try:
-        side = torch.cuda.Stream()
-        side.wait_stream(stream)
-        with torch.cuda.stream(side):
+FLUSH_BYTES = 512 << 20   # twice the 256 MB MALL, far beyond the 8 x 4 MB L2
+
+
+class ColdTimer:
+    """Launch time with the MALL and L2 flushed before every rep: each rep
+    writes a 512 MB buffer and reads another, then runs fn; the same flush is timed alone in
+    interleaved reps. time(fn) = median over reps of (flush + fn) minus the
+    median of (flush alone), from events on the launch stream; no event sits
+    between the flush and fn, so the inter-event gap of an event record does
+    not land on fn, and fn's host-side launch is enqueued while the flush
+    still runs."""
+
+    def __init__(self, dev, stream):
+        import torch
+        self.stream = stream
+        self.buf = torch.empty(FLUSH_BYTES // 4, dtype=torch.float32, device=dev)
+        self.rbuf = torch.ones(FLUSH_BYTES // 4, dtype=torch.float32, device=dev)
+        self.sink = torch.empty((), dtype=torch.float32, device=dev)
+
+    def flush(self):
+        import torch
+        # the write evicts the op's data; the read of another 512 MB then
+        # replaces the write's dirty lines with clean ones, so their
+        # write-back happens inside the flush (timed and subtracted)
+        self.buf.fill_(1.0)
+        torch.sum(self.rbuf, dim=(0,), out=self.sink)
+
+    def time(self, fn, reps=25):
+        import statistics
+
+        import torch
+        fn()
+        self.flush()
+        torch.cuda.synchronize()
+        E = torch.cuda.Event
+        pairs = [[(E(enable_timing=True), E(enable_timing=True)) for _ in range(2)] for _ in range(reps)]
+        for (fa, fb), (ta, tb) in pairs:
+            fa.record(self.stream)
+            self.flush()
+            fb.record(self.stream)
+            ta.record(self.stream)
+            self.flush()
             fn()
-        stream.wait_stream(side)
+            tb.record(self.stream)
         torch.cuda.synchronize()
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
-            for _ in range(reps):
+        fl = [fa.elapsed_time(fb) for (fa, fb), _ in pairs]
+        tot = [ta.elapsed_time(tb) for _, (ta, tb) in pairs]
+        ops = sorted(t - f for t, f in zip(tot, fl))
+        med = statistics.median(tot) - statistics.median(fl)
+        return {"ms": med, "p10_ms": ops[len(ops) // 10], "p90_ms": ops[(9 * len(ops)) // 10],
+                "reps": reps}
+
+
+def time_rotating(fns, stream, rounds=6):
+    """Average ms per launch over back-to-back launches that cycle through
+    `fns` (the same op bound to different copies of its inputs, enough
+    copies that their working set exceeds the 256 MB MALL, so every launch
+    reads its operands from HBM), replayed from one captured HIP graph of
+    rounds x len(fns) launches (no per-call host marshalling in the timed
+    interval; same-stream kernels still run one after another)."""
+    import torch
+    n = rounds * len(fns)
+    side = torch.cuda.Stream()
+    side.wait_stream(stream)
+    with torch.cuda.stream(side):
+        for fn in fns:
+            fn()
+    stream.wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(rounds):
+            for fn in fns:
                 fn()
-        g.replay()
-        torch.cuda.synchronize()
-        a = torch.cuda.Event(enable_timing=True)
-        b = torch.cuda.Event(enable_timing=True)
+    g.replay()
+    torch.cuda.synchronize()
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
+    times = []
+    for _ in range(3):
         a.record(stream)
         g.replay()
         b.record(stream)
         torch.cuda.synchronize()
-        ms = a.elapsed_time(b) / reps
-        del g
-        return ms, "graph replay"
-    except RuntimeError:
-        return time_launches(fn, stream, reps), "eager launches (graph capture failed)"
+        times.append(a.elapsed_time(b) / n)
+    del g
+    return min(times)
+
+
+def rotating_copies(nbytes_per_launch):
+    """Input copies needed so one round of launches touches > 512 MB."""
+    return max(2, -(-(FLUSH_BYTES) // max(nbytes_per_launch, 1)))
+
+
+def cold_line(res, nbytes=None, flop=None, rot_ms=None):
+    """Fields of one cold-timed op: the rotating-input launch time (us,
+    GB/s, hbm_frac: what the kernel sustains from HBM) when given, and the
+    flushed single-launch median (flushed_us, with p10/p90 and GB/s, which
+    also holds the launch's dispatch gap)."""
+    out = {}
+    if rot_ms is not None and nbytes:
+        out["us"] = round(rot_ms * 1e3, 2)
+        out["GB/s"] = round(nbytes / (rot_ms * 1e-3) / 1e9, 1)
+        out["hbm_frac"] = round(nbytes / (rot_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
+    out.update({"flushed_us": round(res["ms"] * 1e3, 2), "flushed_p10_us": round(res["p10_ms"] * 1e3, 2),
+                "flushed_p90_us": round(res["p90_ms"] * 1e3, 2)})
+    if nbytes:
+        out["flushed_GB/s"] = round(nbytes / (res["ms"] * 1e-3) / 1e9, 1)
+    if flop:
+        out["TFLOP/s"] = round(flop / (res["ms"] * 1e-3) / 1e12, 1)
+    return out
+
+
+TIMING_NOTE = ("us / GB/s / hbm_frac: back-to-back launches cycling through copies of the inputs "
+               "whose working set exceeds the 256 MB MALL (every launch reads HBM), replayed from a "
+               "captured graph; flushed_*: MALL/L2 flushed before each rep by a 512 MB write then "
+               "a 512 MB read (caches clean, none of the op's data), median of 25 reps of "
+               "(flush + op) minus the median of (flush alone), dispatch gap included")
 
 
 RMS_N, RMS_H = 8192, 2048
@@ -124,20 +217,29 @@ RMS_FWD_BYTES = 2 * RMS_N * RMS_H * 4 + RMS_H * 4 + RMS_N * 4          # x, w in
 RMS_BWD_BYTES = 3 * RMS_N * RMS_H * 4 + 2 * RMS_H * 4 + RMS_N * 4      # x, dy, w, rrms in; dx, dw out
 
 
-def bench_rmsnorm(dev, stream, reps):
+def bench_rmsnorm(dev, timer):
     """RMSNorm fwd and bwd, fp32 x [8192, 2048], weight 1 + 0.1 N(0, 1),
     eps 1e-6 (rrms saved by the forward, as the autograd Function does)."""
-    import torch
-
     from metal_liger_amd import hip_ops
+    import torch
     x = gpu_randn((RMS_N, RMS_H), 40, dev, dtype=torch.float32)
     w = (1.0 + 0.1 * gpu_randn((RMS_H,), 41, dev, dtype=torch.float32))
     dy = gpu_randn((RMS_N, RMS_H), 42, dev, dtype=torch.float32)
     _, rrms = hip_ops.rms_norm_fwd(x, w, 1e-6)
-    f_ms = time_launches(lambda: hip_ops.rms_norm_fwd(x, w, 1e-6), stream, reps)
-    b_ms = time_launches(lambda: hip_ops.rms_norm_bwd(x, w, dy, rrms, 1e-6), stream, reps)
-    return {"fwd_us": round(f_ms * 1e3, 2), "fwd_GB/s": round(RMS_FWD_BYTES / (f_ms * 1e-3) / 1e9, 1),
-            "bwd_us": round(b_ms * 1e3, 2), "bwd_GB/s": round(RMS_BWD_BYTES / (b_ms * 1e-3) / 1e9, 1)}
+    f = timer.time(lambda: hip_ops.rms_norm_fwd(x, w, 1e-6))
+    b = timer.time(lambda: hip_ops.rms_norm_bwd(x, w, dy, rrms, 1e-6))
+    C = rotating_copies(RMS_FWD_BYTES)
+    cp = [(x.clone(), dy.clone(), rrms.clone()) for _ in range(C)]
+    rf = time_rotating([lambda t=t: hip_ops.rms_norm_fwd(t[0], w, 1e-6) for t in cp], timer.stream)
+    rb = time_rotating([lambda t=t: hip_ops.rms_norm_bwd(t[0], w, t[1], t[2], 1e-6) for t in cp],
+                       timer.stream)
+    del cp
+    tot = rf + rb
+    return {"fwd": cold_line(f, RMS_FWD_BYTES, rot_ms=rf), "bwd": cold_line(b, RMS_BWD_BYTES, rot_ms=rb),
+            "fwd_bwd_GB/s": round((RMS_FWD_BYTES + RMS_BWD_BYTES) / (tot * 1e-3) / 1e9, 1),
+            "fwd_bwd_hbm_frac": round((RMS_FWD_BYTES + RMS_BWD_BYTES) / (tot * 1e-3) / 1e9
+                                      / HBM_PEAK_GBS, 4),
+            "bwd_note": "includes the fixed-order dW partial-row reduction launch"}
 
 
 ADD_N, ADD_H = 8192, 2048
@@ -145,7 +247,7 @@ ADD_FWD_BYTES = 4 * ADD_N * ADD_H * 2 + ADD_H * 2 + ADD_N * 4      # x, res, w i
 ADD_BWD_BYTES = 4 * ADD_N * ADD_H * 2 + 2 * ADD_H * 2 + ADD_N * 4  # sum, dy, dsum, w, rrms in; dx, dw out
 
 
-def bench_add_rmsnorm(dev, stream, reps):
+def bench_add_rmsnorm(dev, timer):
     """Residual add fused into RMSNorm (a decoder layer's post-attention
     step), bf16 hidden states [8192, 2048], bf16 weight 1 + 0.1 N(0, 1),
     eps 1e-6; beside it the unfused pair (torch's add, then the fused norm;
@@ -157,22 +259,41 @@ def bench_add_rmsnorm(dev, stream, reps):
     dy = gpu_randn((ADD_N, ADD_H), 48, dev)
     ds = gpu_randn((ADD_N, ADD_H), 49, dev)
     _, total, rrms = hip_ops.rms_norm_add_fwd(x, res, w, 1e-6)
-    f_ms, how = time_graph(lambda: hip_ops.rms_norm_add_fwd(x, res, w, 1e-6), stream, reps)
-    b_ms, _ = time_graph(lambda: hip_ops.rms_norm_bwd(total, w, dy, rrms, 1e-6, dsum=ds), stream, reps)
-    uf_ms, _ = time_graph(lambda: hip_ops.rms_norm_fwd(x + res, w, 1e-6), stream, reps)
-    ub_ms, _ = time_graph(lambda: hip_ops.rms_norm_bwd(total, w, dy, rrms, 1e-6)[0] + ds, stream, reps)
-    return {"fwd_us": round(f_ms * 1e3, 2), "fwd_GB/s": round(ADD_FWD_BYTES / (f_ms * 1e-3) / 1e9, 1),
-            "bwd_us": round(b_ms * 1e3, 2), "bwd_GB/s": round(ADD_BWD_BYTES / (b_ms * 1e-3) / 1e9, 1),
-            "unfused_fwd_us": round(uf_ms * 1e3, 2), "unfused_bwd_us": round(ub_ms * 1e3, 2),
-            "timing": how}
+    f = timer.time(lambda: hip_ops.rms_norm_add_fwd(x, res, w, 1e-6))
+    b = timer.time(lambda: hip_ops.rms_norm_bwd(total, w, dy, rrms, 1e-6, dsum=ds))
+    C = rotating_copies(ADD_FWD_BYTES)
+    cp = [(x.clone(), res.clone(), total.clone(), dy.clone(), ds.clone(), rrms.clone())
+          for _ in range(C)]
+    rf = time_rotating([lambda t=t: hip_ops.rms_norm_add_fwd(t[0], t[1], w, 1e-6) for t in cp],
+                       timer.stream)
+    rb = time_rotating([lambda t=t: hip_ops.rms_norm_bwd(t[2], w, t[3], t[5], 1e-6, dsum=t[4])
+                        for t in cp], timer.stream)
+    ruf = time_rotating([lambda t=t: hip_ops.rms_norm_fwd(t[0] + t[1], w, 1e-6) for t in cp],
+                        timer.stream)
+    rub = time_rotating([lambda t=t: hip_ops.rms_norm_bwd(t[2], w, t[3], t[5], 1e-6)[0] + t[4]
+                         for t in cp], timer.stream)
+    del cp
+    return {"fwd": cold_line(f, ADD_FWD_BYTES, rot_ms=rf), "bwd": cold_line(b, ADD_BWD_BYTES, rot_ms=rb),
+            "unfused_fwd_us": round(ruf * 1e3, 2), "unfused_bwd_us": round(rub * 1e3, 2)}
 
 
-def bench_flce(dev, stream, reps, token_chunk=None):
+def flce_reference_peak_bytes(N, V, H, chunk):
+    """Peak extra device memory of the reference's Function in its backward
+    (ops/fused_linear_cross_entropy.py:159-185): fp32 copies of hidden and
+    weight, fp32 grad_hidden and grad_weight, about three live fp32 [N, chunk]
+    temporaries (logit_chunk, prob_chunk, the masked product) and the final
+    bf16 cast of grad_weight while its fp32 buffer is alive."""
+    return 2 * N * H * 4 + 2 * V * H * 4 + 3 * N * chunk * 4 + V * H * 2
+
+
+def bench_flce(dev, timer, reps=20, token_chunk=None):
     """Fused linear cross-entropy fwd + bwd as the autograd Function runs it:
     hidden [8192, 2048], lm_head [151936, 2048] ~N(0, 0.02), no bias, 10% of
     labels ignored; the forward forms loss, dH and dW in one pass (logits
     computed once), the backward applies grad_output. 15.29 TFLOP of
-    necessary GEMM work (logits, dH, dW) per fwd+bwd."""
+    necessary GEMM work (logits, dH, dW) per fwd+bwd. Peak extra memory: the
+    allocator's peak above the inputs during one fwd + bwd (workspace plus
+    the dH / dW outputs)."""
     import torch
 
     from metal_liger_amd import hip_ops
@@ -191,15 +312,32 @@ def bench_flce(dev, stream, reps, token_chunk=None):
         _, _, _, dh, dw = state["f"]
         hip_ops.flce_scale_grads(one, dh, dw)
 
-    f_ms = time_launches(fwd, stream, reps)
-    b_ms = time_launches(bwd, stream, reps)
-    tot = f_ms + b_ms
+    fwd()
+    torch.cuda.synchronize()
+    state.clear()
+    torch.cuda.empty_cache()
+    base = torch.cuda.memory_allocated()
+    torch.cuda.reset_peak_memory_stats()
+    fwd()
+    bwd()
+    torch.cuda.synchronize()
+    peak_extra = torch.cuda.max_memory_allocated() - base
+    f = timer.time(fwd, reps)
+    b = timer.time(bwd, reps)
+    tot = f["ms"] + b["ms"]
     tf = FLCE_FLOP / (tot * 1e-3) / 1e12
     T = token_chunk or hip_ops.flce_token_chunk(FLCE_N, FLCE_V)
+    ws = hip_ops._hip.query("ml_flce_fwd_grad_workspace_bytes", FLCE_N, FLCE_V, FLCE_H, T, 1)
     del h, w, lab, state
     torch.cuda.empty_cache()
-    return {"fwd_ms": round(f_ms, 3), "bwd_ms": round(b_ms, 3), "TFLOP/s": round(tf, 1),
-            "mfma_frac": round(tf / MFMA_PEAK_TFLOPS, 4), "flop": FLCE_FLOP, "token_chunk": T}
+    return {"fwd_ms": round(f["ms"], 3), "bwd_ms": round(b["ms"], 3), "TFLOP/s": round(tf, 1),
+            "mfma_frac": round(tf / MFMA_PEAK_TFLOPS, 4), "flop": FLCE_FLOP, "token_chunk": T,
+            "peak_extra_bytes": int(peak_extra), "workspace_bytes": int(ws),
+            "grad_output_bytes": (FLCE_N + FLCE_V) * FLCE_H * 2,
+            "full_logits_bf16_bytes": FLCE_N * FLCE_V * 2,
+            "reference_model_peak_extra_bytes": flce_reference_peak_bytes(FLCE_N, FLCE_V, FLCE_H,
+                                                                          FLCE_CHUNK),
+            "reps": reps, "timing": "median of reps (flush before each)"}
 
 
 QKN_DIR_TABLE_BYTES = 2 * RB * RS * RD * 2                  # cos + sin [B, S, D] bf16
@@ -207,7 +345,7 @@ QKN_FWD_BYTES = 2 * RB * (RHQ + RHK) * RS * RD * 2 + QKN_DIR_TABLE_BYTES    # x 
 QKN_BWD_BYTES = 3 * RB * (RHQ + RHK) * RS * RD * 2 + QKN_DIR_TABLE_BYTES    # x, dy in; dx out
 
 
-def bench_qk_norm_rope(dev, stream, reps):
+def bench_qk_norm_rope(dev, timer):
     """Qwen3 q_norm / k_norm fused with RoPE at the RoPE config: q [4, 16,
     2048, 128], k [4, 8, 2048, 128] bf16 as HF's transposed views of the
     projections, bf16 weights 1 + 0.1 N(0, 1), bf16 theta-1e6 tables [4,
@@ -226,21 +364,25 @@ def bench_qk_norm_rope(dev, stream, reps):
     sin = emb.sin().to(torch.bfloat16).unsqueeze(1)
     dq = gpu_randn((RB, RHQ, RS, RD), 64, dev)
     dk = gpu_randn((RB, RHK, RS, RD), 65, dev)
-    f_ms, how = time_graph(lambda: hip_ops.qk_norm_rope_fwd(q, k, wq, wk, cos, sin, 1e-6), stream, reps)
-    b_ms, _ = time_graph(lambda: hip_ops.qk_norm_rope_bwd(q, k, wq, wk, cos, sin, 1e-6, dq, dk),
-                         stream, reps)
-    return {"fwd_us": round(f_ms * 1e3, 2), "fwd_GB/s": round(QKN_FWD_BYTES / (f_ms * 1e-3) / 1e9, 1),
-            "bwd_us": round(b_ms * 1e3, 2), "bwd_GB/s": round(QKN_BWD_BYTES / (b_ms * 1e-3) / 1e9, 1),
-            "bwd_note": "includes the dw partial-row reduction launch", "timing": how}
+    f = timer.time(lambda: hip_ops.qk_norm_rope_fwd(q, k, wq, wk, cos, sin, 1e-6))
+    b = timer.time(lambda: hip_ops.qk_norm_rope_bwd(q, k, wq, wk, cos, sin, 1e-6, dq, dk))
+    C = rotating_copies(QKN_FWD_BYTES)
+    cp = [(q.clone(memory_format=torch.preserve_format), k.clone(memory_format=torch.preserve_format),
+           dq.clone(), dk.clone()) for _ in range(C)]
+    rf = time_rotating([lambda t=t: hip_ops.qk_norm_rope_fwd(t[0], t[1], wq, wk, cos, sin, 1e-6)
+                        for t in cp], timer.stream)
+    rb = time_rotating([lambda t=t: hip_ops.qk_norm_rope_bwd(t[0], t[1], wq, wk, cos, sin, 1e-6,
+                                                             t[2], t[3]) for t in cp], timer.stream)
+    del cp
+    return {"fwd": cold_line(f, QKN_FWD_BYTES, rot_ms=rf), "bwd": cold_line(b, QKN_BWD_BYTES, rot_ms=rb),
+            "bwd_note": "includes the dw partial-row reduction launch"}
 
 
-def bench_lora_bwd(dev, stream, reps):
+def bench_lora_bwd(dev, timer, reps=20):
     """Fused LoRA backward of a Qwen3-style 2B layer (QKV + MLP): X [8192, 2048],
     Wq [2048, 2048], Wk/Wv [1024, 2048], Wgate/Wup [6144, 2048], Wdown
     [2048, 6144] ~N(0, 0.02), rank 16, alpha 32, A ~N(0, 1/16), B ~N(0, 0.02);
     forward intermediates made by the library's forward ops beforehand."""
-    import torch
-
     from metal_liger_amd import hip_ops
     N, H, KV, I, r = LORA_N, LORA_H, LORA_KV, LORA_I, LORA_R
     s = 2.0
@@ -271,13 +413,14 @@ def bench_lora_bwd(dev, stream, reps):
         hip_ops.lora_mlp_bwd(x, gate, up, hmid, dy, WG, WU, WD, a_gu, a_d, BG, BU, BD,
                              [s, s, s], xa_gu, ha_d, r)
 
-    q_ms = time_launches(qkv, stream, reps)
-    m_ms = time_launches(mlp, stream, reps)
-    tot = q_ms + m_ms
+    q = timer.time(qkv, reps)
+    m = timer.time(mlp, reps)
+    tot = q["ms"] + m["ms"]
     tf = LORA_BWD_FLOP / (tot * 1e-3) / 1e12
-    return {"qkv_ms": round(q_ms, 3), "mlp_ms": round(m_ms, 3), "TFLOP/s": round(tf, 1),
+    return {"qkv_ms": round(q["ms"], 3), "mlp_ms": round(m["ms"], 3), "TFLOP/s": round(tf, 1),
             "mfma_frac": round(tf / MFMA_PEAK_TFLOPS, 4), "flop": LORA_BWD_FLOP,
-            "tokens_per_s": round(N / (tot * 1e-3), 1)}
+            "tokens_per_s": round(N / (tot * 1e-3), 1), "reps": reps,
+            "timing": "median of reps (flush before each)"}
 
 
 def build_train_model(dev, layers=None):
@@ -407,6 +550,14 @@ def pmc_probe(dev):
           "rms_norm add fwd, bwd [8192, 2048] bf16", flush=True)
 
 
+class _RunOnce:
+    """Stands in for ColdTimer where only the launches matter (PMC probes)."""
+
+    def time(self, fn, reps=1):
+        fn()
+        return {"ms": 1.0, "p10_ms": 1.0, "p90_ms": 1.0, "reps": 1}
+
+
 def pmc_mfma_probe(dev):
     """Launch sequence for rocprofv3 --pmc matrix-core counting: one warm-up
     and one measured call each of the one-pass FLCE forward (loss, dH, dW;
@@ -424,8 +575,7 @@ def pmc_mfma_probe(dev):
     torch.cuda.synchronize()
     del out, h, w, lab
     torch.cuda.empty_cache()
-    stream = torch.cuda.current_stream(dev)
-    bench_lora_bwd(dev, stream, 1)
+    bench_lora_bwd(dev, _RunOnce(), 1)
     torch.cuda.synchronize()
     print("pmc mfma probe: 2 x flce_fwd_grad, 2 x (lora qkv bwd + mlp bwd)", flush=True)
 
@@ -441,6 +591,34 @@ def load_traffic():
         return int(d["hbm_bytes_per_launch"])
     except (OSError, KeyError, ValueError):
         return None
+
+
+def host_cpu():
+    """os.cpu_count(), torch's thread count and the CPU model of this host."""
+    import torch
+    model = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"os_cpu_count": os.cpu_count(), "torch_threads": torch.get_num_threads(),
+            "model": model}
+
+
+def _time_cpu(fn, warmup, reps):
+    import statistics
+    for _ in range(warmup):
+        fn()
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return statistics.median(ts)
 
 
 def cpu_baseline(seconds: float):
@@ -489,7 +667,132 @@ def cpu_baseline(seconds: float):
         "sample": (f"oracle torch-CPU SwiGLU fwd+bwd on [{n}, {INTER}] bf16 + RoPE fwd+bwd on "
                    f"q [1,{RHQ},{RS},{RD}], k [1,{RHK},{RS},{RD}] bf16 (tables built per call), "
                    f"{reps} reps in {el:.1f} s, {sample_bytes} algorithmic bytes per rep"),
+        "host": host_cpu(),
     }
+
+
+def cpu_baselines(full: bool):
+    """The oracle (the reference's torch ops restated, run on this host's CPU
+    with all of torch's threads) on every config. full=False: bounded
+    samples (RMSNorm at full size; SwiGLU and RoPE on a quarter, LoRA on an
+    eighth, FLCE on a sixteenth of the tokens; the train step at batch 1 x
+    256), 1 warm-up + 3 reps (FLCE: 1 rep; train step: 1 warm-up + 1 rep),
+    ~15 s on an 8-core host; full=True: every config at its full shape, 1
+    warm-up + 3 reps for RMSNorm, SwiGLU, RoPE and LoRA, 1 rep for FLCE and
+    the train step. Each value is in the unit of the GPU line it stands
+    beside; the sample is named."""
+    import torch
+
+    from oracle import reference_ops as ref
+    torch.manual_seed(0)
+    out = {"host": host_cpu(), "full_shapes": full}
+    bf = torch.bfloat16
+
+    # RMSNorm fp32 [8192, 2048] fwd + bwd
+    x = seeded((RMS_N, RMS_H), 40, torch.float32)
+    w = 1.0 + 0.1 * seeded((RMS_H,), 41, torch.float32)
+    gy = seeded((RMS_N, RMS_H), 42, torch.float32)
+
+    def rms():
+        y, r = ref.rms_norm_forward(x, w, 1e-6)
+        ref.rms_norm_backward(x, w, r, gy)
+    t = _time_cpu(rms, 1, 3)
+    out["rmsnorm_fp32"] = {"GB/s": round((RMS_FWD_BYTES + RMS_BWD_BYTES) / t / 1e9, 2),
+                           "sample": f"x [{RMS_N}, {RMS_H}] fp32 fwd+bwd", "s_per_rep": round(t, 3)}
+
+    # SwiGLU bf16 [n, 6144] fwd + bwd
+    n = N_TOK if full else N_TOK // 4
+    g = seeded((n, INTER), 0, bf)
+    u = seeded((n, INTER), 1, bf)
+    dyy = seeded((n, INTER), 2, bf)
+
+    def swg():
+        o, sig = ref.swiglu_forward(g, u)
+        ref.swiglu_backward(g, u, sig, dyy)
+    t = _time_cpu(swg, 1, 3)
+    out["swiglu_bf16"] = {"GB/s": round(8 * n * INTER * 2 / t / 1e9, 2),
+                          "sample": f"gate/up [{n}, {INTER}] bf16 fwd+bwd", "s_per_rep": round(t, 3)}
+    del g, u, dyy
+
+    # RoPE bf16 fwd + bwd, tables built per call
+    b = RB if full else 1
+    q = seeded((b, RHQ, RS, RD), 3, bf)
+    k = seeded((b, RHK, RS, RD), 4, bf)
+    pos = torch.arange(RS)
+
+    def rope():
+        cos, sin = ref.rope_tables(pos, RD, THETA)
+        cos, sin = cos.to(bf), sin.to(bf)
+        ref.rope_forward(q, cos, sin), ref.rope_forward(k, cos, sin)
+        ref.rope_backward(q, cos, sin, bf), ref.rope_backward(k, cos, sin, bf)
+    t = _time_cpu(rope, 1, 3)
+    out["rope_bf16"] = {"GB/s": round(2 * 2 * b * (RHQ + RHK) * RS * RD * 2 / t / 1e9, 2),
+                        "sample": f"q [{b},{RHQ},{RS},{RD}], k [{b},{RHK},{RS},{RD}] bf16 fwd+bwd",
+                        "s_per_rep": round(t, 3)}
+    del q, k
+
+    # LoRA backward of the Qwen3-style layer (QKV + MLP), rank 16
+    nl = LORA_N if full else LORA_N // 8
+    H, KV, I, r = LORA_H, LORA_KV, LORA_I, LORA_R
+    X = seeded((nl, H), 20, bf)
+    qkv = [(seeded((o, H), 21 + i, bf) * 0.02, seeded((r, H), 24 + i, bf) * 0.25,
+            seeded((o, r), 27 + i, bf) * 0.02, 2.0) for i, o in enumerate((H, KV, KV))]
+    dqkv = [seeded((nl, o), 30 + i, bf) for i, o in enumerate((H, KV, KV))]
+    mlp = [(seeded((I, H), 33, bf) * 0.02, seeded((r, H), 34, bf) * 0.25, seeded((I, r), 35, bf) * 0.02, 2.0),
+           (seeded((I, H), 36, bf) * 0.02, seeded((r, H), 37, bf) * 0.25, seeded((I, r), 38, bf) * 0.02, 2.0),
+           (seeded((H, I), 39, bf) * 0.02, seeded((r, I), 40, bf) * 0.25, seeded((H, r), 41, bf) * 0.02, 2.0)]
+    fq = [t_ for p in qkv for t_ in p]
+    fm = [t_ for p in mlp for t_ in p]
+    dY = seeded((nl, H), 42, bf)
+    _, gate, up, hmid = ref.lora_mlp_forward(X, *fm)
+
+    def lora():
+        ref.lora_qkv_backward(X, *dqkv, *fq)
+        ref.lora_mlp_backward(X, gate, up, hmid, dY, *fm)
+    t = _time_cpu(lora, 1, 3)
+    lf = LORA_BWD_FLOP * nl / LORA_N
+    out["lora_bwd_layer"] = {"TFLOP/s": round(lf / t / 1e12, 3), "tokens_per_s": round(nl / t, 1),
+                             "sample": f"X [{nl}, {H}] (QKV + MLP backward, rank {r}) bf16",
+                             "s_per_rep": round(t, 3)}
+    del X, qkv, mlp, gate, up, hmid, dqkv, dY
+
+    # FLCE fwd + bwd over the full vocabulary (chunk 8192), fp32 inside
+    nf = FLCE_N if full else FLCE_N // 16
+    hf = seeded((nf, FLCE_H), 10, bf)
+    wf = seeded((FLCE_V, FLCE_H), 11, bf) * 0.02
+    gl = torch.Generator().manual_seed(12)
+    lab = torch.randint(0, FLCE_V, (nf,), generator=gl)
+    lab[torch.rand(nf, generator=gl) < 0.1] = -100
+
+    def flce():
+        loss, lse, mask = ref.flce_forward(hf, wf, lab, None, -100, FLCE_CHUNK)
+        ref.flce_backward(hf, wf, lab, lse, mask, torch.tensor(1.0), None, FLCE_CHUNK)
+    t = _time_cpu(flce, 0, 1)
+    ff = 3 * 2 * nf * FLCE_V * FLCE_H
+    out["flce_fwd_bwd"] = {"TFLOP/s": round(ff / t / 1e12, 3),
+                           "sample": f"hidden [{nf}, {FLCE_H}], lm_head [{FLCE_V}, {FLCE_H}] bf16",
+                           "s_per_rep": round(t, 3)}
+    del hf, wf
+
+    # 4-layer Qwen3-style LoRA train step (unpatched HF model: the same math
+    # as the reference's patched model, whose fused ops are torch on the CPU)
+    from tests import qwen_tiny
+    bs, sl = (qwen_tiny.TRAIN_B, qwen_tiny.TRAIN_S) if full else (1, 256)
+    model = qwen_tiny.build_train_config(torch.device("cpu"), attn="sdpa")
+    model.train()
+    params = [p for p in model.parameters() if p.requires_grad]
+    opt = torch.optim.AdamW(params, lr=1e-4)
+    ids = torch.randint(0, qwen_tiny.TRAIN_V, (bs, sl), generator=torch.Generator().manual_seed(0))
+
+    def step():
+        opt.zero_grad(set_to_none=True)
+        model(input_ids=ids, labels=ids).loss.backward()
+        opt.step()
+    t = _time_cpu(step, 0 if full else 1, 1)
+    out["train_step_4layer"] = {"tokens_per_s": round(bs * sl / t, 1),
+                                "sample": f"batch {bs} x seq {sl}, bf16, fwd + loss + bwd + AdamW",
+                                "s_per_rep": round(t, 3)}
+    return out
 
 
 def main():
@@ -499,6 +802,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--cpu-full", action="store_true",
+                    help="only the CPU baselines of every config at full shape (one JSON line; "
+                         "minutes of CPU work)")
     ap.add_argument("--pmc-probe", action="store_true",
                     help="only the launch sequence used for rocprofv3 --pmc traffic counting")
     ap.add_argument("--pmc-mfma-probe", action="store_true",
@@ -511,6 +817,9 @@ def main():
     ap.add_argument("--train-step-only", action="store_true",
                     help="only the 4-layer Qwen3 LoRA train step (one JSON line)")
     args = ap.parse_args()
+    if args.cpu_full:
+        print(json.dumps({"cpu_baselines": cpu_baselines(full=True)}), flush=True)
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: metal_liger_amd has no multi-GPU path "
               "(run with --gpus 1)", file=sys.stderr)
@@ -571,35 +880,42 @@ def main():
     wall = time.perf_counter() - t0
     gpu_ms_step = e0.elapsed_time(e1) / args.steps
 
-    # Per-kernel launch duration: HIP events on the kernel's stream around
-    # 20 back-to-back launches of that kernel alone, eagerly and replayed
-    # from a captured graph; the smaller of the two is kept (eager launches
-    # of the ~17 us RoPE kernel are timed through each call's host-side
-    # argument marshalling, a graph adds ~1.5 us between its nodes).
-    reps = 20
-    per_op, how = {}, {}
+    # Per-kernel launch duration, cold (ColdTimer: MALL / L2 flushed before
+    # each of 25 reps, median), and warm (20 back-to-back launches).
+    timer = ColdTimer(dev, stream)
+    per_op, warm, rot = {}, {}, {}
+    C = rotating_copies(ROPE_DIR_BYTES)
+    rot_in = [(gate.clone(), up.clone(), dy.clone(), q.clone(), k.clone()) for _ in range(C)]
+    rot_ops = {
+        "swiglu_fwd": lambda t: hip_ops.swiglu_fwd(t[0], t[1]),
+        "swiglu_bwd": lambda t: hip_ops.swiglu_bwd(t[0], t[1], t[2]),
+        "rope_fwd": lambda t: hip_ops.rope_pos(t[3], t[4], pos, inv, 1.0),
+        "rope_bwd": lambda t: hip_ops.rope_pos(t[3], t[4], pos, inv, -1.0),
+    }
     for name, fn in ops.items():
-        eager = time_launches(fn, stream, reps)
-        graph, gh = time_graph(fn, stream, reps)
-        per_op[name], how[name] = (graph, gh) if graph < eager else (eager, "eager launches")
+        per_op[name] = timer.time(fn)
+        warm[name] = time_launches(fn, stream, 20)
+        rot[name] = time_rotating([lambda t=t, f=rot_ops[name]: f(t) for t in rot_in], stream)
+    del rot_in
 
     ms_step = wall * 1e3 / args.steps
     value = STEP_BYTES / (wall / args.steps) / 1e9
     op_bytes = {"swiglu_fwd": SWIGLU_FWD_BYTES, "swiglu_bwd": SWIGLU_BWD_BYTES,
                 "rope_fwd": ROPE_DIR_BYTES, "rope_bwd": ROPE_DIR_BYTES}
-    breakdown = {n: {"us": round(per_op[n] * 1e3, 2),
-                     "GB/s": round(op_bytes[n] / (per_op[n] * 1e-3) / 1e9, 1), "timing": how[n]}
-                 for n in per_op}
+    breakdown = {n: dict(cold_line(per_op[n], op_bytes[n], rot_ms=rot[n]),
+                         warm_us=round(warm[n] * 1e3, 2)) for n in per_op}
+    breakdown["timing"] = TIMING_NOTE + ("; warm_us: mean of 20 back-to-back eager launches of "
+                                         "the same inputs")
     breakdown["gpu_ms_per_step"] = round(gpu_ms_step, 4)
-    breakdown["rmsnorm_fp32"] = bench_rmsnorm(dev, stream, reps)
-    breakdown["qk_norm_rope_bf16"] = bench_qk_norm_rope(dev, stream, reps)
-    breakdown["add_rmsnorm_bf16"] = bench_add_rmsnorm(dev, stream, reps)
+    breakdown["rmsnorm_fp32"] = bench_rmsnorm(dev, timer)
+    breakdown["qk_norm_rope_bf16"] = bench_qk_norm_rope(dev, timer)
+    breakdown["add_rmsnorm_bf16"] = bench_add_rmsnorm(dev, timer)
     if not args.no_mfma_ops:
-        breakdown["flce_fwd_bwd"] = bench_flce(dev, stream, 5)
-        breakdown["lora_bwd_layer"] = bench_lora_bwd(dev, stream, 10)
+        breakdown["flce_fwd_bwd"] = bench_flce(dev, timer)
+        breakdown["lora_bwd_layer"] = bench_lora_bwd(dev, timer)
     if not args.no_train_step:
         breakdown["train_step_4layer"] = bench_train_step(dev)
-    dom_ms = per_op["swiglu_bwd"]
+    dom_ms = rot["swiglu_bwd"]
     achieved = SWIGLU_BWD_BYTES / (dom_ms * 1e-3) / 1e9
     roofline = {
         "kernel": "swiglu_bwd_vec<bf16> (ml_swiglu_bwd)",
@@ -610,8 +926,11 @@ def main():
         "frac": round(achieved / HBM_PEAK_GBS, 4),
         "traffic": load_traffic(),
         "algorithmic_bytes_per_launch": SWIGLU_BWD_BYTES,
-        "avg_launch_us": round(dom_ms * 1e3, 2),
-        "timing": how["swiglu_bwd"],
+        "launch_us": round(dom_ms * 1e3, 2),
+        "flushed_launch_us": round(per_op["swiglu_bwd"]["ms"] * 1e3, 2),
+        "timing": ("back-to-back launches over 2 copies of gate/up/dy (1 GB, beyond the MALL), "
+                   "replayed from a captured graph; flushed_launch_us: median of 25 launches each "
+                   "after a 512 MB write + 512 MB read flush, dispatch gap included"),
     }
     line = {
         "metric": METRIC,
@@ -637,6 +956,7 @@ def main():
     }
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+        line["cpu_baselines"] = cpu_baselines(full=False)
     print(json.dumps(line), flush=True)
 
 

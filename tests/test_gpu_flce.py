@@ -213,3 +213,32 @@ def test_flce_config_full_size(dev):
     # size-independent property: softmax - one_hot sums to zero over the vocabulary
     colsum = dw.float().sum(0)
     assert colsum.abs().max().item() <= 1e-2 * dw.float().abs().sum(0).max().item()
+
+
+def test_flce_dw_over_16_token_chunks_full_vocab(dev):
+    """dW accumulated over 16 token chunks at the full vocabulary (N = 4096,
+    chunks of 256 tokens, V = 151936, H = 1024): each chunk's D^T H_c is
+    added into the bf16 output. Against the oracle evaluated in fp32 on the
+    same bf16 inputs (fp32 accumulation throughout, the "exact" value), dW is
+    at the bf16 bar, and its error is compared with the reference's own
+    rounding (the exact value rounded once to bf16, what its fp32 accumulator
+    followed by .to(bf16) gives)."""
+    from metal_liger_amd import hip_ops
+    N, H, V, T = 4096, 1024, 151936, 256
+    h, w, lab = make_inputs(N, H, V, seed=31, ignore_frac=0.1, w_scale=0.02)
+    hd, wd, ld = h.to(dev), w.to(dev), lab.to(dev)
+    loss, lse, n_valid, dh, dw = hip_ops.flce_fwd_grad(hd, wd, ld, None, -100, token_chunk=T)
+    rl, rlse, mask = ref.flce_forward(hd.float(), wd.float(), ld, None, -100, 8192)
+    ex_dh, ex_dw = ref.flce_backward(hd.float(), wd.float(), ld, rlse, mask,
+                                     torch.tensor(1.0, device=dev), None, 8192)
+    assert abs(loss.item() - rl.item()) <= 1e-3 * abs(rl.item())
+    e_dw = rel_fro(dw, ex_dw)
+    e_ref = rel_fro(ex_dw.to(torch.bfloat16), ex_dw)
+    e_dh = rel_fro(dh, ex_dh)
+    print(f"16 chunks: dW rel err {e_dw:.3e} (reference rounding {e_ref:.3e}), dH {e_dh:.3e}")
+    assert e_dw <= 2e-2 and e_dh <= 2e-2
+    # measured 3.6e-3 against 1.65e-3: the bf16 dlogits cost as much as the
+    # chunk-wise bf16 accumulation (dH, which is not accumulated, shows the
+    # same 3.6e-3)
+    assert e_dw <= 3.0 * e_ref, (e_dw, e_ref)
+    assert torch.allclose(dw.float(), ex_dw, rtol=2e-2, atol=1e-2)
