@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define ML_ABI_VERSION 4
+#define ML_ABI_VERSION 5
 
 /* dtype tags */
 #define ML_F32 0
@@ -306,6 +306,27 @@ int ml_flce_fwd_grad(const void* hidden, int64_t ldh, const void* weight, int64_
 int ml_flce_scale_grads(const float* grad_loss, void* d_hidden, int64_t n_hidden, void* d_weight,
                         int64_t n_weight, void* stream);
 
+/*
+ * fp32 fused linear cross-entropy (hidden, weight, bias and both gradients
+ * fp32; any H and V), with the reference's own vocabulary-chunked schedule
+ * (ops/fused_linear_cross_entropy.py:39-80, :93-185): per chunk of `chunk`
+ * vocabulary columns an fp32 [tokens, chunk] logits tile (the reference's
+ * chunk), online (max, sum exp) partials, then per chunk again the
+ * dlogits (softmax - one_hot) * mask / max(#valid, 1), dH += D W_c and
+ * dW_c = D^T H. Outputs as ml_flce_fwd_grad (gradients for d(loss) = 1;
+ * d_hidden / d_weight may be NULL). bias fp32 or NULL.
+ */
+size_t ml_flce_fwd_grad_f32_workspace_bytes(int64_t n_tokens, int64_t vocab, int64_t chunk);
+int ml_flce_fwd_grad_f32(const float* hidden, int64_t ldh, const float* weight, int64_t ldw,
+                         const float* bias, const int64_t* labels, int64_t n_tokens,
+                         int64_t vocab, int64_t hidden_size, int64_t ignore_index, int64_t chunk,
+                         float* loss, float* lse, float* n_valid, float* d_hidden,
+                         float* d_weight, void* workspace, size_t workspace_bytes, void* stream);
+
+/* ml_flce_scale_grads for fp32 gradients (16-byte aligned). */
+int ml_flce_scale_grads_f32(const float* grad_loss, float* d_hidden, int64_t n_hidden,
+                            float* d_weight, int64_t n_weight, void* stream);
+
 /* ----------------------------------------------------------- fused LoRA bwd
  * Replaces _LoRA_QKV.backward (ops/fused_lora.py:121-171). Three adapters
  * (q, k, v) share the saved input X [n_tokens, in_features] (bf16). For
@@ -399,6 +420,21 @@ int ml_gemm_bf16_splitk(int64_t M, int64_t N, int64_t K, const void* A, int64_t 
                         const void* B, int64_t ldb, int b_layout, void* C, int64_t ldc, int c_dtype,
                         float alpha, float beta, int tile_cfg, int ksplit, void* workspace,
                         size_t workspace_bytes, void* stream);
+
+/*
+ * fp32 products for the fp32 forms of the LoRA and FLCE ops (the reference
+ * runs _lora_linear / _LoRA_QKV / _LoRA_MLP in the activation dtype,
+ * ops/fused_lora.py:69-266, and its FLCE in fp32,
+ * ops/fused_linear_cross_entropy.py:108-109):
+ *   C = alpha * sum_s op(A_s) op(B_s) + beta * C      (fp32 throughout,
+ * v_mfma_f32_32x32x2_f32), layouts and K segments as ml_gemm_bf16_segments;
+ * any M, N, K and leading dimensions.
+ */
+int ml_gemm_f32_segments(int64_t M, int64_t N, int nseg, const int64_t* k_lens,
+                         const void* const* a_ptrs, const int64_t* ldas,
+                         const void* const* b_ptrs, const int64_t* ldbs, int a_layout,
+                         int b_layout, float* C, int64_t ldc, float alpha, float beta,
+                         void* stream);
 
 #ifdef __cplusplus
 }

@@ -184,23 +184,24 @@ def _(q, k, q_weight, k_weight, cos, sin, eps, dq_out, dk_out, need_dq_weight, n
 
 @torch.library.custom_op(f"{NS}::flce_fwd_grad", mutates_args=(), device_types=_DEV)
 def flce_fwd_grad(hidden: Tensor, weight: Tensor, labels: Tensor, bias: Optional[Tensor],
-                  ignore_index: int, need_dhidden: bool,
-                  need_dweight: bool) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+                  ignore_index: int, need_dhidden: bool, need_dweight: bool,
+                  chunk_size: int = 8192) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
     loss, lse, n_valid, dh, dw = hip_ops.flce_fwd_grad(hidden, weight, labels, bias, ignore_index,
-                                                       need_dhidden, need_dweight)
+                                                       need_dhidden, need_dweight,
+                                                       vocab_chunk=chunk_size)
     return (loss, lse, n_valid, dh if dh is not None else _none(lse),
             dw if dw is not None else _none(lse))
 
 
 @flce_fwd_grad.register_fake
-def _(hidden, weight, labels, bias, ignore_index, need_dhidden, need_dweight):
+def _(hidden, weight, labels, bias, ignore_index, need_dhidden, need_dweight, chunk_size=8192):
     N, H = hidden.shape
     V = weight.shape[0]
     f32 = torch.float32
     lse = hidden.new_empty((N,), dtype=f32)
     return (hidden.new_empty((), dtype=f32), lse, hidden.new_empty((1,), dtype=f32),
-            hidden.new_empty((N, H), dtype=torch.bfloat16) if need_dhidden else _none(lse),
-            hidden.new_empty((V, H), dtype=torch.bfloat16) if need_dweight else _none(lse))
+            hidden.new_empty((N, H), dtype=hidden.dtype) if need_dhidden else _none(lse),
+            hidden.new_empty((V, H), dtype=hidden.dtype) if need_dweight else _none(lse))
 
 
 @torch.library.custom_op(f"{NS}::flce_scale_grads", mutates_args=("d_hidden", "d_weight"),
@@ -229,11 +230,25 @@ def _(hidden, weight, labels, bias, ignore_index, lse, n_valid, grad_loss, chunk
       need_dhidden, need_dweight):
     N, H = hidden.shape
     V = weight.shape[0]
-    return (hidden.new_empty((N, H), dtype=torch.bfloat16) if need_dhidden else _none(lse),
-            hidden.new_empty((V, H), dtype=torch.bfloat16) if need_dweight else _none(lse))
+    return (hidden.new_empty((N, H), dtype=hidden.dtype) if need_dhidden else _none(lse),
+            hidden.new_empty((V, H), dtype=hidden.dtype) if need_dweight else _none(lse))
 
 
 # ------------------------------------------------------------------- LoRA --
+
+@torch.library.custom_op(f"{NS}::gemm_f32", mutates_args=(), device_types=_DEV)
+def gemm_f32(a_list: List[Tensor], b_list: List[Tensor], a_t: bool, b_t: bool,
+             alpha: float) -> Tensor:
+    """alpha * sum_s op(a_s) op(b_s), fp32 matrix cores (the fp32 LoRA path)."""
+    return hip_ops.gemm_f32(a_list, b_list, a_t, b_t, alpha)
+
+
+@gemm_f32.register_fake
+def _(a_list, b_list, a_t, b_t, alpha):
+    M = a_list[0].shape[1] if a_t else a_list[0].shape[0]
+    N = b_list[0].shape[0] if b_t else b_list[0].shape[1]
+    return a_list[0].new_empty((M, N), dtype=torch.float32)
+
 
 @torch.library.custom_op(f"{NS}::linear_bf16", mutates_args=(), device_types=_DEV)
 def linear_bf16(x2: Tensor, w: Tensor) -> Tensor:

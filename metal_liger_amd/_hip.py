@@ -97,6 +97,17 @@ SIGNATURES: dict[str, tuple] = {
          _sz, _p],
     ),
     "ml_flce_scale_grads": (_i32, [_p, _p, _i64, _p, _i64, _p]),
+    "ml_gemm_f32_segments": (
+        _i32,
+        [_i64, _i64, _i32, _i64p, ctypes.POINTER(_p), _i64p, ctypes.POINTER(_p), _i64p, _i32, _i32,
+         _p, _i64, _f32, _f32, _p],
+    ),
+    "ml_flce_fwd_grad_f32_workspace_bytes": (_sz, [_i64, _i64, _i64]),
+    "ml_flce_fwd_grad_f32": (
+        _i32,
+        [_p, _i64, _p, _i64, _p, _p, _i64, _i64, _i64, _i64, _i64, _p, _p, _p, _p, _p, _p, _sz, _p],
+    ),
+    "ml_flce_scale_grads_f32": (_i32, [_p, _p, _i64, _p, _i64, _p]),
     "ml_gemm_splitk_workspace_bytes": (_sz, [_i64, _i64, _i64, _i32]),
     "ml_gemm_bf16_splitk": (
         _i32,
@@ -122,7 +133,7 @@ SIGNATURES: dict[str, tuple] = {
     ),
 }
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 _lib = None
 _lock = threading.Lock()

@@ -253,22 +253,25 @@ __global__ __launch_bounds__(256) void dlogit_pass_kernel(
   }
 }
 
-// x *= g[0] for bf16 arrays (skipped as a whole when g[0] == 1).
-__global__ __launch_bounds__(256) void scale_bf16_kernel(bf16* __restrict__ x, int64_t n,
-                                                         const float* __restrict__ g) {
+// x *= g[0] for bf16 or fp32 arrays (skipped as a whole when g[0] == 1).
+// The vector loop needs x 16-byte aligned (the caller checks).
+template <typename T>
+__global__ __launch_bounds__(256) void scale_kernel(T* __restrict__ x, int64_t n,
+                                                    const float* __restrict__ g) {
+  constexpr int V = 16 / sizeof(T);
   const float s = g[0];
   if (s == 1.0f) return;
-  const int64_t nv = n / 8;
+  const int64_t nv = n / V;
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < nv; i += (int64_t)gridDim.x * 256) {
-    float v[8];
-    load_n<bf16, 8>(x + i * 8, v);
+    float v[V];
+    load_n<T, V>(x + i * V, v);
 #pragma unroll
-    for (int k = 0; k < 8; ++k) v[k] *= s;
-    store_n<bf16, 8>(x + i * 8, v);
+    for (int k = 0; k < V; ++k) v[k] *= s;
+    store_n<T, V>(x + i * V, v);
   }
-  for (int64_t i = nv * 8 + (int64_t)blockIdx.x * 256 + threadIdx.x; i < n;
+  for (int64_t i = nv * V + (int64_t)blockIdx.x * 256 + threadIdx.x; i < n;
        i += (int64_t)gridDim.x * 256)
-    x[i] = from_f32<bf16>(to_f32(x[i]) * s);
+    x[i] = from_f32<T>(to_f32(x[i]) * s);
 }
 
 // One wave per row: merge the row's partials into lse and its loss term.
@@ -420,9 +423,90 @@ __global__ __launch_bounds__(256) void zero_bf16_kernel(bf16* __restrict__ p, in
     p[i] = from_f32<bf16>(0.f);
 }
 
+__global__ __launch_bounds__(256) void zero_f32_kernel(float* __restrict__ p, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256)
+    p[i] = 0.f;
+}
+
 __global__ void empty_loss_kernel(float* loss, float* n_valid) {
   loss[0] = 0.f;
   n_valid[0] = 0.f;
+}
+
+// ----------------------------------------------- fp32 (vocabulary chunks) --
+// The fp32 form follows the reference's own schedule
+// (ops/fused_linear_cross_entropy.py:39-80): per vocabulary chunk an fp32
+// logits tile [N, C] from the fp32 matrix-core GEMM, reduced per row to a
+// (max, sum exp) partial that lse_reduce_kernel merges; then, per chunk
+// again, the logits recomputed and turned into dlogits in place, dH += D W_c
+// and dW_c = D^T H. Every value is fp32; the logits tile is the reference's
+// [N, chunk] fp32 chunk.
+
+// pmax / psum [row * nblk + blk] = (max_j z, sum_j exp(z - max)) over the C
+// logits of row `row` (z = Z + bias). One wave per row.
+template <typename TB>
+__global__ __launch_bounds__(256) void chunk_partials_f32_kernel(
+    const float* __restrict__ Z, int64_t ldz, int rows, int C, const TB* __restrict__ bias,
+    float* __restrict__ pmax, float* __restrict__ psum, int nblk, int blk) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const float* z = Z + (int64_t)row * ldz;
+  float mx = -INFINITY;
+  for (int j = lane; j < C; j += 64) mx = fmaxf(mx, z[j] + (bias ? to_f32(bias[j]) : 0.f));
+  mx = wave_max(mx);
+  float sm = 0.f;
+  for (int j = lane; j < C; j += 64) sm += expf((z[j] + (bias ? to_f32(bias[j]) : 0.f)) - mx);
+  sm = wave_sum(sm);
+  if (lane == 0) {
+    pmax[(int64_t)row * nblk + blk] = mx;
+    psum[(int64_t)row * nblk + blk] = sm;
+  }
+}
+
+// zy[t] = h_t . W[label_t] (+ b[label_t]) in fp32 for a label in [0, V),
+// else 0; any H. One wave per token.
+template <typename TB>
+__global__ __launch_bounds__(256) void label_logit_f32_kernel(
+    const float* __restrict__ hidden, int64_t ldh, const float* __restrict__ weight, int64_t ldw,
+    const TB* __restrict__ bias, const int64_t* __restrict__ labels, int M, int64_t V, int H,
+    float* __restrict__ zy) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= M) return;
+  const int64_t lab = labels[row];
+  if (lab < 0 || lab >= V) {
+    if (lane == 0) zy[row] = 0.f;
+    return;
+  }
+  const float* h = hidden + (int64_t)row * ldh;
+  const float* w = weight + lab * ldw;
+  float acc = 0.f;
+  for (int k = lane; k < H; k += 64) acc += h[k] * w[k];
+  acc = wave_sum(acc);
+  if (lane == 0) zy[row] = acc + (bias ? to_f32(bias[lab]) : 0.f);
+}
+
+// In place over the fp32 logits tile of columns c0 .. c0 + C - 1:
+// d = (exp(z + b - lse) - [c0 + j == label]) * [label != ignore] / max(n_valid, 1)
+// (the reference's softmax minus one-hot with its mask and 1 / #valid scale,
+// :67-76, for grad_output = 1). One block of 256 per row and column segment.
+template <typename TB>
+__global__ __launch_bounds__(256) void chunk_dlogit_f32_kernel(
+    float* __restrict__ Z, int64_t ldz, int rows, int C, int64_t c0, const TB* __restrict__ bias,
+    const float* __restrict__ lse, const int64_t* __restrict__ labels, int64_t ignore,
+    const float* __restrict__ n_valid) {
+  const int row = blockIdx.y;
+  if (row >= rows) return;
+  const int64_t lab = labels[row];
+  const float scale = lab != ignore ? 1.0f / fmaxf(n_valid[0], 1.0f) : 0.f;
+  const float L = lse[row];
+  float* z = Z + (int64_t)row * ldz;
+  for (int j = blockIdx.x * 256 + threadIdx.x; j < C; j += gridDim.x * 256) {
+    float p = expf((z[j] + (bias ? to_f32(bias[j]) : 0.f)) - L);
+    if (c0 + j == lab) p -= 1.0f;
+    z[j] = p * scale;
+  }
 }
 
 // -------------------------------------------------------------- host side --
@@ -673,11 +757,174 @@ int bwd_impl(const bf16* hidden, int64_t ldh, const bf16* weight, int64_t ldw, c
   return ML_OK;
 }
 
+// fp32 workspace: the logits tile [N, chunk], partials [N, nblk] x 2, zy,
+// loss_row, valid_row [N].
+size_t f32_ws_layout(int64_t N, int64_t V, int64_t chunk, float** Z, float** pm, float** ps,
+                     float** zy, float** lr, float** vr, char* base) {
+  auto al = [](size_t b) { return (b + 255) / 256 * 256; };
+  const int64_t nblk = (V + chunk - 1) / chunk;
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    char* p = base ? base + off : nullptr;
+    off += al(bytes);
+    return reinterpret_cast<float*>(p);
+  };
+  float* z = take((size_t)(N * chunk) * 4);
+  float* a = take((size_t)(N * nblk) * 4);
+  float* b = take((size_t)(N * nblk) * 4);
+  float* c = take((size_t)N * 4);
+  float* d = take((size_t)N * 4);
+  float* e = take((size_t)N * 4);
+  if (Z) {
+    *Z = z;
+    *pm = a;
+    *ps = b;
+    *zy = c;
+    *lr = d;
+    *vr = e;
+  }
+  return off;
+}
+
+template <typename TB>
+int fwd_grad_f32_impl(const float* hidden, int64_t ldh, const float* weight, int64_t ldw,
+                      const TB* bias, const int64_t* labels, int N, int V, int H, int64_t ignore,
+                      int chunk, float* loss, float* lse, float* n_valid, float* d_hidden,
+                      float* d_weight, char* ws, hipStream_t st) {
+  float *Z, *pm, *ps, *zy, *lr, *vr;
+  f32_ws_layout(N, V, chunk, &Z, &pm, &ps, &zy, &lr, &vr, ws);
+  const int nblk = (V + chunk - 1) / chunk;
+  const unsigned row_blocks = (unsigned)((N + 3) / 4);
+  count_valid_kernel<<<1, 1024, 0, st>>>(labels, N, ignore, n_valid);
+  ML_LAUNCH_CHECK();
+  auto logits = [&](int c0, int C) -> int {
+    const int64_t kl = H;
+    const void* a = hidden;
+    const void* b = weight + (int64_t)c0 * ldw;
+    return ml_gemm_f32_segments(N, C, 1, &kl, &a, &ldh, &b, &ldw, kKMajor, kKMajor, Z, chunk,
+                                1.0f, 0.0f, st);
+  };
+  for (int blk = 0, c0 = 0; c0 < V; ++blk, c0 += chunk) {  // pass 1: partials
+    const int C = V - c0 < chunk ? V - c0 : chunk;
+    int rc = logits(c0, C);
+    if (rc) return rc;
+    chunk_partials_f32_kernel<TB><<<row_blocks, 256, 0, st>>>(Z, chunk, N, C,
+                                                              bias ? bias + c0 : nullptr, pm, ps,
+                                                              nblk, blk);
+    ML_LAUNCH_CHECK();
+  }
+  label_logit_f32_kernel<TB><<<row_blocks, 256, 0, st>>>(hidden, ldh, weight, ldw, bias, labels, N,
+                                                         V, H, zy);
+  ML_LAUNCH_CHECK();
+  lse_reduce_kernel<<<row_blocks, 256, 0, st>>>(pm, ps, nblk, zy, labels, ignore, N, V, lse, lr,
+                                                 vr);
+  ML_LAUNCH_CHECK();
+  loss_mean_kernel<<<1, 1024, 0, st>>>(lr, vr, N, loss, n_valid);
+  ML_LAUNCH_CHECK();
+  if (!d_hidden && !d_weight) return ML_OK;
+  for (int c0 = 0; c0 < V; c0 += chunk) {  // pass 2: gradients
+    const int C = V - c0 < chunk ? V - c0 : chunk;
+    int rc = logits(c0, C);
+    if (rc) return rc;
+    const unsigned segs = (unsigned)std::min<int64_t>((C + 255) / 256, 16);
+    chunk_dlogit_f32_kernel<TB><<<dim3(segs, (unsigned)N), 256, 0, st>>>(
+        Z, chunk, N, C, c0, bias ? bias + c0 : nullptr, lse, labels, ignore, n_valid);
+    ML_LAUNCH_CHECK();
+    const float* wc = weight + (int64_t)c0 * ldw;
+    if (d_hidden) {  // dH (+)= D W_c
+      const int64_t kl = C;
+      const void* a = Z;
+      const int64_t lda = chunk;
+      const void* b = wc;
+      rc = ml_gemm_f32_segments(N, H, 1, &kl, &a, &lda, &b, &ldw, kKMajor, kMNMajor, d_hidden, H,
+                                1.0f, c0 > 0 ? 1.0f : 0.0f, st);
+      if (rc) return rc;
+    }
+    if (d_weight) {  // dW_c = D^T H
+      const int64_t kl = N;
+      const void* a = Z;
+      const int64_t lda = chunk;
+      const void* b = hidden;
+      rc = ml_gemm_f32_segments(C, H, 1, &kl, &a, &lda, &b, &ldh, kMNMajor, kMNMajor,
+                                d_weight + (int64_t)c0 * H, H, 1.0f, 0.0f, st);
+      if (rc) return rc;
+    }
+  }
+  return ML_OK;
+}
+
 }  // namespace
 }  // namespace flce
 }  // namespace mla
 
 using namespace mla;
+
+extern "C" size_t ml_flce_fwd_grad_f32_workspace_bytes(int64_t n_tokens, int64_t vocab,
+                                                      int64_t chunk) {
+  if (n_tokens <= 0 || vocab <= 0 || chunk <= 0) return 0;
+  return flce::f32_ws_layout(n_tokens, vocab, chunk, nullptr, nullptr, nullptr, nullptr, nullptr,
+                             nullptr, nullptr);
+}
+
+extern "C" int ml_flce_fwd_grad_f32(const float* hidden, int64_t ldh, const float* weight,
+                                    int64_t ldw, const float* bias, const int64_t* labels,
+                                    int64_t n_tokens, int64_t vocab, int64_t hidden_size,
+                                    int64_t ignore_index, int64_t chunk, float* loss, float* lse,
+                                    float* n_valid, float* d_hidden, float* d_weight,
+                                    void* workspace, size_t workspace_bytes, void* stream) {
+  ML_CHECK(n_tokens >= 0 && vocab > 0 && hidden_size > 0 && chunk > 0,
+           "flce f32: bad sizes tokens=%lld vocab=%lld hidden=%lld chunk=%lld",
+           (long long)n_tokens, (long long)vocab, (long long)hidden_size, (long long)chunk);
+  ML_CHECK(n_tokens < (1LL << 31) && vocab < (1LL << 31) && hidden_size < (1LL << 31),
+           "flce f32: sizes too large");
+  ML_CHECK(n_tokens == 0 || (hidden && labels), "flce f32: null hidden / labels");
+  ML_CHECK(weight && loss && n_valid, "flce f32: null weight / loss / n_valid");
+  ML_CHECK(n_tokens == 0 || lse, "flce f32: null lse");
+  ML_CHECK(ldh >= hidden_size && ldw >= hidden_size, "flce f32: leading dimension < hidden size");
+  hipStream_t st = (hipStream_t)stream;
+  if (n_tokens == 0) {
+    flce::empty_loss_kernel<<<1, 1, 0, st>>>(loss, n_valid);
+    ML_LAUNCH_CHECK();
+    // an empty sum: zero gradients for the weight (dH is empty); a fill
+    // kernel rather than a memset node, so the call can be graph-captured
+    if (d_weight) {
+      const int64_t n = vocab * hidden_size;
+      int64_t blocks = (n + 255) / 256;
+      blocks = blocks < 4096 ? blocks : 4096;
+      flce::zero_f32_kernel<<<dim3((unsigned)blocks), 256, 0, st>>>(d_weight, n);
+      ML_LAUNCH_CHECK();
+    }
+    return ML_OK;
+  }
+  const int64_t c = chunk < vocab ? chunk : vocab;
+  const size_t need = ml_flce_fwd_grad_f32_workspace_bytes(n_tokens, vocab, c);
+  ML_CHECK(workspace && workspace_bytes >= need, "flce f32: workspace too small (%zu < %zu)",
+           workspace_bytes, need);
+  return flce::fwd_grad_f32_impl<float>(hidden, ldh, weight, ldw, bias, labels, (int)n_tokens,
+                                        (int)vocab, (int)hidden_size, ignore_index, (int)c, loss,
+                                        lse, n_valid, d_hidden, d_weight,
+                                        static_cast<char*>(workspace), st);
+}
+
+extern "C" int ml_flce_scale_grads_f32(const float* grad_loss, float* d_hidden, int64_t n_hidden,
+                                       float* d_weight, int64_t n_weight, void* stream) {
+  ML_CHECK(grad_loss, "flce: null grad_loss");
+  ML_CHECK(n_hidden >= 0 && n_weight >= 0, "flce: negative sizes");
+  ML_CHECK((n_hidden == 0 || d_hidden) && (n_weight == 0 || d_weight), "flce: null gradient");
+  ML_CHECK((n_hidden == 0 || aligned16(d_hidden)) && (n_weight == 0 || aligned16(d_weight)),
+           "flce: gradients must be 16-byte aligned");
+  hipStream_t st = (hipStream_t)stream;
+  float* ptrs[2] = {d_hidden, d_weight};
+  const int64_t ns[2] = {n_hidden, n_weight};
+  for (int i = 0; i < 2; ++i) {
+    if (ns[i] == 0) continue;
+    int64_t blocks = (ns[i] / 4 + 255) / 256;
+    blocks = blocks < 4096 ? (blocks > 0 ? blocks : 1) : 4096;
+    flce::scale_kernel<float><<<dim3((unsigned)blocks), 256, 0, st>>>(ptrs[i], ns[i], grad_loss);
+    ML_LAUNCH_CHECK();
+  }
+  return ML_OK;
+}
 
 extern "C" size_t ml_flce_fwd_workspace_bytes(int64_t n_tokens, int64_t vocab) {
   if (n_tokens <= 0 || vocab <= 0) return 0;
@@ -821,7 +1068,7 @@ extern "C" int ml_flce_scale_grads(const float* grad_loss, void* d_hidden, int64
     if (ns[i] == 0) continue;
     int64_t blocks = (ns[i] / 8 + 255) / 256;
     blocks = blocks < 4096 ? (blocks > 0 ? blocks : 1) : 4096;
-    flce::scale_bf16_kernel<<<dim3((unsigned)blocks), 256, 0, st>>>(static_cast<bf16*>(ptrs[i]),
+    flce::scale_kernel<bf16><<<dim3((unsigned)blocks), 256, 0, st>>>(static_cast<bf16*>(ptrs[i]),
                                                                     ns[i], grad_loss);
     ML_LAUNCH_CHECK();
   }

@@ -532,15 +532,56 @@ def matmul(a: torch.Tensor, b: torch.Tensor, *, a_t: bool = False, b_t: bool = F
     return out
 
 
+def _f32_2d(t: torch.Tensor) -> torch.Tensor:
+    if t.dtype != torch.float32:
+        t = t.float()
+    if t.dim() != 2 or t.stride(1) != 1 or t.stride(0) < t.shape[1]:
+        t = t.contiguous()
+    return t
+
+
+def gemm_f32(a_list, b_list, a_t: bool = False, b_t: bool = False, alpha: float = 1.0):
+    """alpha * sum_s op(a_s) @ op(b_s) in fp32 on the matrix cores (op(x) =
+    x.T when the flag is set): a_s [M, K_s] (or [K_s, M]), b_s [K_s, N] (or
+    [N, K_s]). Returns a new [M, N] fp32 tensor."""
+    ensure_rocm_device(*a_list, *b_list)
+    if len(a_list) != len(b_list) or not a_list:
+        raise ValueError("gemm_f32: one b operand per a operand")
+    a_list = [_f32_2d(a) for a in a_list]
+    b_list = [_f32_2d(b) for b in b_list]
+    M = a_list[0].shape[1] if a_t else a_list[0].shape[0]
+    N = b_list[0].shape[0] if b_t else b_list[0].shape[1]
+    ks = []
+    for a, b in zip(a_list, b_list):
+        ma, ka = (a.shape[1], a.shape[0]) if a_t else (a.shape[0], a.shape[1])
+        kb, nb = (b.shape[1], b.shape[0]) if b_t else (b.shape[0], b.shape[1])
+        if ma != M or nb != N or ka != kb:
+            raise ValueError(f"gemm_f32: segment shapes {tuple(a.shape)} x {tuple(b.shape)} do "
+                             f"not fit [{M}, K] x [K, {N}]")
+        ks.append(int(ka))
+    out = torch.empty(M, N, dtype=torch.float32, device=a_list[0].device)
+    if M == 0 or N == 0:
+        return out
+    if sum(ks) == 0:
+        return out.zero_()
+    call(
+        "ml_gemm_f32_segments", M, N, len(ks), geom(ks), _hip.ptrs([a.data_ptr() for a in a_list]),
+        geom([a.stride(0) for a in a_list]), _hip.ptrs([b.data_ptr() for b in b_list]),
+        geom([b.stride(0) for b in b_list]), 1 if a_t else 0, 0 if b_t else 1, ptr(out),
+        out.stride(0), float(alpha), 0.0, stream_of(a_list[0]),
+    )
+    return out
+
+
 # -------------------------------------------------------------------- FLCE --
 
 
 def _flce_operands(hidden, weight, labels, bias):
     ensure_rocm_device(hidden, weight, labels, bias)
-    if hidden.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16:
+    if hidden.dtype != weight.dtype or hidden.dtype not in (torch.bfloat16, torch.float32):
         raise TypeError(
-            "fused linear cross-entropy runs bf16 MFMA GEMMs: hidden and weight must be bfloat16 "
-            f"(got {hidden.dtype}, {weight.dtype})"
+            "fused linear cross-entropy: hidden and weight must share a dtype, bfloat16 (bf16 "
+            f"MFMA GEMMs) or float32 (fp32 MFMA GEMMs) (got {hidden.dtype}, {weight.dtype})"
         )
     if hidden.dim() != 2 or weight.dim() != 2 or hidden.shape[1] != weight.shape[1]:
         raise ValueError(f"flce: hidden {tuple(hidden.shape)} / weight {tuple(weight.shape)} mismatch")
@@ -557,9 +598,33 @@ def _flce_operands(hidden, weight, labels, bias):
     if bias is not None:
         if bias.shape != (weight.shape[0],):
             raise ValueError("flce: bias must be [vocab]")
-        bias = bias if bias.dtype in (torch.float32, torch.bfloat16) else bias.float()
+        ok = (torch.float32, torch.bfloat16) if hidden.dtype == torch.bfloat16 else (torch.float32,)
+        bias = bias if bias.dtype in ok else bias.float()
         bias = bias.contiguous()
     return hidden, weight, labels, bias
+
+
+def _flce_f32(hidden, weight, labels, bias, ignore_index, need_dhidden, need_dweight, chunk):
+    """fp32 loss, lse, n_valid and (unit grad_output) gradients by the
+    vocabulary-chunked schedule (ml_flce_fwd_grad_f32)."""
+    N, H = hidden.shape
+    V = weight.shape[0]
+    dev = hidden.device
+    f32 = torch.float32
+    loss = torch.empty((), dtype=f32, device=dev)
+    lse = torch.empty(N, dtype=f32, device=dev)
+    n_valid = torch.empty(1, dtype=f32, device=dev)
+    dh = torch.empty(N, H, dtype=f32, device=dev) if need_dhidden else None
+    dw = torch.empty(V, H, dtype=f32, device=dev) if need_dweight else None
+    c = max(1, min(int(chunk), V))
+    wsb = _hip.query("ml_flce_fwd_grad_f32_workspace_bytes", N, V, c)
+    ws = torch.empty(max(wsb, 16), dtype=torch.uint8, device=dev)
+    call(
+        "ml_flce_fwd_grad_f32", ptr(hidden), hidden.stride(0) if N > 0 else H, ptr(weight),
+        weight.stride(0), ptr(bias), ptr(labels), N, V, H, int(ignore_index), c, ptr(loss),
+        ptr(lse), ptr(n_valid), ptr(dh), ptr(dw), ptr(ws), ws.numel(), stream_of(weight),
+    )
+    return loss, lse, n_valid, dh, dw
 
 
 def flce_fwd(hidden, weight, labels, bias=None, ignore_index: int = -100):
@@ -596,13 +661,18 @@ def flce_token_chunk(n_tokens: int, vocab: int) -> int:
 
 def flce_fwd_grad(hidden, weight, labels, bias=None, ignore_index: int = -100,
                   need_dhidden: bool = True, need_dweight: bool = True,
-                  token_chunk: int | None = None):
-    """Loss and gradients in one pass (logits computed once).
+                  token_chunk: int | None = None, vocab_chunk: int = 8192):
+    """Loss and gradients for d(loss) = 1.
 
-    Returns (loss 0-d fp32, lse [N] fp32, n_valid [1] fp32, d_hidden bf16 or
-    None, d_weight bf16 or None); the gradients are for d(loss) = 1.
+    bf16: one pass over token chunks (logits computed once); fp32: the
+    reference's vocabulary-chunked schedule with vocab_chunk columns per
+    chunk. Returns (loss 0-d fp32, lse [N] fp32, n_valid [1] fp32, d_hidden
+    or None, d_weight or None), gradients in the input dtype.
     """
     hidden, weight, labels, bias = _flce_operands(hidden, weight, labels, bias)
+    if hidden.dtype == torch.float32:
+        return _flce_f32(hidden, weight, labels, bias, ignore_index, need_dhidden, need_dweight,
+                         vocab_chunk)
     N, H = hidden.shape
     V = weight.shape[0]
     dev = hidden.device
@@ -624,22 +694,29 @@ def flce_fwd_grad(hidden, weight, labels, bias=None, ignore_index: int = -100,
 
 
 def flce_scale_grads(grad_loss, d_hidden, d_weight):
-    """d_hidden *= grad_loss, d_weight *= grad_loss in place (bf16; no-op
-    on the device when grad_loss == 1)."""
+    """d_hidden *= grad_loss, d_weight *= grad_loss in place (bf16 or fp32,
+    as flce_fwd_grad returned them; no-op on the device when grad_loss == 1)."""
     t = d_hidden if d_hidden is not None else d_weight
     if t is None:
         return
     g = grad_loss.detach().to(device=t.device, dtype=torch.float32).reshape(1).contiguous()
+    fn = "ml_flce_scale_grads_f32" if t.dtype == torch.float32 else "ml_flce_scale_grads"
     call(
-        "ml_flce_scale_grads", ptr(g), ptr(d_hidden), d_hidden.numel() if d_hidden is not None else 0,
+        fn, ptr(g), ptr(d_hidden), d_hidden.numel() if d_hidden is not None else 0,
         ptr(d_weight), d_weight.numel() if d_weight is not None else 0, stream_of(t),
     )
 
 
 def flce_bwd(hidden, weight, labels, bias, ignore_index, lse, n_valid, grad_loss, chunk_size,
              need_dhidden=True, need_dweight=True):
-    """Returns (d_hidden bf16 or None, d_weight bf16 or None)."""
+    """Returns (d_hidden or None, d_weight or None) in the input dtype."""
     hidden, weight, labels, bias = _flce_operands(hidden, weight, labels, bias)
+    if hidden.dtype == torch.float32:
+        # the fp32 schedule recomputes everything from the inputs
+        _, _, _, dh, dw = _flce_f32(hidden, weight, labels, bias, ignore_index, need_dhidden,
+                                    need_dweight, chunk_size)
+        flce_scale_grads(grad_loss, dh, dw)
+        return dh, dw
     N, H = hidden.shape
     V = weight.shape[0]
     dev = hidden.device

@@ -23,6 +23,10 @@ computed. dW is skipped when the lm_head weight is frozen.
 Semantics kept from the reference: labels are not shifted; ignore_index
 tokens contribute nothing; the mean divides by max(#valid, 1) (all-ignored
 batches give loss 0); the loss is fp32; no bias gradient is returned.
+fp32 inputs run the reference's own vocabulary-chunked schedule on fp32
+matrix-core GEMMs (logits tile [tokens, chunk_size] fp32); other float
+dtypes are upcast to fp32 first, as the reference upcasts, and their
+gradients cast back.
 
 ``patch_causal_lm_loss(model)`` (``apply_metal_liger_to_qwen3vl(...,
 fuse_lm_loss=True)``) goes one step further than the reference, whose
@@ -43,6 +47,15 @@ from metal_liger_amd import _custom_ops as cops
 from metal_liger_amd._model_walk import shadowed
 
 
+def _compute_dtype(hidden, weight, bias):
+    """hidden, weight (and bias) in the dtype the kernels compute in: bf16
+    stays bf16; fp32 stays fp32; any other float dtype (or a mix) is upcast
+    to fp32, as the reference upcasts both (:108-109)."""
+    if hidden.dtype == weight.dtype and hidden.dtype in (torch.bfloat16, torch.float32):
+        return hidden, weight, bias
+    return hidden.float(), weight.float(), bias.float() if bias is not None else None
+
+
 class _FusedLinearCrossEntropyFunction(torch.autograd.Function):
     """Linear + cross-entropy that never materialises full logits
     (ops/fused_linear_cross_entropy.py:82-185)."""
@@ -52,8 +65,9 @@ class _FusedLinearCrossEntropyFunction(torch.autograd.Function):
                 labels: torch.Tensor, bias: torch.Tensor = None,
                 ignore_index: int = -100, chunk_size: int = 8192):
         need_h, need_w = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
+        hidden_c, weight_c, bias_c = _compute_dtype(hidden, weight, bias)
         loss, lse, n_valid, dh, dw = cops.flce_fwd_grad(
-            hidden, weight, labels, bias, ignore_index, need_h, need_w)
+            hidden_c, weight_c, labels, bias_c, ignore_index, need_h, need_w, chunk_size)
         ctx.save_for_backward(hidden, weight, labels, lse, n_valid)
         # The gradients are handed over (scaled in place) by the first
         # backward, so they are kept out of the saved tensors, whose versions
@@ -78,8 +92,9 @@ class _FusedLinearCrossEntropyFunction(torch.autograd.Function):
         else:
             # a second backward through the same graph: fresh tensors from the
             # vocabulary-chunked recomputation
+            hidden_c, weight_c, bias_c = _compute_dtype(hidden, weight, ctx.bias)
             grad_hidden, grad_weight = cops.flce_bwd(
-                hidden, weight, labels, ctx.bias, ctx.ignore_index, lse, n_valid, grad_output,
+                hidden_c, weight_c, labels, bias_c, ctx.ignore_index, lse, n_valid, grad_output,
                 ctx.chunk_size, need_h, need_w)
             grad_hidden, grad_weight = cops.maybe(grad_hidden), cops.maybe(grad_weight)
         if grad_hidden is not None and grad_hidden.dtype != hidden.dtype:

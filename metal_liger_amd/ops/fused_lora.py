@@ -23,8 +23,10 @@ Semantics kept from the reference (ops/fused_lora.py:43-421): PEFT parameter
 layout (first adapter only, dropout ignored), A/B cast to the activation
 dtype, dA/dB returned in fp32, no gradient for the frozen base weights, and
 the patcher shadows q/k/v_proj without replacing modules (state_dict keys
-unchanged). The HIP path computes in bf16 (MI355X's training dtype); other
-activation dtypes raise.
+unchanged). bf16 activations run the bf16 MFMA kernels above; fp32 (and,
+upcast, fp16) activations run fp32 matrix-core products of the same
+formulas (gemm_f32: forward [X | X A^T] x [W; s B]^T, backward P = s dY B,
+dA = P^T X, dB = s dY^T (X A^T), dX one K-concatenated product).
 """
 
 import logging
@@ -55,12 +57,38 @@ def _get_lora_params(linear):
     return W, A, B, scaling
 
 
-def _check_bf16(X: torch.Tensor, what: str):
-    if X.dtype != torch.bfloat16:
-        raise TypeError(
-            f"metal_liger_amd {what}: the fused LoRA path runs bf16 MFMA GEMMs; got activations "
-            f"of dtype {X.dtype} (cast the model to bfloat16)"
-        )
+def _check_float(X: torch.Tensor, what: str):
+    if not X.is_floating_point():
+        raise TypeError(f"metal_liger_amd {what}: activations must be floating point (got {X.dtype})")
+
+
+# ---------------------------------------------------------- fp32 building blocks --
+# Activations other than bf16 run in fp32 on the fp32 matrix cores (fp16 is
+# upcast, as the reference's fp32 upcasts elsewhere; outputs and dX are cast
+# back to the activation dtype, dA / dB are fp32 as in the reference).
+
+def _f32(t: torch.Tensor) -> torch.Tensor:
+    return t.detach().float()
+
+
+def _lora_out_f32(X2, W, A, B, s):
+    """(X W^T + (X A^T) (s B)^T, X A^T) in fp32 (ops/fused_lora.py:69-82)."""
+    xa = cops.gemm_f32([X2], [_f32(A)], False, True, 1.0)
+    out = cops.gemm_f32([X2, xa], [_f32(W), _f32(B) * float(s)], False, True, 1.0)
+    return out, xa
+
+
+def _adapter_grads_f32(dY, X2, xa, B, s):
+    """P = s dY B, dA = P^T X, dB = s dY^T (X A^T) in fp32
+    (ops/fused_lora.py:121-171)."""
+    P = cops.gemm_f32([dY], [B], False, False, float(s))
+    dA = cops.gemm_f32([P], [X2], True, False, 1.0)
+    dB = cops.gemm_f32([dY], [xa], True, False, float(s))
+    return P, dA, dB
+
+
+def _rows_f32(t: torch.Tensor) -> torch.Tensor:
+    return t.reshape(-1, t.shape[-1]).float()
 
 
 def _pad_rank(r: int) -> int:
@@ -90,9 +118,17 @@ def _pad_b(B: torch.Tensor, rp: int, scale: float = 1.0) -> torch.Tensor:
 
 def _lora_linear(X: torch.Tensor, W: torch.Tensor,
                  A: torch.Tensor, B: torch.Tensor, scaling: float) -> torch.Tensor:
-    """X W^T + s (X A^T) B^T (ops/fused_lora.py:69-82) on the MFMA engine."""
-    _check_bf16(X, "_lora_linear")
+    """X W^T + s (X A^T) B^T (ops/fused_lora.py:69-82) on the MFMA engine
+    (bf16 activations: bf16 products; other float dtypes: fp32 products)."""
+    _check_float(X, "_lora_linear")
     shape = X.shape
+    if X.dtype != torch.bfloat16:
+        X2 = _rows_f32(X)
+        if A is None or B is None:
+            out = cops.gemm_f32([X2], [_f32(W)], False, True, 1.0)
+        else:
+            out, _ = _lora_out_f32(X2, W, A, B, scaling)
+        return out.to(X.dtype).view(*shape[:-1], out.shape[-1])
     X2 = hip_ops._bf16_rows(X.reshape(-1, shape[-1]))
     W2 = hip_ops._bf16_rows(W.detach())
     if A is None or B is None:
@@ -114,8 +150,21 @@ class _LoRA_QKV(torch.autograd.Function):
                 QW, QA, QB, QS,
                 KW, KA, KB, KS,
                 VW, VA, VB, VS):
-        _check_bf16(X, "LoRA QKV")
+        _check_float(X, "LoRA QKV")
         shape = X.shape
+        ctx.fp32 = X.dtype != torch.bfloat16
+        if ctx.fp32:
+            X2 = _rows_f32(X)
+            outs, xas = [], []
+            for W, A, B, S in ((QW, QA, QB, QS), (KW, KA, KB, KS), (VW, VA, VB, VS)):
+                o, xa = _lora_out_f32(X2, W, A, B, S)
+                outs.append(o.to(X.dtype).view(*shape[:-1], o.shape[-1]))
+                xas.append(xa)
+            ctx.save_for_backward(X2, *xas, *(_f32(W) for W in (QW, KW, VW)),
+                                  *(_f32(A) for A in (QA, KA, VA)), *(_f32(B) for B in (QB, KB, VB)))
+            ctx.scales = [float(QS), float(KS), float(VS)]
+            ctx.orig_shape, ctx.x_dtype = shape, X.dtype
+            return tuple(outs)
         Xf = hip_ops._bf16_rows(X.reshape(-1, shape[-1]))
         ranks = {QA.shape[0], KA.shape[0], VA.shape[0]}
         if len(ranks) != 1:
@@ -140,6 +189,22 @@ class _LoRA_QKV(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, dQ, dK, dV):
+        if ctx.fp32:
+            X2, *rest = ctx.saved_tensors
+            xas, Ws, As, Bs = rest[0:3], rest[3:6], rest[6:9], rest[9:12]
+            dys = [_rows_f32(d) for d in (dQ, dK, dV)]
+            grads, a_ops, b_ops = [], [], []
+            for dy, xa, W, A, B, s in zip(dys, xas, Ws, As, Bs, ctx.scales):
+                P, dA, dB = _adapter_grads_f32(dy, X2, xa, B, s)
+                grads.append((dA, dB))
+                a_ops += [dy, P]
+                b_ops += [W, A]
+            dX = cops.gemm_f32(a_ops, b_ops, False, False, 1.0)
+            dX = dX.to(ctx.x_dtype).view(*ctx.orig_shape)
+            return (dX,
+                    None, grads[0][0], grads[0][1], None,
+                    None, grads[1][0], grads[1][1], None,
+                    None, grads[2][0], grads[2][1], None)
         Xf, xa, a_stack, QW, KW, VW, QB, KB, VB = ctx.saved_tensors
         r, rp = ctx.rank, ctx.rank_p
         shape = ctx.orig_shape
@@ -167,8 +232,20 @@ class _LoRA_MLP(torch.autograd.Function):
                 GW, GA, GB, GS,   # gate projection
                 UW, UA, UB, US,   # up projection
                 DW, DA, DB, DS):  # down projection
-        _check_bf16(X, "LoRA MLP")
+        _check_float(X, "LoRA MLP")
         shape = X.shape
+        ctx.fp32 = X.dtype != torch.bfloat16
+        if ctx.fp32:
+            X2 = _rows_f32(X)
+            gate, xa_g = _lora_out_f32(X2, GW, GA, GB, GS)
+            up, xa_u = _lora_out_f32(X2, UW, UA, UB, US)
+            h = cops.swiglu_fwd(gate, up)                          # silu(gate) * up, fp32
+            out, ha = _lora_out_f32(h, DW, DA, DB, DS)
+            ctx.save_for_backward(X2, gate, up, h, xa_g, xa_u, ha,
+                                  *(_f32(t) for t in (GW, UW, DW, GA, UA, DA, GB, UB, DB)))
+            ctx.scales = [float(GS), float(US), float(DS)]
+            ctx.orig_shape, ctx.x_dtype = shape, X.dtype
+            return out.to(X.dtype).view(*shape[:-1], out.shape[-1])
         Xf = hip_ops._bf16_rows(X.reshape(-1, shape[-1]))
         ranks = {GA.shape[0], UA.shape[0], DA.shape[0]}
         if len(ranks) != 1:
@@ -194,6 +271,21 @@ class _LoRA_MLP(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, dY):
+        if ctx.fp32:
+            (X2, gate, up, h, xa_g, xa_u, ha, GW, UW, DW, GA, UA, DA, GB, UB, DB) = ctx.saved_tensors
+            sg, su, sd = ctx.scales
+            dy = _rows_f32(dY)
+            PD, dA_D, dB_D = _adapter_grads_f32(dy, h, ha, DB, sd)
+            dH = cops.gemm_f32([dy, PD], [DW, DA], False, False, 1.0)
+            d_gate, d_up = cops.swiglu_bwd(gate, up, dH)
+            PG, dA_G, dB_G = _adapter_grads_f32(d_gate, X2, xa_g, GB, sg)
+            PU, dA_U, dB_U = _adapter_grads_f32(d_up, X2, xa_u, UB, su)
+            dX = cops.gemm_f32([d_gate, PG, d_up, PU], [GW, GA, UW, UA], False, False, 1.0)
+            dX = dX.to(ctx.x_dtype).view(*ctx.orig_shape)
+            return (dX,
+                    None, dA_G, dB_G, None,
+                    None, dA_U, dB_U, None,
+                    None, dA_D, dB_D, None)
         (Xf, gate, up, h, xa_gu, ha_d, a_gu, a_d, GW, UW, DW, BG, BU, BD) = ctx.saved_tensors
         r, rp = ctx.rank, ctx.rank_p
         shape = ctx.orig_shape
@@ -217,8 +309,15 @@ class _LoRA_W(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, X, W, A, B, S):
-        _check_bf16(X, "LoRA projection")
+        _check_float(X, "LoRA projection")
         shape = X.shape
+        ctx.fp32 = X.dtype != torch.bfloat16
+        if ctx.fp32:
+            X2 = _rows_f32(X)
+            out, xa = _lora_out_f32(X2, W, A, B, S)
+            ctx.save_for_backward(X2, xa, _f32(W), _f32(A), _f32(B))
+            ctx.scale, ctx.orig_shape, ctx.x_dtype = float(S), shape, X.dtype
+            return out.to(X.dtype).view(*shape[:-1], out.shape[-1])
         Xf = hip_ops._bf16_rows(X.reshape(-1, shape[-1]))
         r = A.shape[0]
         rp = _pad_rank(r)
@@ -236,6 +335,12 @@ class _LoRA_W(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, dY):
+        if ctx.fp32:
+            X2, xa, W, A, B = ctx.saved_tensors
+            dy = _rows_f32(dY)
+            P, dA, dB = _adapter_grads_f32(dy, X2, xa, B, ctx.scale)
+            dX = cops.gemm_f32([dy, P], [W, A], False, False, 1.0)
+            return dX.to(ctx.x_dtype).view(*ctx.orig_shape), None, dA, dB, None
         Xf, xa, a, Wc, Bp = ctx.saved_tensors
         r, rp = ctx.rank, ctx.rank_p
         dy = hip_ops._bf16_rows(dY.reshape(-1, dY.shape[-1]))

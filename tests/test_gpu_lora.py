@@ -260,13 +260,3 @@ def test_lora_linear_single_projection(dev, N, IN, OUT, r):
     check(Xd.grad, fdX, rdX, "dX")
     check(Ad.grad.float(), fdA, rdA, "dA")
     check(Bd.grad.float(), fdB, rdB, "dB")
-
-
-def test_lora_rejects_fp32(dev):
-    from metal_liger_amd.ops.fused_lora import _LoRA_QKV
-    X = torch.randn(4, 64, device=dev)
-    W = torch.randn(64, 64, device=dev)
-    A = torch.randn(8, 64, device=dev)
-    B = torch.randn(64, 8, device=dev)
-    with pytest.raises(TypeError, match="bf16"):
-        _LoRA_QKV.apply(X, W, A, B, 2.0, W, A, B, 2.0, W, A, B, 2.0)

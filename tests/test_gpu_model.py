@@ -127,3 +127,27 @@ def test_patched_qwen3_vl_train_step(dev):
         e_bf = rel_fro(g_bf[n], g_ex[n])
         e_pt = rel_fro(g_pt[n], g_ex[n])
         assert e_pt <= 1.5 * e_bf + 2e-3, f"{n}: patched {e_pt:.3e} vs bf16 {e_bf:.3e}"
+
+
+def test_patched_qwen3_lora_train_step_fp32(dev):
+    """An fp32 model (the reference's own test dtype) patched with every
+    flag: the fused LoRA Functions run fp32 matrix-core products, the norms
+    and SwiGLU their fp32 kernels, the loss the fp32 chunked cross-entropy;
+    loss and LoRA gradients match the unpatched fp32 model (relative 1e-4:
+    fp32 sums in another order through two layers)."""
+    from metal_liger_amd import apply_metal_liger_to_qwen3vl
+    attn = qwen_tiny.register_fp32_attention()
+    base = qwen_tiny.build(seed=11, attn=attn, dtype=torch.float32).to(dev)
+    for n, p in base.named_parameters():
+        p.requires_grad_("lora_" in n)
+    patched = apply_metal_liger_to_qwen3vl(copy.deepcopy(base), fuse_qk_norm_rope=True,
+                                           fuse_lm_loss=True, fuse_residual_norm=True)
+    for n, p in patched.named_parameters():
+        p.requires_grad_("lora_" in n)
+    ids = torch.randint(0, 512, (2, 64), generator=torch.Generator().manual_seed(12)).to(dev)
+    l_ref, g_ref = train_step(base, ids)
+    l_pt, g_pt = train_step(patched, ids)
+    assert abs(l_pt - l_ref).item() <= 1e-5 * abs(l_ref.item())
+    assert set(g_pt) == set(g_ref) and len(g_ref) == 2 * 7 * 2
+    for n in g_ref:
+        assert rel_fro(g_pt[n], g_ref[n]) <= 1e-4, (n, rel_fro(g_pt[n], g_ref[n]))
