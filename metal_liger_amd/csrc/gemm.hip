@@ -19,8 +19,14 @@ int run(int64_t M, int64_t N, int nseg, const Segment* segs, int la, int lb, voi
   int rc = make_problem<BigCfg>(pb, (int)M, (int)N, nseg, segs, la, lb, 0);
   if (rc) return rc;
   hipStream_t st = (hipStream_t)stream;
-  if (c_dtype == ML_F32) return launch_store<float>(pb, la, lb, C, ldc, alpha, beta, st);
-  if (c_dtype == ML_BF16) return launch_store<bf16>(pb, la, lb, C, ldc, alpha, beta, st);
+  // r4 is the faster engine when A is K-major, the big engine otherwise
+  if (la == kKMajor) {
+    if (c_dtype == ML_F32) return launch_store<float, R4Cfg>(pb, la, lb, C, ldc, alpha, beta, st);
+    if (c_dtype == ML_BF16) return launch_store<bf16, R4Cfg>(pb, la, lb, C, ldc, alpha, beta, st);
+  } else {
+    if (c_dtype == ML_F32) return launch_store<float>(pb, la, lb, C, ldc, alpha, beta, st);
+    if (c_dtype == ML_BF16) return launch_store<bf16>(pb, la, lb, C, ldc, alpha, beta, st);
+  }
   set_error("gemm: C dtype %d not supported (fp32 or bf16)", c_dtype);
   return ML_ERR_INVALID;
 }

@@ -59,17 +59,20 @@ constexpr int kXcds = 8;
 #define ML_GEMM_GROUP_M 8
 #endif
 
-template <int BM_, int BN_, int WAVES_M_>
+
+// ENGINE_ selects the engine of the 256 x 256 tile: 1 = the big engine (8
+// waves, 32-deep k-tiles), 2 = r4 (4 waves, 64-deep k-tiles).
+template <int BM_, int BN_, int WAVES_M_, int ENGINE_ = 1>
 struct Cfg {
-  static constexpr int BM = BM_, BN = BN_;
+  static constexpr int BM = BM_, BN = BN_, ENGINE = ENGINE_;
   static constexpr int WAVES_M = WAVES_M_, WAVES_N = 4 / WAVES_M_;
   static constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
   static constexpr int TM = WM / 32, TN = WN / 32;
   static constexpr int A_BYTES = BM * kRowBytes, B_BYTES = BN * kRowBytes;
   static constexpr int STAGE_BYTES = A_BYTES + B_BYTES;
   static constexpr int LDS_BYTES = 2 * STAGE_BYTES;
-  // the 256 x 256 tile runs its own engine with 8 waves
-  static constexpr int THREADS = (BM_ == 256 && BN_ == 256) ? 512 : 256;
+  // the 256 x 256 tile runs its own engines (8 waves, or 4 for r4)
+  static constexpr int THREADS = (BM_ == 256 && BN_ == 256) ? (ENGINE_ == 2 ? 256 : 512) : 256;
   static_assert(WAVES_M * WAVES_N == 4, "4 waves per block");
   static_assert(TM >= 1 && TN >= 1 && WM % 32 == 0 && WN % 32 == 0, "wave tile of 32x32 MFMAs");
   static_assert(BM <= 256 && BN <= 256, "at most one 16-byte chunk set per thread");
@@ -77,6 +80,7 @@ struct Cfg {
 };
 
 using BigCfg = Cfg<256, 256, 2>;   // 2 x 4 waves of 128 x 64 (its own engine)
+using R4Cfg = Cfg<256, 256, 2, 2>; // 4 waves of 128 x 128 (the r4 engine)
 using TallCfg = Cfg<256, 32, 4>;   // 4 x 1 waves of 64 x 32  (rank-r wide outputs)
 using WideCfg = Cfg<64, 256, 1>;   // 1 x 4 waves of 64 x 64  (few-row outputs)
 
@@ -946,6 +950,341 @@ __device__ __forceinline__ void big_mainloop(const Problem& pb, int tm, int tn, 
   __syncthreads();  // loads past the end have landed; the epilogue may reuse the LDS
 }
 
+// ====================================================== 256 x 256, r4 ==
+// The 256 x 256 tile on 4 waves, one per SIMD (R4Cfg):
+//   each wave owns a 128 x 128 sub-tile, 8 x 8 v_mfma_f32_16x16x32_bf16 tiles
+//   (256 fp32 accumulators, pinned to AGPRs); k-tiles of 64, so that a
+//   K-major row of a tile is one whole 128-byte line; both operands go
+//   global -> LDS by buffer_load_dwordx4 ... lds (lane l's 16 bytes land at
+//   16 l of the instruction's 1 KB of LDS; no registers, no ds_write), two
+//   stages of 64 KB:
+//   K-major tile  [256 rows][64 k]   128-byte rows; 16-byte chunk c of row r
+//                                    at chunk c ^ r4_swz(r), r4_swz(r) =
+//                                    (r & 7) ^ ((r >> 3) & 1); an instruction
+//                                    fills 8 rows with 8 whole lines
+//   MN-major tile [64 k][256 rows]   512-byte k-rows; 32-byte unit u of k-row
+//                                    r at unit u ^ mn_swz(r) (the big engine's
+//                                    h(r)); an instruction fills 2 k-rows
+// (the swizzles are applied on the global side: each lane fetches the data
+// its LDS slot holds). K-major fragments are ds_read_b128 at one per-lane base
+// plus a constant per fragment (the swizzle depends on the row modulo 16);
+// MN-major fragments are two ds_read_b64_tr_b16 at a per-lane address per
+// fragment. Both layouts keep a fragment read within distinct bank groups.
+// Edges: each k-tile's buffer resource ends at the operand's last valid byte
+// for this tile (K-major: the last valid row; MN-major: the last k-row of the
+// K segment), so rows / k-rows past the end read zeros; per lane, K-major
+// chunks past the segment's K and MN-major columns past N get an offset past
+// every range (zeros as well). No load is ever issued out of the tensor.
+// Pipeline, per k-tile t (stage t % 2 holds t):
+//   phase 0: the 64 MFMAs of k-step 0 (fragments in registers), interleaved
+//            with the fragment reads of k-step 1; then each wave waits for its
+//            loads of k-tile t + 1 and its LDS reads, and a barrier publishes
+//            k-tile t + 1 and retires every read of stage t % 2;
+//   phase 1: the 64 MFMAs of k-step 1, interleaved with the fragment reads of
+//            k-step 0 of k-tile t + 1 and the 16 loads of k-tile t + 2 into
+//            stage t % 2.
+namespace r4 {
+constexpr int THREADS = 256;
+constexpr int BK = 64;
+constexpr int TM = 8, TN = 8;
+constexpr int WM = 128, WN = 128;
+constexpr int OP_BYTES = 256 * BK * 2;      // 32 KB per operand per stage
+constexpr int STAGE_BYTES = 2 * OP_BYTES;   // 64 KB
+constexpr int LDS_BYTES = 2 * STAGE_BYTES;  // two stages
+constexpr int LOADS = 8;                    // 1-KB loads per wave per operand per k-tile
+constexpr int EPI_BYTES = 16384;            // per wave per 128 x 64 half of its sub-tile
+static_assert(4 * 2 * EPI_BYTES <= LDS_BYTES, "epilogue LDS inside the stages");
+constexpr uint32_t kOob = 0x80000000u;  // past every resource range used here
+constexpr int64_t kRangeMax = 0x7FFFFFFF;
+constexpr int kRsrcFlags = 0x00020000;  // raw buffer, 32-bit data format
+}  // namespace r4
+
+// A workgroup barrier ordering LDS operations only (each wave's LDS reads and
+// writes complete before it, s_waitcnt lgkmcnt(0)); global loads in flight
+// stay in flight across it.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+__device__ __forceinline__ int r4_swz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+
+// readfirstlane returns int: each half goes through uint32_t before it is
+// widened (a sign-extended low half would set every high bit).
+__device__ __forceinline__ uint64_t uniform_u64(uint64_t v) {
+  const uint64_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint64_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return lo | (hi << 32);
+}
+
+// Global-load state of one operand for one wave. Wave w issues, per k-tile,
+// the 1-KB groups g = w + 4 i (i < 8) of the operand tile: rows 8 g .. 8 g +
+// 7 (K-major) or k-rows 2 g, 2 g + 1 (MN-major). The uniform fields are kept
+// in SGPRs; per k-tile the cursor adds kstep to base and subtracts it from
+// range.
+template <int L>
+struct R4Load {
+  uint64_t base;     // uniform: the operand at (tile's first row, the cursor's k)
+  int64_t range;     // uniform: bytes from base to the end of the tile's valid data
+  uint32_t kstep;    // uniform: bytes per k-tile
+  uint32_t istride;  // uniform: bytes between the wave's consecutive groups
+  uint32_t voff[2];  // per lane: byte offset for even / odd i (kOob: never loads)
+  int kb;            // per lane, K-major: k offset of the lane's chunk within a k-tile
+};
+
+// Cursor at k = kc of a segment of length klen (kc < klen).
+//   K-major: valid data ends with row (rows - 1 - row0), k = klen - 1; rows
+//            past it start at or after that end.
+//   MN-major: valid data ends with k-row (klen - 1 - kc), column rows - 1 - row0.
+template <int L>
+__device__ __forceinline__ void r4_setup(R4Load<L>& it, const Operand& op, int row0, int rows,
+                                         int kc, int klen, int wave, int lane) {
+  const int64_t ld = op.ld;
+  const char* p = reinterpret_cast<const char*>(op.ptr);
+  if constexpr (L == kKMajor) {
+    it.base = uniform_u64(reinterpret_cast<uint64_t>(p + ((int64_t)row0 * ld + kc) * 2));
+    it.range = (int64_t)uniform_u64((uint64_t)(((int64_t)(rows - row0 - 1) * ld + (klen - kc)) * 2));
+    it.kstep = 2 * r4::BK;
+    // group g = wave + 4 i: lane l holds row 8 g + l / 8, physical chunk l % 8,
+    // i.e. logical chunk (l % 8) ^ r4_swz(row); the swizzle is the same for
+    // every i (row % 16 = 8 (wave % 2) + l / 8)
+    const int r = 8 * wave + (lane >> 3);
+    const int c = (lane & 7) ^ r4_swz(r);
+    it.voff[0] = it.voff[1] = (uint32_t)(((int64_t)r * ld + 8 * c) * 2);
+    it.istride = __builtin_amdgcn_readfirstlane((uint32_t)(32 * ld * 2));
+    it.kb = 8 * c;
+  } else {
+    it.base = uniform_u64(reinterpret_cast<uint64_t>(p + ((int64_t)kc * ld + row0) * 2));
+    it.range = (int64_t)uniform_u64((uint64_t)(((int64_t)(klen - kc - 1) * ld + (rows - row0)) * 2));
+    it.kstep = __builtin_amdgcn_readfirstlane((uint32_t)(r4::BK * ld * 2));
+    // group g = wave + 4 i: lane l holds k-row kr = 2 g + l / 32 = 2 wave + 8 i +
+    // l / 32, physical 16-byte slot l % 32 of it, i.e. logical 32-byte unit
+    // (slot / 2) ^ h(kr), h(kr) = (kr & 3) | ((kr >> 3) & 1) << 2 = h0 | (i & 1) << 2
+    const int kr = 2 * wave + (lane >> 5);
+    const int slot = lane & 31;
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const int h = (kr & 3) | (e << 2);
+      const int col = 16 * ((slot >> 1) ^ h) + 8 * (slot & 1);
+      it.voff[e] = col < rows - row0 ? (uint32_t)(((int64_t)kr * ld + col) * 2) : r4::kOob;
+    }
+    it.istride = __builtin_amdgcn_readfirstlane((uint32_t)(8 * ld * 2));
+    it.kb = 0;
+  }
+}
+
+// Buffer resource and lane offsets of the cursor's k-tile (live: the k-tile
+// exists; otherwise every load reads zeros); kc / klen: the cursor's k and
+// its segment length (K-major chunks past klen read zeros).
+template <int L>
+__device__ __forceinline__ void r4_tile_rsrc(const R4Load<L>& it, int kc, int klen, bool live,
+                                             rsrc_t& rs, uint32_t (&voffs)[2]) {
+  int64_t range = it.range < r4::kRangeMax ? it.range : r4::kRangeMax;
+  range = live ? range : 0;
+  if constexpr (L == kKMajor) {
+    voffs[0] = voffs[1] = kc + it.kb < klen ? it.voff[0] : r4::kOob;
+  } else {
+    voffs[0] = it.voff[0];
+    voffs[1] = it.voff[1];
+  }
+  const uint64_t b = uniform_u64(it.base);
+  rs[0] = (uint32_t)b;
+  rs[1] = (uint32_t)(b >> 32) & 0xFFFFu;
+  rs[2] = (uint32_t)__builtin_amdgcn_readfirstlane((int)range);
+  rs[3] = (uint32_t)r4::kRsrcFlags;
+}
+
+// Per-lane fragment read offsets of a wave sub-tile starting at row wbase.
+// K-major: one per k-step (fragment f adds 2048 f); MN-major: one per
+// fragment (the second half adds 4 k-rows, k-step 1 adds 32 k-rows).
+template <int L>
+struct R4Frag {
+  uint32_t a[L == kKMajor ? 2 : 8];
+};
+
+template <int L>
+__device__ __forceinline__ void r4_frag_setup(R4Frag<L>& fa, int wbase, int lane) {
+  if constexpr (L == kKMajor) {
+    const int r = lane & 15, g = lane >> 4;
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+      fa.a[s] = (uint32_t)((wbase + r) * 128 + (((4 * s + g) ^ r4_swz(r)) << 4));
+  } else {
+    // lane 16 G + i: k-row 8 G + i / 4, columns wbase + 16 f + 4 (i % 4) .. + 3
+    const int G = lane >> 4, i = lane & 15;
+    const int h = ((i >> 2) & 3) | ((G & 1) << 2);
+    const uint32_t b = (uint32_t)((8 * G + (i >> 2)) * 512 + 8 * (i & 3));
+#pragma unroll
+    for (int f = 0; f < 8; ++f) fa.a[f] = b + (uint32_t)((((wbase >> 4) + f) ^ h) << 5);
+  }
+}
+
+// Fragment f of k-step s (an MN-major fragment is two transposing reads,
+// combined into a fresh register).
+template <int L>
+__device__ __forceinline__ bf16x8_t r4_read_frag(const char* op, const R4Frag<L>& fa, int s, int f) {
+  if constexpr (L == kKMajor) {
+    return *reinterpret_cast<const bf16x8_t*>(op + fa.a[s] + 2048 * f);
+  } else {
+    typedef __attribute__((address_space(3))) i16x4_t* lp;
+    const char* p = op + fa.a[f] + 16384 * s;
+    const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lp)(p));
+    const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lp)(p + 2048));
+    typedef short i16x8_t __attribute__((ext_vector_type(8)));
+    const i16x8_t w = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+    return __builtin_bit_cast(bf16x8_t, w);
+  }
+}
+
+// acc += a b on the matrix cores, with acc pinned to AGPRs and the operands
+// to VGPRs (left to itself the register allocator splits the 256
+// accumulators between AGPRs and VGPRs and copies them every k-step).
+__device__ __forceinline__ void r4_mfma(f32x4_t& acc, const bf16x8_t& a, const bf16x8_t& b) {
+  asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+}
+
+struct R4Frags {
+  bf16x8_t a[r4::TM], b[r4::TN];
+};
+
+// Main loop of the r4 engine; lds holds two stages (A tile, then B tile).
+// Wave w computes rows 128 (w >> 1) .. + 127 and columns 128 (w & 1) .. +
+// 127 of the block tile; acc[h][i][j] is MFMA tile (i, 4 h + j).
+template <int LA, int LB>
+__device__ __forceinline__ void r4_mainloop(const Problem& pb, int tm, int tn, int split, char* lds,
+                                            f32x4_t (&acc)[2][r4::TM][4]) {
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = (wave >> 1) * r4::WM;
+  const int wn = (wave & 1) * r4::WN;
+  const int m0 = tm * 256;
+  const int n0 = tn * 256;
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int i = 0; i < r4::TM; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[h][i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  int nk, k0 = 0;
+  if (pb.ksplit > 1) {  // splits are counted in 64-wide k-tiles
+    const int total = (pb.seg[0].k_len + kBK - 1) / kBK;
+    const int first = split * pb.kps;
+    nk = total - first < pb.kps ? total - first : pb.kps;
+    k0 = first * kBK;
+  } else {
+    nk = 0;
+    for (int s = 0; s < pb.nseg; ++s) nk += (pb.seg[s].k_len + r4::BK - 1) / r4::BK;
+  }
+  if (nk <= 0) return;  // block-uniform
+
+  // Load cursor: the next k-tile to load; `loaded` k-tiles have been issued.
+  int seg = 0, kc = k0, klen = pb.seg[0].k_len, loaded = 0;
+  R4Load<LA> ia;
+  R4Load<LB> ib;
+  r4_setup<LA>(ia, pb.seg[0].a, m0, pb.M, kc, klen, wave, lane);
+  r4_setup<LB>(ib, pb.seg[0].b, n0, pb.N, kc, klen, wave, lane);
+  R4Frag<LA> fa;
+  R4Frag<LB> fb;
+  r4_frag_setup<LA>(fa, wm, lane);
+  r4_frag_setup<LB>(fb, wn, lane);
+
+  rsrc_t rsa, rsb;
+  uint32_t va[2], vb[2], sa, sb;
+  // Resources of the cursor's k-tile (with its segment's group stride: the
+  // cursor may move to the next segment before the loads are issued), then
+  // advance the cursor.
+  auto next_tile = [&]() __attribute__((always_inline)) {
+    const bool live = loaded < nk;
+    r4_tile_rsrc<LA>(ia, kc, klen, live, rsa, va);
+    r4_tile_rsrc<LB>(ib, kc, klen, live, rsb, vb);
+    sa = ia.istride;
+    sb = ib.istride;
+    ++loaded;
+    if (loaded < nk) {
+      kc += r4::BK;
+      if (kc >= klen) {
+        ++seg;
+        kc = 0;
+        klen = pb.seg[seg].k_len;
+        r4_setup<LA>(ia, pb.seg[seg].a, m0, pb.M, 0, klen, wave, lane);
+        r4_setup<LB>(ib, pb.seg[seg].b, n0, pb.N, 0, klen, wave, lane);
+      } else {
+        ia.base += ia.kstep;
+        ia.range -= ia.kstep;
+        ib.base += ib.kstep;
+        ib.range -= ib.kstep;
+      }
+    }
+  };
+  // Load w (0 .. 15; A for w < 8) of the current resources into stage `stage`.
+  auto load = [&](char* stage, int w) __attribute__((always_inline)) {
+    const int i = w & 7;
+    char* dst = stage + (w < 8 ? 0 : r4::OP_BYTES) + (wave + 4 * i) * 1024;
+    if (w < 8)
+      buf_load_lds(rsa, va[i & 1] + (uint32_t)i * sa, dst);
+    else
+      buf_load_lds(rsb, vb[i & 1] + (uint32_t)i * sb, dst);
+  };
+
+  R4Frags f0, f1;
+  // Prologue: k-tile 0 into stage 0 and k-tile 1 into stage 1; k-tile 0
+  // published, its k-step 0 fragments read.
+  next_tile();
+#pragma unroll
+  for (int w = 0; w < 2 * r4::LOADS; ++w) load(lds, w);
+  next_tile();
+#pragma unroll
+  for (int w = 0; w < 2 * r4::LOADS; ++w) load(lds + r4::STAGE_BYTES, w);
+  __builtin_amdgcn_s_waitcnt(big::wait_vm(2 * r4::LOADS));  // this wave's k-tile 0 landed
+  lds_barrier();
+#pragma unroll
+  for (int j = 0; j < r4::TN; ++j) f0.b[j] = r4_read_frag<LB>(lds + r4::OP_BYTES, fb, 0, j);
+#pragma unroll
+  for (int i = 0; i < r4::TM; ++i) f0.a[i] = r4_read_frag<LA>(lds, fa, 0, i);
+
+  // One phase: the 64 MFMAs of fragment set fc, with the reads of the next
+  // k-step (k-step NS of stage `src`) into fn, interleaved; in phase 1 also
+  // the loads of the cursor's k-tile into stage `dst`.
+  auto phase = [&](auto pc, R4Frags& fc, R4Frags& fn, const char* src, char* dst)
+                   __attribute__((always_inline)) {
+    constexpr int P = decltype(pc)::value;
+    constexpr int NS = P ^ 1;
+    static_for<r4::TM * r4::TN>([&](auto qc) {
+      constexpr int q = decltype(qc)::value;
+      constexpr int i = q / r4::TN, j = q % r4::TN;
+      // next k-step: B fragments at slots 1, 5, .., 29, A at 33, 37, .., 61
+      if constexpr ((q & 3) == 1 && q < 32) fn.b[q >> 2] = r4_read_frag<LB>(src + r4::OP_BYTES, fb, NS, q >> 2);
+      if constexpr ((q & 3) == 1 && q >= 32) fn.a[(q - 32) >> 2] = r4_read_frag<LA>(src, fa, NS, (q - 32) >> 2);
+      if constexpr (P == 1 && (q & 3) == 3) load(dst, q >> 2);
+      r4_mfma(acc[j >> 2][i][j & 3], fc.a[i], fc.b[j]);
+      __builtin_amdgcn_sched_barrier(0);
+    });
+  };
+  for (int t = 0; t < nk; ++t) {
+    const int cur = (t & 1) * r4::STAGE_BYTES;
+    char* cs = lds + cur;
+    char* ns = lds + (cur ^ r4::STAGE_BYTES);
+    phase(std::integral_constant<int, 0>{}, f0, f1, cs, ns);
+    // this wave's loads of k-tile t + 1 have landed (no other vector memory
+    // operation is in flight); the barrier publishes them
+    __builtin_amdgcn_s_waitcnt(big::kWaitVm0);
+    lds_barrier();
+    next_tile();  // resources of k-tile t + 2, loaded into stage cs during phase 1
+    phase(std::integral_constant<int, 1>{}, f1, f0, ns, cs);
+  }
+  // the epilogue reads the accumulators: wait for the last MFMAs (the
+  // asm statements carry no hazard information for the compiler), and for
+  // the loads past the end (they write LDS the epilogue reuses)
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(big::kWaitVm0);
+  lds_barrier();  // every wave's reads are done; the epilogue may reuse the LDS
+}
+
 // Per-element view of a wave's accumulators: f(m, n, value) for the
 // elements of MFMA-tile row i (for_each_acc_row) or of the whole wave
 // sub-tile at (m0, n0) (for_each_acc), in either MFMA layout:
@@ -1080,7 +1419,18 @@ __global__ __launch_bounds__(C::THREADS) void gemm_kernel(const Problem pb, cons
   if (!tile_coords(pb, tm, tn, split)) return;
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
-  if constexpr (C::BM == 256 && C::BN == 256) {
+  if constexpr (C::BM == 256 && C::BN == 256 && C::ENGINE == 2) {
+    __shared__ __attribute__((aligned(16))) char lds[r4::LDS_BYTES];
+    f32x4_t acc[2][r4::TM][4];
+    r4_mainloop<LA, LB>(pb, tm, tn, split, lds, acc);
+    // each wave gets 2 x 16 KB of LDS of its own for the two 128 x 64 halves
+    // of its sub-tile
+    const int w = __builtin_amdgcn_readfirstlane(wave);
+    char* wl = lds + w * 2 * r4::EPI_BYTES;
+    const int em = tm * 256 + (w >> 1) * r4::WM, en = tn * 256 + (w & 1) * r4::WN;
+    epi(acc[0], em, en, tid & 63, wl, split);
+    epi(acc[1], em, en + 64, tid & 63, wl + r4::EPI_BYTES, split);
+  } else if constexpr (C::BM == 256 && C::BN == 256) {
     __shared__ __attribute__((aligned(16))) char lds[big::STAGES * big::STAGE_BYTES];
     f32x4_t acc[big::TM][big::TN];
     big_mainloop<LA, LB>(pb, tm, tn, split, lds, acc);
@@ -1302,18 +1652,25 @@ inline int make_problem(Problem& pb, int M, int N, int nseg, const Segment* segs
   return ML_OK;
 }
 
-// Big-tile launch with the store epilogue.
-template <typename TC>
+// 256 x 256 launch with the store epilogue (engine of CF: BigCfg or R4Cfg).
+template <typename TC, class CF = BigCfg>
 inline int launch_store(const Problem& pb, int la, int lb, void* C, int64_t ldc, float alpha,
                         float beta, hipStream_t st) {
   EpiStore<TC> epi{static_cast<TC*>(C), ldc, pb.M, pb.N, alpha, beta};
   const dim3 grid(grid_blocks(pb));
 #define ML_G(LA, LB) \
-  gemm_kernel<BigCfg, LA, LB, EpiStore<TC>><<<grid, BigCfg::THREADS, 0, st>>>(pb, epi)
-  if (la == kKMajor && lb == kKMajor) ML_G(kKMajor, kKMajor);
-  else if (la == kKMajor && lb == kMNMajor) ML_G(kKMajor, kMNMajor);
-  else if (la == kMNMajor && lb == kKMajor) ML_G(kMNMajor, kKMajor);
-  else ML_G(kMNMajor, kMNMajor);
+  gemm_kernel<CF, LA, LB, EpiStore<TC>><<<grid, CF::THREADS, 0, st>>>(pb, epi)
+  if (la == kKMajor) {
+    if (lb == kKMajor) ML_G(kKMajor, kKMajor);
+    else ML_G(kKMajor, kMNMajor);
+  } else if constexpr (CF::ENGINE == 2) {
+    // r4 is used where A is K-major (its MN-major A path is not instantiated)
+    set_error("gemm: the r4 engine takes a K-major A");
+    return ML_ERR_INVALID;
+  } else {
+    if (lb == kKMajor) ML_G(kMNMajor, kKMajor);
+    else ML_G(kMNMajor, kMNMajor);
+  }
 #undef ML_G
   ML_LAUNCH_CHECK();
   return ML_OK;

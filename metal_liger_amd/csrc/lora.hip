@@ -622,7 +622,7 @@ static int adapters_bwd(const char* what, int nadp, const void* X, int64_t n_tok
   Problem pb;
   rc = make_problem<BigCfg>(pb, N, IN, nadp + 1, segs, kKMajor, kMNMajor, 0);
   if (rc) return rc;
-  return launch_store<bf16>(pb, kKMajor, kMNMajor, dX, IN, 1.0f, 0.0f, st);
+  return launch_store<bf16, R4Cfg>(pb, kKMajor, kMNMajor, dX, IN, 1.0f, 0.0f, st);
 }
 
 extern "C" size_t ml_lora_qkv_bwd_workspace_bytes(int64_t n_tokens, int64_t in_features,
@@ -766,7 +766,7 @@ extern "C" int ml_lora_mlp_bwd(const void* X, int64_t n_tokens, int64_t hidden,
     Problem pb;
     rc = make_problem<BigCfg>(pb, N, I, 2, segs, kKMajor, kMNMajor, 0);
     if (rc) return rc;
-    rc = launch_store<bf16>(pb, kKMajor, kMNMajor, dgate, I, 1.f, 0.f, st);
+    rc = launch_store<bf16, R4Cfg>(pb, kKMajor, kMNMajor, dgate, I, 1.f, 0.f, st);
     if (rc) return rc;
     rc = ml_swiglu_bwd(gate, up, dgate, dgate, dup, (int64_t)N * I, ML_BF16, st);
     if (rc) return rc;
@@ -810,5 +810,5 @@ extern "C" int ml_lora_mlp_bwd(const void* X, int64_t n_tokens, int64_t hidden,
   Problem pb;
   rc = make_problem<BigCfg>(pb, N, H, 3, segs, kKMajor, kMNMajor, 0);
   if (rc) return rc;
-  return launch_store<bf16>(pb, kKMajor, kMNMajor, dX, H, 1.0f, 0.0f, st);
+  return launch_store<bf16, R4Cfg>(pb, kKMajor, kMNMajor, dX, H, 1.0f, 0.0f, st);
 }
