@@ -233,7 +233,7 @@ __global__ __launch_bounds__(256) void dlogit_pass_kernel(
       const int j = j0 + u * 256;
       if (j < vpr) {
         f[u] = exp_f(pm[(j * 8) / kColBlock] - lse_r) * sc;
-        load_n<bf16, 8>(er + j * 8, e[u]);
+        load_n_nt<bf16, 8>(er + j * 8, e[u]);
       }
     }
 #pragma unroll
@@ -248,7 +248,7 @@ __global__ __launch_bounds__(256) void dlogit_pass_kernel(
         for (int k = 0; k < 8; ++k)
           if (k == (int)d) e[u][k] = e[u][k] - sc;
       }
-      store_n<bf16, 8>(er + j * 8, e[u]);
+      store_n_nt<bf16, 8>(er + j * 8, e[u]);
     }
   }
 }
@@ -264,10 +264,10 @@ __global__ __launch_bounds__(256) void scale_kernel(T* __restrict__ x, int64_t n
   const int64_t nv = n / V;
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < nv; i += (int64_t)gridDim.x * 256) {
     float v[V];
-    load_n<T, V>(x + i * V, v);
+    load_n_nt<T, V>(x + i * V, v);
 #pragma unroll
     for (int k = 0; k < V; ++k) v[k] *= s;
-    store_n<T, V>(x + i * V, v);
+    store_n_nt<T, V>(x + i * V, v);
   }
   for (int64_t i = nv * V + (int64_t)blockIdx.x * 256 + threadIdx.x; i < n;
        i += (int64_t)gridDim.x * 256)

@@ -145,12 +145,12 @@ __global__ __launch_bounds__(kQknThreads) void qkn_rope_kernel(const QknArgs a) 
     for (int u = 0; u < HPI; ++u) {
       const int64_t hh = std::min(h0 + u, H - 1);
       const TX* xp = xbase + (xo + hh * t.xh);
-      xl[u] = ldp<TX, V>(xp);
-      xh[u] = ldp<TX, V>(xp + HALF);
+      xl[u] = load_pack_nt<TX, V>(xp);
+      xh[u] = load_pack_nt<TX, V>(xp + HALF);
       if constexpr (BWD) {
         const TX* dp = dbase + (dox + hh * t.dh);
-        dl[u] = ldp<TX, V>(dp);
-        dh[u] = ldp<TX, V>(dp + HALF);
+        dl[u] = load_pack_nt<TX, V>(dp);
+        dh[u] = load_pack_nt<TX, V>(dp + HALF);
       }
     }
     float c_lo[V], c_hi[V], s_lo[V], s_hi[V];
@@ -216,8 +216,8 @@ __global__ __launch_bounds__(kQknThreads) void qkn_rope_kernel(const QknArgs a) 
       }
       if (store) {
         TX* yp = obase + (oo + (int64_t)hh * t.oh);
-        store_n<TX, V>(yp, o_lo);
-        store_n<TX, V>(yp + HALF, o_hi);
+        store_n_nt<TX, V>(yp, o_lo);
+        store_n_nt<TX, V>(yp + HALF, o_hi);
       }
     }
   }

@@ -70,19 +70,19 @@ __global__ __launch_bounds__(64 * kFwdWaves) void rms_fwd_reg(
   // load, so all ITERS loads are in flight together) and are zeroed after.
   float v[ITERS][VEC];
 #pragma unroll
-  for (int it = 0; it < ITERS; ++it) load_n<TX, VEC>(xr + clamp_col(it, lane, cols, VEC), v[it]);
+  for (int it = 0; it < ITERS; ++it) load_n_nt<TX, VEC>(xr + clamp_col(it, lane, cols, VEC), v[it]);
   if constexpr (ADD) {
     const TX* rr = res + row * ldr;
     float rv[ITERS][VEC];
 #pragma unroll
-    for (int it = 0; it < ITERS; ++it) load_n<TX, VEC>(rr + clamp_col(it, lane, cols, VEC), rv[it]);
+    for (int it = 0; it < ITERS; ++it) load_n_nt<TX, VEC>(rr + clamp_col(it, lane, cols, VEC), rv[it]);
     TX* sr = sum + row * lds;
 #pragma unroll
     for (int it = 0; it < ITERS; ++it) {
 #pragma unroll
       for (int e = 0; e < VEC; ++e) v[it][e] = to_f32(from_f32<TX>(v[it][e] + rv[it][e]));
       const int c = (it * 64 + lane) * VEC;
-      if (c < cols) store_n<TX, VEC>(sr + c, v[it]);
+      if (c < cols) store_n_nt<TX, VEC>(sr + c, v[it]);
     }
   }
 #pragma unroll
@@ -185,10 +185,10 @@ __global__ __launch_bounds__(64 * kBwdWaves) void rms_bwd_reg(
 #pragma unroll
     for (int it = 0; it < ITERS; ++it) {
       const int c = clamp_col(it, lane, cols, VEC);
-      load_n<TX, VEC>(xr + c, xv[it]);
-      load_n<TX, VEC>(gr + c, gv[it]);
+      load_n_nt<TX, VEC>(xr + c, xv[it]);
+      load_n_nt<TX, VEC>(gr + c, gv[it]);
       // (the tail chunk reads the last valid chunk; its result is not stored)
-      if constexpr (HAS_DRES) load_n<TX, VEC>(dres + row * ldd + c, dv[it]);
+      if constexpr (HAS_DRES) load_n_nt<TX, VEC>(dres + row * ldd + c, dv[it]);
     }
 #pragma unroll
     for (int it = 0; it < ITERS; ++it) {

@@ -142,8 +142,8 @@ __global__ __launch_bounds__(kThreads) void rope_kernel(const RopeArgs a) {
       const RopeTensor& tt = a.t[ti];
       const int64_t h = vh - (ti ? Hq : 0);
       const TX* xp = static_cast<const TX*>(tt.in) + (b * (IDX)tt.sb + (IDX)h * (IDX)tt.sh + s * (IDX)tt.ss + j0);
-      raw_lo[t] = *reinterpret_cast<const Pack<TX, VEC>*>(xp);
-      raw_hi[t] = *reinterpret_cast<const Pack<TX, VEC>*>(xp + a.half);
+      raw_lo[t] = load_pack_nt<TX, VEC>(xp);
+      raw_hi[t] = load_pack_nt<TX, VEC>(xp + a.half);
     }
   }
 
