@@ -464,7 +464,10 @@ def bench_train_step(dev, steps=5, warmup=2):
 
     def step():
         opt.zero_grad(set_to_none=True)
-        out = model(input_ids=ids, labels=ids)
+        # use_cache=False: a training forward keeps no KV cache (with the
+        # config's default the model would copy every layer's keys and values
+        # into one, 2 x 33.5 MB per layer per step, for nothing)
+        out = model(input_ids=ids, labels=ids, use_cache=False)
         if out.logits is not None:
             raise RuntimeError("train step: the fused loss hook did not run")
         loss = out.loss
@@ -489,7 +492,7 @@ def bench_train_step(dev, steps=5, warmup=2):
     return {"layers": qwen_tiny.TRAIN_LAYERS, "tokens": n_tok, "ms_per_step": round(dt * 1e3, 2),
             "tokens_per_s": round(n_tok / dt, 1), "loss_first": round(first, 4),
             "loss_last": round(last, 4), "steps": steps, "warmup": warmup,
-            "includes": "fwd + FLCE loss (model(input_ids, labels=input_ids)) + bwd + AdamW on LoRA params",
+            "includes": "fwd + FLCE loss (model(input_ids, labels=input_ids, use_cache=False)) + bwd + AdamW on LoRA params",
             "attention": "torch SDPA (flash / mem-efficient)"}
 
 

@@ -281,42 +281,46 @@ def _(x2, w, xa, sb):
     return x2.new_empty((x2.shape[0], w.shape[0]), dtype=torch.bfloat16)
 
 
+# The LoRA backwards return (dX, grads): grads is one fp32 buffer holding the
+# adapter gradients as laid out by hip_ops.grad_layout (hip_ops.grad_views
+# splits it), so that the caller can cast them to the parameters' dtype in
+# one launch.
+def _grads_fake(x2, shapes):
+    return x2.new_empty((max(hip_ops.grad_layout(shapes)[1], 1),), dtype=torch.float32)
+
+
 @torch.library.custom_op(f"{NS}::lora_qkv_bwd", mutates_args=(), device_types=_DEV)
 def lora_qkv_bwd(x2: Tensor, dys: List[Tensor], ws: List[Tensor], a_stack: Tensor,
                  bs: List[Tensor], scales: List[float], xa: Tensor,
-                 rank: int) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
-    dX, dA, dBs = hip_ops.lora_qkv_bwd(x2, dys, ws, a_stack, bs, scales, xa, rank)
-    return (dX, dA, *dBs)
+                 rank: int) -> tuple[Tensor, Tensor]:
+    return hip_ops.lora_qkv_bwd(x2, dys, ws, a_stack, bs, scales, xa, rank)
 
 
 @lora_qkv_bwd.register_fake
 def _(x2, dys, ws, a_stack, bs, scales, xa, rank):
     N, IN = x2.shape
-    f32 = torch.float32
-    return (x2.new_empty((N, IN), dtype=torch.bfloat16),
-            x2.new_empty((3 * rank, IN), dtype=f32),
-            *(x2.new_empty((d.shape[1], rank), dtype=f32) for d in dys))
+    shapes = hip_ops.lora_qkv_grad_shapes(IN, [d.shape[1] for d in dys], rank)
+    return x2.new_empty((N, IN), dtype=torch.bfloat16), _grads_fake(x2, shapes)
 
 
 @torch.library.custom_op(f"{NS}::lora_linear_bwd", mutates_args=(), device_types=_DEV)
 def lora_linear_bwd(x2: Tensor, dy: Tensor, w: Tensor, a: Tensor, b: Tensor, scale: float,
-                    xa: Tensor, rank: int) -> tuple[Tensor, Tensor, Tensor]:
+                    xa: Tensor, rank: int) -> tuple[Tensor, Tensor]:
     return hip_ops.lora_linear_bwd(x2, dy, w, a, b, scale, xa, rank)
 
 
 @lora_linear_bwd.register_fake
 def _(x2, dy, w, a, b, scale, xa, rank):
     N, IN = x2.shape
-    f32 = torch.float32
-    return (x2.new_empty((N, IN), dtype=torch.bfloat16), x2.new_empty((rank, IN), dtype=f32),
-            x2.new_empty((dy.shape[1], rank), dtype=f32))
+    shapes = hip_ops.lora_linear_grad_shapes(IN, dy.shape[1], rank)
+    return x2.new_empty((N, IN), dtype=torch.bfloat16), _grads_fake(x2, shapes)
 
 
 @torch.library.custom_op(f"{NS}::lora_mlp_bwd", mutates_args=(), device_types=_DEV)
 def lora_mlp_bwd(x2: Tensor, gate: Tensor, up: Tensor, h: Tensor, dy: Tensor, wg: Tensor,
                  wu: Tensor, wd: Tensor, a_gu: Tensor, a_d: Tensor, bg: Tensor, bu: Tensor,
                  bd: Tensor, scales: List[float], xa_gu: Tensor, ha_d: Tensor,
-                 rank: int) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
+                 rank: int) -> tuple[Tensor, Tensor]:
     return hip_ops.lora_mlp_bwd(x2, gate, up, h, dy, wg, wu, wd, a_gu, a_d, bg, bu, bd, scales,
                                 xa_gu, ha_d, rank)
 
@@ -324,8 +328,5 @@ def lora_mlp_bwd(x2: Tensor, gate: Tensor, up: Tensor, h: Tensor, dy: Tensor, wg
 @lora_mlp_bwd.register_fake
 def _(x2, gate, up, h, dy, wg, wu, wd, a_gu, a_d, bg, bu, bd, scales, xa_gu, ha_d, rank):
     N, H = x2.shape
-    I = gate.shape[1]  # noqa: E741
-    f32 = torch.float32
-    return (x2.new_empty((N, H), dtype=torch.bfloat16), x2.new_empty((2 * rank, H), dtype=f32),
-            x2.new_empty((rank, I), dtype=f32), x2.new_empty((I, rank), dtype=f32),
-            x2.new_empty((I, rank), dtype=f32), x2.new_empty((H, rank), dtype=f32))
+    shapes = hip_ops.lora_mlp_grad_shapes(H, gate.shape[1], rank)
+    return x2.new_empty((N, H), dtype=torch.bfloat16), _grads_fake(x2, shapes)

@@ -811,8 +811,47 @@ def lora_linear_out(x2: torch.Tensor, w: torch.Tensor, xa: torch.Tensor,
     return out
 
 
+# The adapter gradients of one LoRA backward call live in one fp32 buffer:
+# each gradient starts on a 256-byte boundary, in the order the call lists
+# them. A caller that wants them in the parameters' dtype converts the buffer
+# with one cast instead of one per gradient.
+def grad_layout(shapes):
+    """(offsets, total elements) of gradients of the given shapes in one buffer."""
+    offs, total = [], 0
+    for s in shapes:
+        offs.append(total)
+        n = 1
+        for d in s:
+            n *= int(d)
+        total += -(-n // 64) * 64
+    return offs, total
+
+
+def grad_views(flat, shapes):
+    """The gradients (views) in a buffer laid out by grad_layout."""
+    offs, _ = grad_layout(shapes)
+    out = []
+    for o, s in zip(offs, shapes):
+        n = 1
+        for d in s:
+            n *= int(d)
+        out.append(flat[o:o + n].view(*s))
+    return out
+
+
+def _grad_buffer(shapes, dev):
+    _, total = grad_layout(shapes)
+    flat = torch.empty(max(total, 1), dtype=torch.float32, device=dev)
+    return flat, grad_views(flat, shapes)
+
+
+def lora_qkv_grad_shapes(IN, outs, rank):
+    return [(3 * rank, IN), *((int(o), rank) for o in outs)]
+
+
 def lora_qkv_bwd(x2, dys, ws_, a_stack, bs, scales, xa, rank):
-    """Returns (dX bf16 [N, in], dA fp32 [3r, in], [dB_i fp32 [out_i, r]])."""
+    """Returns (dX bf16 [N, in], grads fp32): grads holds dA [3r, in] and
+    dB_i [out_i, r] as laid out by grad_layout(lora_qkv_grad_shapes(...))."""
     ensure_rocm_device(x2, *dys, *ws_, a_stack, *bs, xa)
     x2, a_stack, xa = _dense16(x2, a_stack, xa)
     dys, ws_, bs = [list(_dense16(*t, None))[:-1] for t in (dys, ws_, bs)]
@@ -820,10 +859,9 @@ def lora_qkv_bwd(x2, dys, ws_, a_stack, bs, scales, xa, rank):
     outs = [int(d.shape[1]) for d in dys]
     dev = x2.device
     dX = torch.empty(N, IN, dtype=torch.bfloat16, device=dev)
-    dA = torch.empty(3 * rank, IN, dtype=torch.float32, device=dev)
-    dBs = [torch.empty(o, rank, dtype=torch.float32, device=dev) for o in outs]
+    flat, (dA, *dBs) = _grad_buffer(lora_qkv_grad_shapes(IN, outs, rank), dev)
     if N == 0:   # no tokens: the adapter gradients are empty sums
-        return dX, dA.zero_(), [d.zero_() for d in dBs]
+        return dX, flat.zero_()
     wsb = _hip.query("ml_lora_qkv_bwd_workspace_bytes", N, IN, geom(outs), rank)
     ws = torch.empty(max(wsb, 16), dtype=torch.uint8, device=dev)
     call(
@@ -832,48 +870,51 @@ def lora_qkv_bwd(x2, dys, ws_, a_stack, bs, scales, xa, rank):
         _hip.floats(scales), ptr(xa), rank, ptr(dX), ptr(dA),
         _hip.ptrs([b.data_ptr() for b in dBs]), ptr(ws), ws.numel(), stream_of(x2),
     )
-    return dX, dA, dBs
+    return dX, flat
+
+
+def lora_linear_grad_shapes(IN, OUT, rank):
+    return [(rank, IN), (int(OUT), rank)]
 
 
 def lora_linear_bwd(x2, dy, w, a, b, scale, xa, rank):
-    """One LoRA projection's backward: (dX bf16 [N, in], dA fp32 [r, in],
-    dB fp32 [out, r])."""
+    """One LoRA projection's backward: (dX bf16 [N, in], grads fp32 holding
+    dA [r, in] and dB [out, r] as laid out by grad_layout)."""
     ensure_rocm_device(x2, dy, w, a, b, xa)
     x2, dy, w, a, b, xa = _dense16(x2, dy, w, a, b, xa)
     N, IN = x2.shape
     OUT = int(dy.shape[1])
     dev = x2.device
     dX = torch.empty(N, IN, dtype=torch.bfloat16, device=dev)
-    dA = torch.empty(rank, IN, dtype=torch.float32, device=dev)
-    dB = torch.empty(OUT, rank, dtype=torch.float32, device=dev)
+    flat, (dA, dB) = _grad_buffer(lora_linear_grad_shapes(IN, OUT, rank), dev)
     if N == 0:
-        return dX, dA.zero_(), dB.zero_()
+        return dX, flat.zero_()
     wsb = _hip.query("ml_lora_linear_bwd_workspace_bytes", N, IN, OUT, rank)
     ws = torch.empty(max(wsb, 16), dtype=torch.uint8, device=dev)
     call(
         "ml_lora_linear_bwd", ptr(x2), N, IN, ptr(dy), OUT, ptr(w), ptr(a), ptr(b), float(scale),
         ptr(xa), rank, ptr(dX), ptr(dA), ptr(dB), ptr(ws), ws.numel(), stream_of(x2),
     )
-    return dX, dA, dB
+    return dX, flat
+
+
+def lora_mlp_grad_shapes(H, I, rank):
+    return [(2 * rank, H), (rank, int(I)), (int(I), rank), (int(I), rank), (H, rank)]
 
 
 def lora_mlp_bwd(x2, gate, up, h, dy, wg, wu, wd, a_gu, a_d, bg, bu, bd, scales, xa_gu, ha_d, rank):
-    """Returns (dX, dA_GU [2r, H], dA_D [r, I], dB_G [I, r], dB_U [I, r], dB_D [H, r])."""
+    """Returns (dX, grads fp32) with grads holding dA_GU [2r, H], dA_D [r, I],
+    dB_G [I, r], dB_U [I, r], dB_D [H, r] as laid out by grad_layout."""
     ensure_rocm_device(x2, gate, up, h, dy, wg, wu, wd, a_gu, a_d, bg, bu, bd, xa_gu, ha_d)
     (x2, gate, up, h, dy, wg, wu, wd, a_gu, a_d, bg, bu, bd, xa_gu, ha_d) = _dense16(
         x2, gate, up, h, dy, wg, wu, wd, a_gu, a_d, bg, bu, bd, xa_gu, ha_d)
     N, H = x2.shape
     I = gate.shape[1]
     dev = x2.device
-    f32 = torch.float32
     dX = torch.empty(N, H, dtype=torch.bfloat16, device=dev)
-    dA_GU = torch.empty(2 * rank, H, dtype=f32, device=dev)
-    dA_D = torch.empty(rank, I, dtype=f32, device=dev)
-    dB_G = torch.empty(I, rank, dtype=f32, device=dev)
-    dB_U = torch.empty(I, rank, dtype=f32, device=dev)
-    dB_D = torch.empty(H, rank, dtype=f32, device=dev)
+    flat, (dA_GU, dA_D, dB_G, dB_U, dB_D) = _grad_buffer(lora_mlp_grad_shapes(H, I, rank), dev)
     if N == 0:
-        return (dX, dA_GU.zero_(), dA_D.zero_(), dB_G.zero_(), dB_U.zero_(), dB_D.zero_())
+        return dX, flat.zero_()
     wsb = _hip.query("ml_lora_mlp_bwd_workspace_bytes", N, H, I, rank)
     ws = torch.empty(max(wsb, 16), dtype=torch.uint8, device=dev)
     call(
@@ -882,4 +923,4 @@ def lora_mlp_bwd(x2, gate, up, h, dy, wg, wu, wd, a_gu, a_d, bg, bu, bd, scales,
         ptr(ha_d), rank, ptr(dX), ptr(dA_GU), ptr(dA_D), ptr(dB_G), ptr(dB_U), ptr(dB_D), ptr(ws),
         ws.numel(), stream_of(x2),
     )
-    return dX, dA_GU, dA_D, dB_G, dB_U, dB_D
+    return dX, flat

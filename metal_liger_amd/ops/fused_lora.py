@@ -116,6 +116,16 @@ def _pad_b(B: torch.Tensor, rp: int, scale: float = 1.0) -> torch.Tensor:
     return b.contiguous()
 
 
+def _adapter_grads(flat, shapes, dtypes):
+    """The adapter gradients of one fused backward call, from the fp32
+    buffer it returns (hip_ops.grad_layout): cast once to the adapters' dtype
+    when they share one, instead of autograd casting each gradient in a
+    launch of its own."""
+    if len(set(dtypes)) == 1 and dtypes[0] != flat.dtype:
+        flat = flat.to(dtypes[0])
+    return hip_ops.grad_views(flat, shapes)
+
+
 def _lora_linear(X: torch.Tensor, W: torch.Tensor,
                  A: torch.Tensor, B: torch.Tensor, scaling: float) -> torch.Tensor:
     """X W^T + s (X A^T) B^T (ops/fused_lora.py:69-82) on the MFMA engine
@@ -209,8 +219,10 @@ class _LoRA_QKV(torch.autograd.Function):
         r, rp = ctx.rank, ctx.rank_p
         shape = ctx.orig_shape
         dys = [hip_ops._bf16_rows(d.reshape(-1, d.shape[-1])) for d in (dQ, dK, dV)]
-        dX, dA, *dBs = cops.lora_qkv_bwd(Xf, dys, [QW, KW, VW], a_stack, [QB, KB, VB],
-                                         ctx.scales, xa, rp)
+        dX, flat = cops.lora_qkv_bwd(Xf, dys, [QW, KW, VW], a_stack, [QB, KB, VB],
+                                     ctx.scales, xa, rp)
+        shapes = hip_ops.lora_qkv_grad_shapes(Xf.shape[1], [d.shape[1] for d in dys], rp)
+        dA, *dBs = _adapter_grads(flat, shapes, [t for pair in ctx.param_dtypes for t in pair])
         grads = []
         for i in range(3):
             dAi = dA[i * rp:i * rp + r]
@@ -265,6 +277,7 @@ class _LoRA_MLP(torch.autograd.Function):
         out = cops.lora_linear_out(h, DWc, ha_d, BD * scales[2])
         ctx.save_for_backward(Xf, gate, up, h, xa_gu, ha_d, a_gu, a_d, GWc, UWc, DWc, BG, BU, BD)
         ctx.scales = scales
+        ctx.param_dtypes = [t.dtype for t in (GA, UA, DA, GB, UB, DB)]
         ctx.rank, ctx.rank_p = r, rp
         ctx.orig_shape = shape
         return out.view(*shape)
@@ -290,8 +303,10 @@ class _LoRA_MLP(torch.autograd.Function):
         r, rp = ctx.rank, ctx.rank_p
         shape = ctx.orig_shape
         dy = hip_ops._bf16_rows(dY.reshape(-1, dY.shape[-1]))
-        dX, dA_GU, dA_D, dB_G, dB_U, dB_D = cops.lora_mlp_bwd(
+        dX, flat = cops.lora_mlp_bwd(
             Xf, gate, up, h, dy, GW, UW, DW, a_gu, a_d, BG, BU, BD, ctx.scales, xa_gu, ha_d, rp)
+        shapes = hip_ops.lora_mlp_grad_shapes(Xf.shape[1], gate.shape[1], rp)
+        dA_GU, dA_D, dB_G, dB_U, dB_D = _adapter_grads(flat, shapes, ctx.param_dtypes)
         dX = dX.view(*shape)
         return (dX,
                 None, dA_GU[:r], dB_G[:, :r], None,        # GW, GA, GB, GS
@@ -329,6 +344,7 @@ class _LoRA_W(torch.autograd.Function):
         out = cops.lora_linear_out(Xf, Wc, xa, Bp * scale if scale != 1.0 else Bp)
         ctx.save_for_backward(Xf, xa, a, Wc, Bp)
         ctx.scale = scale
+        ctx.param_dtypes = [A.dtype, B.dtype]
         ctx.rank, ctx.rank_p = r, rp
         ctx.orig_shape = shape
         return out.view(*shape[:-1], out.shape[-1])
@@ -344,7 +360,9 @@ class _LoRA_W(torch.autograd.Function):
         Xf, xa, a, Wc, Bp = ctx.saved_tensors
         r, rp = ctx.rank, ctx.rank_p
         dy = hip_ops._bf16_rows(dY.reshape(-1, dY.shape[-1]))
-        dX, dA, dB = cops.lora_linear_bwd(Xf, dy, Wc, a, Bp, ctx.scale, xa, rp)
+        dX, flat = cops.lora_linear_bwd(Xf, dy, Wc, a, Bp, ctx.scale, xa, rp)
+        shapes = hip_ops.lora_linear_grad_shapes(Xf.shape[1], dy.shape[1], rp)
+        dA, dB = _adapter_grads(flat, shapes, ctx.param_dtypes)
         return dX.view(*ctx.orig_shape), None, dA[:r], dB[:, :r], None
 
 

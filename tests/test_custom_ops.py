@@ -58,16 +58,28 @@ def test_fake_kernels_flce_lora(ops):
         x = e(96, 128)
         assert ops.linear_bf16(x, e(64, 128)).shape == (96, 64)
         assert ops.lora_xa(x, e(48, 128)).shape == (96, 48)
-        dX, dA, *dBs = ops.lora_qkv_bwd(x, [e(96, 128), e(96, 64), e(96, 64)],
-                                        [e(128, 128), e(64, 128), e(64, 128)], e(48, 128),
-                                        [e(128, 16), e(64, 16), e(64, 16)], [2.0] * 3, e(96, 48), 16)
-        assert dX.shape == (96, 128) and dA.shape == (48, 128) and dA.dtype == F32
-        assert [tuple(b.shape) for b in dBs] == [(128, 16), (64, 16), (64, 16)]
-        dX, dA, dB = ops.lora_linear_bwd(x, e(96, 64), e(64, 128), e(16, 128), e(64, 16), 2.0,
-                                         e(96, 16), 16)
-        assert dA.shape == (16, 128) and dB.shape == (64, 16)
-        outs = ops.lora_mlp_bwd(x, e(96, 256), e(96, 256), e(96, 256), e(96, 128), e(256, 128),
-                                e(256, 128), e(128, 256), e(32, 128), e(16, 256), e(256, 16),
-                                e(256, 16), e(128, 16), [2.0] * 3, e(96, 32), e(96, 16), 16)
-        assert [tuple(t.shape) for t in outs] == [(96, 128), (32, 128), (16, 256), (256, 16),
-                                                  (256, 16), (128, 16)]
+        # LoRA backwards: dX and one fp32 buffer of the adapter gradients,
+        # each starting on a 64-element boundary (hip_ops.grad_layout)
+        dX, g = ops.lora_qkv_bwd(x, [e(96, 128), e(96, 64), e(96, 64)],
+                                 [e(128, 128), e(64, 128), e(64, 128)], e(48, 128),
+                                 [e(128, 16), e(64, 16), e(64, 16)], [2.0] * 3, e(96, 48), 16)
+        assert dX.shape == (96, 128) and g.dtype == F32
+        assert g.shape == (48 * 128 + 128 * 16 + 64 * 16 + 64 * 16,)
+        dX, g = ops.lora_linear_bwd(x, e(96, 64), e(64, 128), e(16, 128), e(64, 16), 2.0,
+                                    e(96, 16), 16)
+        assert dX.shape == (96, 128) and g.shape == (16 * 128 + 64 * 16,)
+        dX, g = ops.lora_mlp_bwd(x, e(96, 256), e(96, 256), e(96, 256), e(96, 128), e(256, 128),
+                                 e(256, 128), e(128, 256), e(32, 128), e(16, 256), e(256, 16),
+                                 e(256, 16), e(128, 16), [2.0] * 3, e(96, 32), e(96, 16), 16)
+        assert dX.shape == (96, 128) and g.shape == (32 * 128 + 16 * 256 + 2 * 256 * 16 + 128 * 16,)
+
+
+def test_grad_layout_offsets():
+    from metal_liger_amd import hip_ops
+    offs, total = hip_ops.grad_layout([(3, 5), (2, 32), (7,)])
+    assert offs == [0, 64, 128] and total == 192          # 15 -> 64, 64 -> 64, 7 -> 64
+    flat = torch.arange(192, dtype=torch.float32)
+    a, b, c = hip_ops.grad_views(flat, [(3, 5), (2, 32), (7,)])
+    assert a.shape == (3, 5) and a[2, 4].item() == 14
+    assert b.shape == (2, 32) and b[0, 0].item() == 64 and b.is_contiguous()
+    assert c.shape == (7,) and c[0].item() == 128

@@ -30,7 +30,7 @@ pytestmark = pytest.mark.gpu
 def _step(model, ids):
     model.train()
     model.zero_grad(set_to_none=True)
-    out = model(input_ids=ids, labels=ids)
+    out = model(input_ids=ids, labels=ids, use_cache=False)
     out.loss.backward()
     grads = {n: p.grad.detach().float().clone() for n, p in model.named_parameters()
              if "lora_" in n and p.grad is not None}
