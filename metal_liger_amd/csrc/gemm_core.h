@@ -1248,8 +1248,9 @@ __device__ __forceinline__ void r4_mainloop(const Problem& pb, int tm, int tn, i
   for (int i = 0; i < r4::TM; ++i) f0.a[i] = r4_read_frag<LA>(lds, fa, 0, i);
 
   // One phase: the 64 MFMAs of fragment set fc, with the reads of the next
-  // k-step (k-step NS of stage `src`) into fn, interleaved; in phase 1 also
-  // the loads of the cursor's k-tile into stage `dst`.
+  // k-step (k-step NS of stage `src`) into fn, interleaved; phase 0 also
+  // moves the cursor to k-tile t + 2 (next_tile), phase 1 issues that
+  // k-tile's loads into stage `dst`.
   auto phase = [&](auto pc, R4Frags& fc, R4Frags& fn, const char* src, char* dst)
                    __attribute__((always_inline)) {
     constexpr int P = decltype(pc)::value;
@@ -1257,10 +1258,14 @@ __device__ __forceinline__ void r4_mainloop(const Problem& pb, int tm, int tn, i
     static_for<r4::TM * r4::TN>([&](auto qc) {
       constexpr int q = decltype(qc)::value;
       constexpr int i = q / r4::TN, j = q % r4::TN;
-      // next k-step: B fragments at slots 1, 5, .., 29, A at 33, 37, .., 61
-      if constexpr ((q & 3) == 1 && q < 32) fn.b[q >> 2] = r4_read_frag<LB>(src + r4::OP_BYTES, fb, NS, q >> 2);
-      if constexpr ((q & 3) == 1 && q >= 32) fn.a[(q - 32) >> 2] = r4_read_frag<LA>(src, fa, NS, (q - 32) >> 2);
+      // next k-step: B fragments at slots 0, 2, .., 14, A at 16, 18, .., 30
+      // (all sixteen reads land well before the next phase's first MFMA)
+      if constexpr ((q & 1) == 0 && q < 16) fn.b[q >> 1] = r4_read_frag<LB>(src + r4::OP_BYTES, fb, NS, q >> 1);
+      if constexpr ((q & 1) == 0 && q >= 16 && q < 32) fn.a[(q - 16) >> 1] = r4_read_frag<LA>(src, fa, NS, (q - 16) >> 1);
       if constexpr (P == 1 && (q & 3) == 3) load(dst, q >> 2);
+      // the cursor's scalar work for k-tile t + 2 runs in the shadow of
+      // phase 0's MFMAs (phase 0 issues no loads)
+      if constexpr (P == 0 && q == 40) next_tile();
       r4_mfma(acc[j >> 2][i][j & 3], fc.a[i], fc.b[j]);
       __builtin_amdgcn_sched_barrier(0);
     });
@@ -1274,7 +1279,6 @@ __device__ __forceinline__ void r4_mainloop(const Problem& pb, int tm, int tn, i
     // operation is in flight); the barrier publishes them
     __builtin_amdgcn_s_waitcnt(big::kWaitVm0);
     lds_barrier();
-    next_tile();  // resources of k-tile t + 2, loaded into stage cs during phase 1
     phase(std::integral_constant<int, 1>{}, f1, f0, ns, cs);
   }
   // the epilogue reads the accumulators: wait for the last MFMAs (the
