@@ -686,10 +686,10 @@ int fwd_grad_impl(const bf16* hidden, int64_t ldh, const bf16* weight, int64_t l
     if (d_hidden) {  // 4. dH_c = D W (split-K over the vocabulary)
       Segment seg{{w.E, (int64_t)V}, {weight, ldw}, V};
       Problem pb;
-      rc = make_problem<BigCfg>(pb, Tc, H, 1, &seg, kKMajor, kMNMajor, 0, dh_ksplit(Tc, H, V));
+      rc = make_problem<R4Cfg>(pb, Tc, H, 1, &seg, kKMajor, kMNMajor, 0, dh_ksplit(Tc, H, V));
       if (rc) return rc;
       ML_CHECK(splitk_ws_bytes(pb) <= w.part_bytes, "flce: dH partial workspace too small");
-      rc = launch_splitk<BigCfg, kKMajor, kMNMajor, bf16>(pb, w.part, d_hidden + (int64_t)t0 * H,
+      rc = launch_splitk<R4Cfg, kKMajor, kMNMajor, bf16>(pb, w.part, d_hidden + (int64_t)t0 * H,
                                                           H, 1.0f, 0.0f, st);
       if (rc) return rc;
     }

@@ -1,12 +1,17 @@
 // bf16 MFMA GEMM core for gfx950 (CDNA4): C[M,N] = sum_k A[m,k] * B[k,n],
-// fp32 accumulation, pluggable epilogue. Two engines share the problem
+// fp32 accumulation, pluggable epilogue. The engines share the problem
 // description, the tile order and the epilogues:
 //
-// 256 x 256 tiles (every large product: FLCE logits / dH / dW, LoRA dX, the
-//   plain GEMM entry points) - see "256 x 256" below: v_mfma_f32_16x16x32_bf16,
-//   k-tiles of 32, four LDS stages filled by buffer_load ... lds straight
-//   from global memory in both operand layouts, transposing LDS reads
-//   (ds_read_b64_tr_b16) for MN-major operands.
+// 256 x 256 tiles (every large product), v_mfma_f32_16x16x32_bf16, operands
+//   filled into LDS by buffer_load ... lds straight from global memory in
+//   both layouts, transposing LDS reads (ds_read_b64_tr_b16) for MN-major
+//   operands; two engines:
+//   - 8 waves, two per SIMD in ping-pong, k-tiles of 32, four LDS stages
+//     (see "256 x 256" below): the FLCE logits (row-LSE epilogue) and dW
+//     (MN-major A) products;
+//   - r4: 4 waves of 128 x 128, k-tiles of 64, two stages (see "r4" below):
+//     the products with a K-major A and a store or split-K epilogue (LoRA
+//     forward / dX / dH, FLCE dH, the plain GEMM entry points).
 // Narrow tiles Cfg<BM, BN, WAVES_M> (256 x 32, 64 x 256: the rank-r LoRA
 //   products, which would waste most of a 256 x 256 tile on padding):
 //   256 threads = 4 wave64s in a WAVES_M x (4 / WAVES_M) grid; a wave owns a
