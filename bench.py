@@ -429,13 +429,14 @@ def build_train_model(dev, layers=None):
     """The 4-layer Qwen3-style LoRA train-step model (tests/qwen_tiny.py,
     build_train_config: hidden 2048, 16 q / 8 kv heads, head_dim 128, MLP
     6144, vocab 151936, tied embeddings, rank-16 LoRA on q, k, v, o, gate,
-    up, down, bf16) with every fused op patched in; only the adapters
-    train."""
+    up, down, bf16) with every fused op patched in and its grouped-query
+    attention on SDPA's memory-efficient kernel (efficient_attention); only
+    the adapters train."""
     from metal_liger_amd import apply_metal_liger_to_qwen3vl
     from tests import qwen_tiny
     model = qwen_tiny.build_train_config(dev, layers or qwen_tiny.TRAIN_LAYERS)
     model = apply_metal_liger_to_qwen3vl(model, fuse_qk_norm_rope=True, fuse_lm_loss=True,
-                                         fuse_residual_norm=True)
+                                         fuse_residual_norm=True, efficient_attention=True)
     qwen_tiny.freeze_all_but_lora(model)
     return model
 
@@ -449,9 +450,10 @@ def bench_train_step(dev, steps=5, warmup=2):
     fused linear cross-entropy (transformers' label shift: the last position
     of each sequence ignored; no logits formed), backward, AdamW on the
     adapters.
-    Attention is torch's scaled_dot_product_attention restricted to its
-    flash / memory-efficient kernels (an unavailable kernel raises instead of
-    falling back to the batched-matmul path). tokens/s = 8192 / step time."""
+    Attention is torch's scaled_dot_product_attention over key / value heads
+    repeated to the 16 query heads, on its memory-efficient kernel (flash
+    after it; an unavailable kernel raises instead of falling back to the
+    batched-matmul path). tokens/s = 8192 / step time."""
     import torch
     from torch.nn.attention import SDPBackend, sdpa_kernel
 
@@ -493,7 +495,7 @@ def bench_train_step(dev, steps=5, warmup=2):
             "tokens_per_s": round(n_tok / dt, 1), "loss_first": round(first, 4),
             "loss_last": round(last, 4), "steps": steps, "warmup": warmup,
             "includes": "fwd + FLCE loss (model(input_ids, labels=input_ids, use_cache=False)) + bwd + AdamW on LoRA params",
-            "attention": "torch SDPA (flash / mem-efficient)"}
+            "attention": "torch SDPA, memory-efficient kernel, key/value heads repeated (efficient_attention=True)"}
 
 
 def pmc_probe(dev):

@@ -21,6 +21,7 @@ from metal_liger_amd.ops.fused_lora import patch_fused_lora
 from metal_liger_amd.ops.fused_qk_norm_rope import patch_qk_norm_rope
 from metal_liger_amd.ops.fused_rms_norm import MetalLigerRMSNorm
 from metal_liger_amd.ops.fused_swiglu import MetalLigerSwiGLU
+from metal_liger_amd.ops.gqa_attention import patch_efficient_attention
 
 logger = logging.getLogger(__name__)
 
@@ -80,6 +81,7 @@ def apply_metal_liger_to_qwen3vl(
     fuse_residual_norm: bool = False,
     fuse_qk_norm_rope: bool = False,
     fuse_lm_loss: bool = False,
+    efficient_attention: bool = False,
 ) -> nn.Module:
     """Apply the fused operations to a Qwen3 / Qwen3-VL model in place and
     return it (patch.py:181-240).
@@ -100,6 +102,10 @@ def apply_metal_liger_to_qwen3vl(
     training mode) comes from the fused linear cross-entropy with
     transformers' label shift, and the output's logits are None
     (ops/fused_linear_cross_entropy.py, patch_causal_lm_loss).
+    efficient_attention: grouped-query attention modules on transformers'
+    "sdpa" implementation run SDPA's memory-efficient kernel over repeated
+    key / value heads instead of the flash kernel with GQA
+    (ops/gqa_attention.py).
     use_optimized_generator is not part of metal_liger_amd (inference path).
     """
     stats = {}
@@ -128,6 +134,10 @@ def apply_metal_liger_to_qwen3vl(
         n = patch_causal_lm_loss(model)
         stats["lm_loss"] = n
         logger.info(f"MetalLiger: fused linear cross-entropy loss on {n} causal LM heads")
+    if efficient_attention:
+        n = patch_efficient_attention(model)
+        stats["efficient_attention"] = n
+        logger.info(f"MetalLiger: {n} attention modules on SDPA's memory-efficient kernel")
     if use_optimized_generator:
         logger.warning("MetalLiger: the optimized generator is not part of metal_liger_amd; skipped")
         stats["generator"] = "unavailable"

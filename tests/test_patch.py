@@ -429,3 +429,42 @@ def test_qwen3_vl_text_stack_patched(monkeypatch):
     for n, g in g0.items():
         err = (g1[n].double() - g.double()).abs().max()
         assert err <= 1e-4 * g.double().abs().max() + 1e-7, n
+
+
+def test_efficient_attention_matches_sdpa():
+    """efficient_attention=True (key / value heads repeated, SDPA with the
+    memory-efficient kernel first) against transformers' own "sdpa" path on
+    the tiny GQA model (4 query / 2 key-value heads), fp32 on the CPU: the
+    causal case (no mask tensor) and a left-padded batch (a mask tensor);
+    a model on "eager" keeps it."""
+    import copy
+
+    from metal_liger_amd import apply_metal_liger_to_qwen3vl
+    from metal_liger_amd.ops.gqa_attention import ATTN_KEY, _repeat_heads
+    base = qwen_tiny.build(lora=False, peft_wrap=False, attn="sdpa")
+    base.eval()
+    patched = apply_metal_liger_to_qwen3vl(copy.deepcopy(base), fuse_rms_norm=False,
+                                           fuse_swiglu=False, fuse_lora=False,
+                                           efficient_attention=True)
+    assert patched.config._attn_implementation == ATTN_KEY
+    assert base.config._attn_implementation == "sdpa"
+    g = torch.Generator().manual_seed(5)
+    ids = torch.randint(0, 512, (2, 24), generator=g)
+    mask = torch.ones(2, 24, dtype=torch.long)
+    mask[1, :7] = 0
+    with torch.no_grad():
+        for kw in ({}, {"attention_mask": mask}):
+            ref = base(input_ids=ids, use_cache=False, **kw).logits
+            out = patched(input_ids=ids, use_cache=False, **kw).logits
+            keep = slice(None) if not kw else (mask[:, :, None] > 0).expand_as(ref)
+            assert torch.allclose(out[keep], ref[keep], rtol=1e-4, atol=1e-4), kw
+    # query head h reads key / value head h // groups
+    kv = torch.arange(2 * 3, dtype=torch.float32).reshape(1, 3, 2, 1)
+    rep = _repeat_heads(kv, 2)
+    assert rep.shape == (1, 6, 2, 1)
+    assert torch.equal(rep[0, :, 0, 0], torch.tensor([0.0, 0.0, 2.0, 2.0, 4.0, 4.0]))
+    eager = qwen_tiny.build(lora=False, peft_wrap=False, attn="eager")
+    from metal_liger_amd.ops.gqa_attention import patch_efficient_attention
+    assert patch_efficient_attention(eager) == 0
+    assert eager.config._attn_implementation == "eager"
+    assert patch_efficient_attention(patched) == 2                   # both layers
