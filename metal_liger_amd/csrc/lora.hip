@@ -13,11 +13,14 @@
 //         dY with its W plus the stacked rank-r terms (K = sum(out) + n r).
 // The MLP backward first forms dH = dY_D W_D + P_D A_D (bf16), runs the
 // SwiGLU backward over it in place (sigmoid recomputed), then treats
-// (d_gate, d_up) as the output grads of the gate / up adapters. Partials are
+// (d_gate, d_up) as the output grads of the gate / up adapters; at rank 16
+// one pass (mlp_mid_kernel) does the SwiGLU backward, the gate / up dY-pass
+// work and P_D^T h. Partials are
 // summed in a fixed order, so every gradient is bit-reproducible.
 #include <algorithm>
 
 #include "gemm_core.h"
+#include "swiglu_math.h"
 
 namespace mla {
 namespace lora {
@@ -518,6 +521,338 @@ inline int ptx_pass(int N, const bf16* P, int64_t ldp, int RT, const bf16* X, in
   return ML_OK;
 }
 
+// -------------------------------------------- MLP SwiGLU backward pass --
+// The MLP backward's middle, rank 16, in one pass over dH [N, I]: the SwiGLU
+// backward and the three rank-16 products that read its inputs or outputs,
+//   d_gate, d_up = SwiGLU'(gate, up) dH   (stored; d_gate over dH in place)
+//   P_G, dB_G    = s_G d_gate B_G, s_G d_gate^T XA_G     (as the dY pass)
+//   P_U, dB_U    = s_U d_up B_U,   s_U d_up^T XA_U
+//   dA_D         = P_D^T h                               (as the P^T X pass)
+// instead of a SwiGLU backward, a dY pass over d_gate / d_up and a P^T X
+// pass over h (which read d_gate / d_up back from HBM and take 5 launches).
+// A workgroup of 4 waves owns a 256 x 256 tile and walks it in chunks of 32
+// rows. Per chunk each thread loads one 16-byte vector of dH, gate, up and h
+// from each of 4 rows (rows t / 32 + 8 i, columns 8 (t % 32) ..) - the next
+// chunk's loads are in flight while the current chunk's MFMAs run - forms
+// d_gate / d_up with the SwiGLU kernels' element math, stores them, and
+// writes d_gate, d_up and h into LDS in the dY pass's MN-major layout (the
+// 32-byte unit u of row r at u ^ h(r)), beside the chunk's XA and P_D rows.
+// The MFMA work, the partial layouts and the fixed-order reduction are the
+// dY pass's and the P^T X pass's, so the results equal theirs bit for bit.
+// Rows past N and columns past I enter as zeros and are not stored.
+constexpr int kMidD = 0;                                // d_gate chunk
+constexpr int kMidU = kDyChunkBytes;                    // d_up chunk
+constexpr int kMidH = 2 * kDyChunkBytes;                // h chunk; then the P meets
+constexpr int kMidXa = 3 * kDyChunkBytes;               // XA_G [32][16], XA_U [32][16]
+constexpr int kMidPd = kMidXa + 2 * kDyXaBytes;         // P_D [32][16]
+constexpr int kMidBytes = kMidPd + kDyXaBytes;          // 51 KB: three workgroups per CU
+constexpr int kMidMeetBytes = 4 * kDyChunk * kDyRank * 4;  // one adapter's P meet
+static_assert(2 * kMidMeetBytes <= kDyChunkBytes, "both P meets fit in the h region");
+
+struct MlpMidArgs {
+  bf16* dh;  // [N, I]: dH in, d_gate out
+  bf16* dup;  // [N, I]
+  const bf16* gate;
+  const bf16* up;
+  const bf16* h;   // [N, I] each, dense
+  const bf16* xa;  // [N, 32]: XA_G | XA_U, row stride ldxa
+  const bf16* pd;  // [N, 16]: P_D, row stride ldpd
+  const bf16* b[2];  // B_G, B_U [I, 16], row stride ldb
+  float* ppart[2];   // [ctiles][N][16]
+  float* dbpart[2];  // [rtiles][I][16]
+  float* dapart;     // [rtiles][16][I]
+  int64_t ldxa, ldpd, ldb;
+  int N, I, ctiles;
+};
+
+__device__ __forceinline__ int mn_swz(int r) { return (r & 3) | (((r >> 3) & 1) << 2); }
+
+// 16 bytes or zeros, as a vector select (a select between two structs would
+// go through scratch memory)
+__device__ __forceinline__ u32x4_t keep16(bool ok, u32x4_t v) {
+  return ok ? v : u32x4_t{0u, 0u, 0u, 0u};
+}
+
+__global__ __launch_bounds__(256) void mlp_mid_kernel(const MlpMidArgs args) {
+  typedef Pack<bf16, 8> V8;
+  __shared__ __attribute__((aligned(16))) char lds[kMidBytes];
+  const int ct = blockIdx.x % args.ctiles, rt = blockIdx.x / args.ctiles;
+  const int m0 = rt * kDyRows, c0 = ct * kDyCols;
+  const int N = args.N, I = args.I;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int rows = N - m0 < kDyRows ? N - m0 : kDyRows;
+  const int nchunks = (rows + kDyChunk - 1) / kDyChunk;
+
+  // B fragments of this wave's two k-steps, as in the dY pass: the tile's
+  // B_G / B_U rows [256][16] are staged through the (still unused) h region
+  // with 16-byte loads, rows past I as zeros.
+  bf16x8_t bfr[2][2];
+  {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      // 16-byte vector v: adapter v / 512 (= q / 2), row (v / 2) % 256, half v % 2
+      const int v = tid + 256 * q;
+      const int row = (v >> 1) & 255, c = c0 + row;
+      const bf16* src = args.b[q >> 1];
+      const u32x4_t x = *reinterpret_cast<const u32x4_t*>(
+          src + (int64_t)(c < I ? c : I - 1) * args.ldb + 8 * (v & 1));
+      *reinterpret_cast<u32x4_t*>(lds + kMidH + 16 * v) = keep16(c < I, x);
+    }
+    __syncthreads();
+    const bf16* bl = reinterpret_cast<const bf16*>(lds + kMidH);
+#pragma unroll
+    for (int ad = 0; ad < 2; ++ad)
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        const int cb = 64 * wave + 32 * ks + 8 * (lane >> 4);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) bfr[ad][ks][j] = bl[(ad * 256 + cb + j) * kDyRank + (lane & 15)];
+      }
+  }
+
+  // This thread's vectors: chunk rows (tid / 32) + 8 i, columns cc .. cc + 7
+  // (a column group past I reads the last valid one and is zeroed).
+  const int cg = tid & 31;
+  const int cc = c0 + 8 * cg;
+  const bool okc = cc < I;
+  const int ccl = okc ? cc : I - 8;
+  uint32_t ldsoff[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int rq = (tid >> 5) + 8 * i;
+    ldsoff[i] = (uint32_t)(rq * 512 + ((((cg >> 1) ^ mn_swz(rq)) << 5) | ((cg & 1) << 4)));
+  }
+  // The chunk's small rows: threads 0..127 one 16-byte quarter of an XA_GU
+  // row (row tid / 4), threads 128..191 one half of a P_D row; the others
+  // load P_D's first vector again and store nothing (every thread loads, so
+  // that no load sits in a branch the compiler would wait for).
+  const int srow = tid < 128 ? (tid >> 2) : tid < 192 ? ((tid - 128) >> 1) : 0;
+  const bool sxa = tid < 128;
+  const bf16* sbase = sxa ? args.xa : args.pd;
+  const int64_t sld = sxa ? args.ldxa : args.ldpd;
+  const int scol = sxa ? 8 * (tid & 3) : tid < 192 ? 8 * (tid & 1) : 0;
+  const uint32_t sdst =
+      sxa ? (uint32_t)(kMidXa + ((tid & 3) >> 1) * kDyXaBytes + srow * 32 + (tid & 1) * 16)
+          : (uint32_t)(kMidPd + srow * 32 + (tid & 1) * 16);
+
+  // The [N, I] operands share one layout: a chunk's vectors are addressed
+  // as a uniform chunk base plus a 32-bit byte offset per row (the host
+  // checks N I < 2^31), one VGPR each instead of a 64-bit address per load.
+  auto nt16 = [](const bf16* base, int64_t chunk_bytes, uint32_t off) __attribute__((always_inline)) {
+    return __builtin_nontemporal_load(
+        reinterpret_cast<const u32x4_t*>(reinterpret_cast<const char*>(base) + chunk_bytes + off));
+  };
+  u32x4_t vd[4], vg[4], vu[4], vh[4], vs;
+  auto load_chunk = [&](int t) __attribute__((always_inline)) {
+    const int rb = m0 + kDyChunk * t;
+    const int64_t cb = (int64_t)rb * I * 2;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int rq = (tid >> 5) + 8 * i;
+      const int rr = rb + rq < N ? rq : N - 1 - rb;  // rows past N re-read the last row
+      const uint32_t off = (uint32_t)(rr * I + ccl) * 2u;
+      vd[i] = nt16(args.dh, cb, off);
+      vg[i] = nt16(args.gate, cb, off);
+      vu[i] = nt16(args.up, cb, off);
+      vh[i] = nt16(args.h, cb, off);
+    }
+    const int r = rb + srow;
+    vs = *reinterpret_cast<const u32x4_t*>(sbase + (int64_t)(r < N ? r : N - 1) * sld + scol);
+  };
+
+  FragAddr<kMNMajor, 4> fa;
+  frag_addr_setup<kMNMajor, 4>(fa, 64 * wave, lane);
+  f32x4_t accb[2][4], acca[4];
+#pragma unroll
+  for (int f = 0; f < 4; ++f) {
+    accb[0][f] = accb[1][f] = acca[f] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  }
+  load_chunk(0);
+  for (int t = 0; t < nchunks; ++t) {
+    const int rb = m0 + kDyChunk * t;
+    __syncthreads();  // the previous chunk's LDS reads are done
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = rb + (tid >> 5) + 8 * i;
+      const bool ok = okc && r < N;
+      const V8 g8 = __builtin_bit_cast(V8, vg[i]), u8 = __builtin_bit_cast(V8, vu[i]),
+               y8 = __builtin_bit_cast(V8, vd[i]);
+      V8 pg, pu;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        float dgf, duf;
+        swiglu_bwd_elem(to_f32(g8.v[e]), to_f32(u8.v[e]), to_f32(y8.v[e]), dgf, duf);
+        pg.v[e] = from_f32<bf16>(dgf);
+        pu.v[e] = from_f32<bf16>(duf);
+      }
+      const u32x4_t xg = __builtin_bit_cast(u32x4_t, pg), xu = __builtin_bit_cast(u32x4_t, pu);
+      if (ok) {
+        const int64_t cb = (int64_t)rb * I * 2;
+        const uint32_t off = (uint32_t)(((tid >> 5) + 8 * i) * I + cc) * 2u;
+        __builtin_nontemporal_store(
+            xg, reinterpret_cast<u32x4_t*>(reinterpret_cast<char*>(args.dh) + cb + off));
+        __builtin_nontemporal_store(
+            xu, reinterpret_cast<u32x4_t*>(reinterpret_cast<char*>(args.dup) + cb + off));
+      }
+      *reinterpret_cast<u32x4_t*>(lds + kMidD + ldsoff[i]) = keep16(ok, xg);
+      *reinterpret_cast<u32x4_t*>(lds + kMidU + ldsoff[i]) = keep16(ok, xu);
+      *reinterpret_cast<u32x4_t*>(lds + kMidH + ldsoff[i]) = keep16(ok, vh[i]);
+      // one vector at a time: interleaved, the four vectors' fp32 operands
+      // would need 96 VGPRs
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (tid < 192) *reinterpret_cast<u32x4_t*>(lds + sdst) = keep16(rb + srow < N, vs);
+    // the next chunk's loads go out only after this chunk's vectors are
+    // consumed (hoisted above, both chunks' 64 VGPRs would be live at once)
+    asm volatile("" ::: "memory");
+    if (t + 1 < nchunks) load_chunk(t + 1);
+    __syncthreads();  // chunk t published
+
+    // dA_D: A = P_D^T (rows of the chunk's P_D), B = h, as the P^T X pass
+    {
+      const bf16* pl = reinterpret_cast<const bf16*>(lds + kMidPd);
+      bf16x8_t a;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) a[j] = pl[(8 * (lane >> 4) + j) * kDyRank + (lane & 15)];
+#pragma unroll
+      for (int f = 0; f < 4; ++f) {
+        bf16x8_t bx;
+        read_big_frag<kMNMajor, 4>(bx, lds + kMidH, fa, f, 0);
+        read_big_frag<kMNMajor, 4>(bx, lds + kMidH, fa, f, 1);
+        acca[f] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bx, acca[f], 0, 0, 0);
+      }
+    }
+    __syncthreads();  // every wave is done with the h region, which takes the P meets
+#pragma unroll
+    for (int ad = 0; ad < 2; ++ad) {
+      const char* cur = lds + (ad == 0 ? kMidD : kMidU);
+      // P, as the dY pass; the four waves' partials meet in LDS (element v
+      // of tile mt: row 16 mt + 4 (lane / 16) + v, column lane % 16)
+      float* pred = reinterpret_cast<float*>(lds + kMidH + ad * kMidMeetBytes);
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) {
+        const int r = 16 * mt + (lane & 15);
+        const int h = mn_swz(r);
+        f32x4_t accp = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+          const int c = 64 * wave + 32 * ks + 8 * (lane >> 4);
+          const bf16x8_t a = *reinterpret_cast<const bf16x8_t*>(
+              cur + r * 512 + (((c >> 4) ^ h) << 5) + (c & 15) * 2);
+          accp = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bfr[ad][ks], accp, 0, 0, 0);
+        }
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+          pred[wave * (kDyChunk * kDyRank) + (16 * mt + 4 * (lane >> 4) + v) * kDyRank +
+               (lane & 15)] = accp[v];
+      }
+      // dB, as the dY pass
+      bf16x8_t xf;
+      const bf16* xl = reinterpret_cast<const bf16*>(lds + kMidXa + ad * kDyXaBytes);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) xf[j] = xl[(8 * (lane >> 4) + j) * kDyRank + (lane & 15)];
+#pragma unroll
+      for (int f = 0; f < 4; ++f) {
+        bf16x8_t af;
+        read_big_frag<kMNMajor, 4>(af, cur, fa, f, 0);
+        read_big_frag<kMNMajor, 4>(af, cur, fa, f, 1);
+        accb[ad][f] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, xf, accb[ad][f], 0, 0, 0);
+      }
+    }
+    __syncthreads();  // the P meets are complete
+#pragma unroll
+    for (int ad = 0; ad < 2; ++ad) {
+      const float* pred = reinterpret_cast<const float*>(lds + kMidH + ad * kMidMeetBytes);
+      constexpr int W = kDyChunk * kDyRank;
+#pragma unroll
+      for (int e = tid; e < W; e += 256) {
+        const int row = rb + e / kDyRank;
+        if (row < N)
+          args.ppart[ad][((int64_t)ct * N + row) * kDyRank + (e % kDyRank)] =
+              (pred[e] + pred[W + e]) + (pred[2 * W + e] + pred[3 * W + e]);
+      }
+    }
+  }
+  // dB partials (element v of tile f: column c0 + 64 w + 16 f + 4 (lane / 16) + v)
+  // and the dA partial (row 4 (lane / 16) + v, column c0 + 64 w + 16 f + lane % 16)
+#pragma unroll
+  for (int f = 0; f < 4; ++f)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int col = c0 + 64 * wave + 16 * f + 4 * (lane >> 4) + v;
+      if (col < I) {
+#pragma unroll
+        for (int ad = 0; ad < 2; ++ad)
+          args.dbpart[ad][((int64_t)rt * I + col) * kDyRank + (lane & 15)] = accb[ad][f][v];
+      }
+      const int cola = c0 + 64 * wave + 16 * f + (lane & 15);
+      if (cola < I)
+        args.dapart[((int64_t)rt * kDyRank + 4 * (lane >> 4) + v) * I + cola] = acca[f][v];
+    }
+}
+
+inline size_t mlp_mid_ws_bytes(int N, int I) {
+  const int O[2] = {I, I};
+  return dy_pass_ws_bytes(N, O, 2) + align256(ptx_pass_ws_bytes(N, kDyRank, I));
+}
+
+// Whether the fused pass takes these operands (16-byte aligned vectors).
+inline bool mlp_mid_ok(int I, const void* const* ptrs, int n, int64_t ldxa, int64_t ldpd) {
+  if (I < 8 || I % 8 != 0 || ldxa % 8 != 0 || ldpd % 8 != 0) return false;
+  for (int i = 0; i < n; ++i)
+    if (!aligned16(ptrs[i])) return false;
+  return true;
+}
+
+// Host side: d_gate (over dH) and d_up; P_G, P_U (bf16, s times the sums,
+// row stride ldp) and dB_G, dB_U (fp32 [I, lddb]); dA_D (fp32 [16, I], row
+// stride I).
+inline int mlp_mid_pass(int N, int I, bf16* dh, bf16* dup, const bf16* gate, const bf16* up,
+                        const bf16* h, const bf16* xa, int64_t ldxa, const bf16* pd,
+                        int64_t ldpd, const bf16* bg, const bf16* bu, int64_t ldb, float sg,
+                        float su, bf16* pg, bf16* pu, int64_t ldp, float* dbg, float* dbu,
+                        int64_t lddb, float* da, char* ws, size_t ws_bytes, hipStream_t st) {
+  ML_CHECK(mlp_mid_ws_bytes(N, I) <= ws_bytes, "lora mlp pass: workspace too small");
+  MlpMidArgs a{};
+  a.dh = dh;
+  a.dup = dup;
+  a.gate = gate;
+  a.up = up;
+  a.h = h;
+  a.xa = xa;
+  a.pd = pd;
+  a.b[0] = bg;
+  a.b[1] = bu;
+  a.ldxa = ldxa;
+  a.ldpd = ldpd;
+  a.ldb = ldb;
+  a.N = N;
+  a.I = I;
+  a.ctiles = dy_ctiles(I);
+  char* w = ws;
+  for (int ad = 0; ad < 2; ++ad) {
+    a.ppart[ad] = reinterpret_cast<float*>(w);
+    w += align256(dy_ppart_bytes(N, I));
+    a.dbpart[ad] = reinterpret_cast<float*>(w);
+    w += align256(dy_dbpart_bytes(N, I));
+  }
+  a.dapart = reinterpret_cast<float*>(w);
+  const unsigned blocks = (unsigned)(a.ctiles * dy_rtiles(N));
+  mlp_mid_kernel<<<dim3(blocks), 256, 0, st>>>(a);
+  ML_LAUNCH_CHECK();
+  DyReduceArgs red{};
+  red.job[0] = DyReduceJob{a.ppart[0], a.ctiles, N, pg, ldp, sg, 0};
+  red.job[1] = DyReduceJob{a.dbpart[0], dy_rtiles(N), I, dbg, lddb, sg, 1};
+  red.job[2] = DyReduceJob{a.ppart[1], a.ctiles, N, pu, ldp, su, 0};
+  red.job[3] = DyReduceJob{a.dbpart[1], dy_rtiles(N), I, dbu, lddb, su, 1};
+  // dA_D [16, I] dense: the same flat index in the partials and the output
+  red.job[4] = DyReduceJob{a.dapart, dy_rtiles(N), I, da, kDyRank, 1.0f, 1};
+  dy_reduce_kernel<<<dim3(128, 5), 256, 0, st>>>(red);
+  ML_LAUNCH_CHECK();
+  return ML_OK;
+}
+
 }  // namespace
 }  // namespace lora
 }  // namespace mla
@@ -679,6 +1014,7 @@ static size_t mlp_partial_bytes(int64_t N, int64_t H, int64_t I, int64_t r) {
     m = std::max(m, lora::dy_pass_ws_bytes((int)N, OGU, 2));
     m = std::max(m, lora::ptx_pass_ws_bytes((int)N, (int)r, (int)I));
     m = std::max(m, lora::ptx_pass_ws_bytes((int)N, (int)(2 * r), (int)H));
+    m = std::max(m, lora::mlp_mid_ws_bytes((int)N, (int)I));
   }
   return m;
 }
@@ -726,7 +1062,13 @@ extern "C" int ml_lora_mlp_bwd(const void* X, int64_t n_tokens, int64_t hidden,
   const size_t part_bytes = workspace_bytes - (size_t)(ws - static_cast<char*>(workspace));
   const bf16* x = static_cast<const bf16*>(X);
   const bf16* dy = static_cast<const bf16*>(dY);
+  const bf16* xa = static_cast<const bf16*>(XA_GU);
   int rc;
+  // rank 16 with 16-byte aligned operands: the SwiGLU backward, the gate /
+  // up adapters' P and dB, and dA_D in one pass (lora::mlp_mid_pass)
+  const void* mid_ptrs[9] = {gate, up, h, dgate, dup, xa, PD, BG, BU};
+  const bool fused_mid = R == lora::kDyRank && (int64_t)N * I < (1LL << 31) &&
+                         lora::mlp_mid_ok(I, mid_ptrs, 9, R2, R);
 
   // down projection: P_D, dA_D = P_D^T h, dB_D = s_D dY^T hA_D
   if (R == lora::kDyRank) {  // P_D and dB_D in one pass over dY
@@ -744,7 +1086,9 @@ extern "C" int ml_lora_mlp_bwd(const void* X, int64_t n_tokens, int64_t hidden,
                                                            part_bytes, st);
     if (rc) return rc;
   }
-  if (R == lora::kDyRank) {
+  if (fused_mid) {
+    rc = ML_OK;  // dA_D comes from the fused pass below
+  } else if (R == lora::kDyRank) {
     rc = lora::ptx_pass(N, PD, R, R, static_cast<const bf16*>(h), I, I, dA_D, I,
                         reinterpret_cast<char*>(part), part_bytes, st);
   } else {
@@ -756,10 +1100,11 @@ extern "C" int ml_lora_mlp_bwd(const void* X, int64_t n_tokens, int64_t hidden,
   // dH = dY W_D + P_D A_D, a bf16 product as in the reference
   // (ops/fused_lora.py:230-233), written into d_gate's buffer; then the
   // SwiGLU backward (:235-244) streams dH, gate, up into d_gate (in place:
-  // each element is read before it is written) and d_up. Two passes beat
-  // the backward fused into the GEMM's epilogue here: with every CU in the
-  // epilogue at once, the 512 KB of gate / up / d_gate / d_up per tile left
-  // the matrix cores idle (324 us against 200 + 74 us).
+  // each element is read before it is written) and d_up - at rank 16 inside
+  // the fused pass that also forms the gate / up adapters' P, dB and dA_D.
+  // A separate pass beats the backward fused into the GEMM's epilogue here:
+  // with every CU in the epilogue at once, the 512 KB of gate / up / d_gate
+  // / d_up per tile left the matrix cores idle (324 us against 200 + 74 us).
   {
     Segment segs[2] = {Segment{{dy, H}, {static_cast<const bf16*>(WD), I}, H},
                        Segment{{PD, R}, {static_cast<const bf16*>(A_D), I}, R}};
@@ -768,6 +1113,15 @@ extern "C" int ml_lora_mlp_bwd(const void* X, int64_t n_tokens, int64_t hidden,
     if (rc) return rc;
     rc = launch_store<bf16, R4Cfg>(pb, kKMajor, kMNMajor, dgate, I, 1.f, 0.f, st);
     if (rc) return rc;
+  }
+  if (fused_mid) {
+    rc = lora::mlp_mid_pass(N, I, dgate, dup, static_cast<const bf16*>(gate),
+                            static_cast<const bf16*>(up), static_cast<const bf16*>(h), xa, R2, PD,
+                            R, static_cast<const bf16*>(BG), static_cast<const bf16*>(BU), R,
+                            scale[0], scale[1], PGU, PGU + R, R2, dB_G, dB_U, R, dA_D,
+                            reinterpret_cast<char*>(part), part_bytes, st);
+    if (rc) return rc;
+  } else {
     rc = ml_swiglu_bwd(gate, up, dgate, dgate, dup, (int64_t)N * I, ML_BF16, st);
     if (rc) return rc;
   }
@@ -775,8 +1129,9 @@ extern "C" int ml_lora_mlp_bwd(const void* X, int64_t n_tokens, int64_t hidden,
   const bf16* dgu[2] = {dgate, dup};
   const void* Bs[2] = {BG, BU};
   float* dBs[2] = {dB_G, dB_U};
-  const bf16* xa = static_cast<const bf16*>(XA_GU);
-  if (R == lora::kDyRank) {  // P_G, P_U, dB_G, dB_U: one pass over each of d_gate, d_up
+  if (fused_mid) {
+    // P_G, P_U, dB_G, dB_U came from the fused pass
+  } else if (R == lora::kDyRank) {  // P_G, P_U, dB_G, dB_U: one pass over each of d_gate, d_up
     lora::DyJob jobs[2];
     for (int i = 0; i < 2; ++i)
       jobs[i] = lora::DyJob{dgu[i], I, I, static_cast<const bf16*>(Bs[i]), R, xa + i * R, R2,

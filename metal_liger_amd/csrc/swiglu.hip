@@ -8,7 +8,7 @@
 // (the reference saved it as an extra fp32 tensor, ops/fused_swiglu.py:34;
 // recomputing it costs no HBM traffic). All math in fp32, products evaluated
 // in the reference's order with one rounding each.
-#include "common.h"
+#include "swiglu_math.h"
 
 #pragma clang fp contract(off)
 
@@ -16,13 +16,6 @@ namespace mla {
 namespace {
 
 constexpr int kThreads = 256;
-
-// sigmoid(x) = 1 / (1 + e^-x) with the hardware exp2 and reciprocal
-// (each ~1 ulp); saturates correctly to 0 / 1 for large |x|.
-__device__ __forceinline__ float sigmoid_f(float x) {
-  const float e = __builtin_amdgcn_exp2f(-x * 1.4426950408889634f);
-  return __builtin_amdgcn_rcpf(1.0f + e);
-}
 
 // One grid-stride step over UNROLL 16-byte chunks. FULL: every chunk is in
 // range, so the loads carry no guard (a guarded load sits in its own branch
@@ -47,7 +40,7 @@ __device__ __forceinline__ void swiglu_fwd_step(const T* __restrict__ g, const T
     if (FULL || i < nvec) {
       float ov[VEC];
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) ov[e] = (gv[k][e] * sigmoid_f(gv[k][e])) * uv[k][e];
+      for (int e = 0; e < VEC; ++e) ov[e] = swiglu_fwd_elem(gv[k][e], uv[k][e]);
       store_n_nt<T, VEC>(o + i * VEC, ov);
     }
   }
@@ -87,11 +80,7 @@ __device__ __forceinline__ void swiglu_bwd_step(const T* __restrict__ g, const T
     if (FULL || i < nvec) {
       float dgv[VEC], duv[VEC];
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) {
-        const float s = sigmoid_f(gv[k][e]);
-        duv[e] = yv[k][e] * (gv[k][e] * s);
-        dgv[e] = ((yv[k][e] * uv[k][e]) * s) * (1.0f + gv[k][e] * (1.0f - s));
-      }
+      for (int e = 0; e < VEC; ++e) swiglu_bwd_elem(gv[k][e], uv[k][e], yv[k][e], dgv[e], duv[e]);
       store_n_nt<T, VEC>(dg + i * VEC, dgv);
       store_n_nt<T, VEC>(du + i * VEC, duv);
     }
@@ -118,7 +107,7 @@ __global__ __launch_bounds__(kThreads) void swiglu_fwd_scalar(const T* __restric
   for (int64_t i = begin + (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n;
        i += (int64_t)gridDim.x * kThreads) {
     const float gv = to_f32(g[i]);
-    o[i] = from_f32<T>((gv * sigmoid_f(gv)) * to_f32(u[i]));
+    o[i] = from_f32<T>(swiglu_fwd_elem(gv, to_f32(u[i])));
   }
 }
 
@@ -131,9 +120,10 @@ __global__ __launch_bounds__(kThreads) void swiglu_bwd_scalar(
     const float gv = to_f32(g[i]);
     const float uv = to_f32(u[i]);
     const float yv = to_f32(dy[i]);
-    const float s = sigmoid_f(gv);
-    du[i] = from_f32<T>(yv * (gv * s));
-    dg[i] = from_f32<T>(((yv * uv) * s) * (1.0f + gv * (1.0f - s)));
+    float dgv, duv;
+    swiglu_bwd_elem(gv, uv, yv, dgv, duv);
+    du[i] = from_f32<T>(duv);
+    dg[i] = from_f32<T>(dgv);
   }
 }
 

@@ -169,7 +169,7 @@ def run_mlp(dev, X, params, dY):
     return out, Xd.grad, leaves
 
 
-@pytest.mark.parametrize("N,H,I,r", [(48, 128, 256, 8), (200, 256, 768, 16)])
+@pytest.mark.parametrize("N,H,I,r", [(48, 128, 256, 8), (200, 256, 768, 16), (130, 128, 328, 16)])
 def test_lora_mlp_small(dev, N, H, I, r):
     X = seeded((N, H), 5, BF)
     G = adapter(I, H, r, 80, w_std=0.1, b_std=0.05)
