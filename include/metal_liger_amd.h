@@ -404,12 +404,27 @@ int ml_gemm_bf16(int64_t M, int64_t N, int64_t K, const void* A, int64_t lda, in
                  const void* B, int64_t ldb, int b_layout, void* C, int64_t ldc, int c_dtype,
                  float alpha, float beta, void* stream);
 
-/* Same product with K split into nseg (1..4) segments, segment s pairing
+/* Same product with K split into nseg (1..8) segments, segment s pairing
  * A_s (lda_s) with B_s (ldb_s) over k_lens[s]: C = alpha * sum_s A_s B_s + beta * C. */
 int ml_gemm_bf16_segments(int64_t M, int64_t N, int nseg, const int64_t* k_lens,
                           const void* const* a_ptrs, const int64_t* ldas, const void* const* b_ptrs,
                           const int64_t* ldbs, int a_layout, int b_layout, void* C, int64_t ldc,
                           int c_dtype, float alpha, float beta, void* stream);
+
+/* count (1..3) independent segmented products in ONE launch, A [M_g, K]
+ * row-major (a_layout 0) for every product: product g has nseg[g] segments,
+ * the next nseg[g] entries of k_lens / a_ptrs / ldas / b_ptrs / ldbs, and
+ * writes C[g] (ldc[g]) = alpha * sum_s A_s B_s + beta * C[g]. For products
+ * too small to fill the GPU on their own: the LoRA QKV forward's q, k and v
+ * projections (ops/fused_lora.py:85-120 forms them one after another; k and
+ * v have half as many 256 x 256 tiles as there are CUs) share rounds of
+ * tiles. Same operand rules as ml_gemm_bf16_segments. */
+int ml_gemm_bf16_segments_group(int count, const int64_t* M, const int64_t* N, const int* nseg,
+                                const int64_t* k_lens, const void* const* a_ptrs,
+                                const int64_t* ldas, const void* const* b_ptrs,
+                                const int64_t* ldbs, int b_layout, void* const* C,
+                                const int64_t* ldc, int c_dtype, float alpha, float beta,
+                                void* stream);
 
 /* Split-K form with a tile shape (tile_cfg 0: 256x256, 1: 256x32 for
  * rank-r outputs, 2: 64x256 for few-row outputs): ksplit slices of K write

@@ -281,6 +281,16 @@ def _(x2, w, xa, sb):
     return x2.new_empty((x2.shape[0], w.shape[0]), dtype=torch.bfloat16)
 
 
+@torch.library.custom_op(f"{NS}::lora_qkv_out", mutates_args=(), device_types=_DEV)
+def lora_qkv_out(x2: Tensor, ws: List[Tensor], xa: Tensor, sbs: List[Tensor]) -> List[Tensor]:
+    return hip_ops.lora_qkv_out(x2, ws, xa, sbs)
+
+
+@lora_qkv_out.register_fake
+def _(x2, ws, xa, sbs):
+    return [x2.new_empty((x2.shape[0], w.shape[0]), dtype=torch.bfloat16) for w in ws]
+
+
 # The LoRA backwards return (dX, grads): grads is one fp32 buffer holding the
 # adapter gradients as laid out by hip_ops.grad_layout (hip_ops.grad_views
 # splits it), so that the caller can cast them to the parameters' dtype in

@@ -79,6 +79,11 @@ SIGNATURES: dict[str, tuple] = {
         [_i64, _i64, _i32, _i64p, ctypes.POINTER(_p), _i64p, ctypes.POINTER(_p), _i64p, _i32, _i32,
          _p, _i64, _i32, _f32, _f32, _p],
     ),
+    "ml_gemm_bf16_segments_group": (
+        _i32,
+        [_i32, _i64p, _i64p, ctypes.POINTER(_i32), _i64p, ctypes.POINTER(_p), _i64p,
+         ctypes.POINTER(_p), _i64p, _i32, ctypes.POINTER(_p), _i64p, _i32, _f32, _f32, _p],
+    ),
     "ml_flce_fwd_workspace_bytes": (_sz, [_i64, _i64]),
     "ml_flce_fwd": (
         _i32,
@@ -195,6 +200,10 @@ def geom(vals) -> ctypes.Array:
 
 def ptrs(vals) -> ctypes.Array:
     return (ctypes.c_void_p * len(vals))(*[v for v in vals])
+
+
+def ints(vals) -> ctypes.Array:
+    return (ctypes.c_int * len(vals))(*[int(v) for v in vals])
 
 
 def floats(vals) -> ctypes.Array:

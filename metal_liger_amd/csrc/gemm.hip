@@ -90,6 +90,46 @@ extern "C" int ml_gemm_bf16_segments(int64_t M, int64_t N, int nseg, const int64
   return gemm::run(M, N, nseg, segs, a_layout, b_layout, C, ldc, c_dtype, alpha, beta, stream);
 }
 
+extern "C" int ml_gemm_bf16_segments_group(int count, const int64_t* M, const int64_t* N,
+                                           const int* nseg, const int64_t* k_lens,
+                                           const void* const* a_ptrs, const int64_t* ldas,
+                                           const void* const* b_ptrs, const int64_t* ldbs,
+                                           int b_layout, void* const* C, const int64_t* ldc,
+                                           int c_dtype, float alpha, float beta, void* stream) {
+  ML_CHECK(count >= 1 && count <= gemm::kMaxGroup, "gemm group: 1..%d products (got %d)",
+           gemm::kMaxGroup, count);
+  ML_CHECK(M && N && nseg && k_lens && a_ptrs && ldas && b_ptrs && ldbs && C && ldc,
+           "gemm group: null argument arrays");
+  ML_CHECK(b_layout == gemm::kKMajor || b_layout == gemm::kMNMajor, "gemm group: bad B layout");
+  gemm::Problem pbs[gemm::kMaxGroup];
+  int base = 0;
+  for (int g = 0; g < count; ++g) {
+    ML_CHECK(M[g] > 0 && N[g] > 0 && M[g] < (1LL << 31) && N[g] < (1LL << 31),
+             "gemm group: bad M=%lld N=%lld (product %d)", (long long)M[g], (long long)N[g], g);
+    ML_CHECK(C[g] != nullptr && ldc[g] >= N[g], "gemm group: bad C (product %d)", g);
+    ML_CHECK(nseg[g] >= 1 && nseg[g] <= gemm::kMaxSeg, "gemm group: 1..%d segments (product %d)",
+             gemm::kMaxSeg, g);
+    gemm::Segment segs[gemm::kMaxSeg];
+    for (int s = 0; s < nseg[g]; ++s) {
+      const int q = base + s;
+      ML_CHECK(k_lens[q] >= 0 && k_lens[q] < (1LL << 31), "gemm group: bad K segment %d", q);
+      segs[s] = gemm::Segment{{static_cast<const bf16*>(a_ptrs[q]), ldas[q]},
+                              {static_cast<const bf16*>(b_ptrs[q]), ldbs[q]}, (int)k_lens[q]};
+    }
+    const int rc = gemm::make_problem<gemm::R4Cfg>(pbs[g], (int)M[g], (int)N[g], nseg[g], segs,
+                                                   gemm::kKMajor, b_layout, 0);
+    if (rc) return rc;
+    base += nseg[g];
+  }
+  hipStream_t st = (hipStream_t)stream;
+  if (c_dtype == ML_BF16)
+    return gemm::launch_store_group<bf16>(pbs, count, b_layout, C, ldc, alpha, beta, st);
+  if (c_dtype == ML_F32)
+    return gemm::launch_store_group<float>(pbs, count, b_layout, C, ldc, alpha, beta, st);
+  set_error("gemm group: C dtype %d not supported (fp32 or bf16)", c_dtype);
+  return ML_ERR_INVALID;
+}
+
 extern "C" size_t ml_gemm_splitk_workspace_bytes(int64_t M, int64_t N, int64_t K, int ksplit) {
   if (M <= 0 || N <= 0 || K <= 0) return 0;
   const int64_t total = (K + gemm::kBK - 1) / gemm::kBK;

@@ -487,10 +487,12 @@ __device__ __forceinline__ void mma_tile_pipelined(f32x16_t (&acc)[C::TM][C::TN]
 }
 
 // Work item of this workgroup (XCD-aware, grouped); false if none.
-__device__ __forceinline__ bool tile_coords(const Problem& pb, int& tm, int& tn, int& split) {
+// bid: the block's index among the product's blocks (blockIdx.x, or its
+// offset inside a grouped launch, whose products start at multiples of 8)
+__device__ __forceinline__ bool tile_coords(const Problem& pb, int bid, int& tm, int& tn,
+                                            int& split) {
   const int W = pb.tiles_m * pb.tiles_n * pb.ksplit;
   const int W8 = (W + kXcds - 1) / kXcds;
-  const int bid = blockIdx.x;
   const int logical = (bid % kXcds) * W8 + bid / kXcds;
   if (logical >= W) return false;
   split = logical % pb.ksplit;
@@ -1425,7 +1427,7 @@ __device__ __forceinline__ void load_row8_bf16(const bf16* p, int n, int N, floa
 template <class C, int LA, int LB, class Epi>
 __global__ __launch_bounds__(C::THREADS) void gemm_kernel(const Problem pb, const Epi epi) {
   int tm, tn, split;
-  if (!tile_coords(pb, tm, tn, split)) return;
+  if (!tile_coords(pb, blockIdx.x, tm, tn, split)) return;
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   if constexpr (C::BM == 256 && C::BN == 256 && C::ENGINE == 2) {
@@ -1455,6 +1457,39 @@ __global__ __launch_bounds__(C::THREADS) void gemm_kernel(const Problem pb, cons
     epi(acc, tm * C::BM + (wave / C::WAVES_N) * C::WM, tn * C::BN + (wave % C::WAVES_N) * C::WN,
         tid & 63, stage0, split);
   }
+}
+
+// Up to kMaxGroup independent r4 products in one launch: blocks
+// [first[g], first[g + 1]) run product g. Products too small to fill the GPU
+// on their own (the LoRA k and v projections: 128 tiles each, half of the
+// CUs) share rounds of tiles instead of each taking a round of its own.
+constexpr int kMaxGroup = 3;
+
+template <class Epi>
+struct GemmGroup {
+  Problem pb[kMaxGroup];
+  Epi epi[kMaxGroup];
+  int first[kMaxGroup + 1];
+  int count;
+};
+
+template <int LA, int LB, class Epi>
+__global__ __launch_bounds__(R4Cfg::THREADS) void gemm_group_kernel(const GemmGroup<Epi> g) {
+  const int bid = blockIdx.x;
+  const int p = (g.count > 2 && bid >= g.first[2]) ? 2 : (g.count > 1 && bid >= g.first[1]) ? 1 : 0;
+  const Problem& pb = p == 0 ? g.pb[0] : p == 1 ? g.pb[1] : g.pb[2];
+  const Epi& epi = p == 0 ? g.epi[0] : p == 1 ? g.epi[1] : g.epi[2];
+  int tm, tn, split;
+  if (!tile_coords(pb, bid - g.first[p], tm, tn, split)) return;
+  const int tid = threadIdx.x;
+  __shared__ __attribute__((aligned(16))) char lds[r4::LDS_BYTES];
+  f32x4_t acc[2][r4::TM][4];
+  r4_mainloop<LA, LB>(pb, tm, tn, split, lds, acc);
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  char* wl = lds + w * 2 * r4::EPI_BYTES;
+  const int em = tm * 256 + (w >> 1) * r4::WM, en = tn * 256 + (w & 1) * r4::WN;
+  epi(acc[0], em, en, tid & 63, wl, split);
+  epi(acc[1], em, en + 64, tid & 63, wl + r4::EPI_BYTES, split);
 }
 
 // --------------------------------------------------------------- epilogues --
@@ -1681,6 +1716,31 @@ inline int launch_store(const Problem& pb, int la, int lb, void* C, int64_t ldc,
     else ML_G(kMNMajor, kMNMajor);
   }
 #undef ML_G
+  ML_LAUNCH_CHECK();
+  return ML_OK;
+}
+
+// count (1..kMaxGroup) products on the r4 engine in one launch, each with the
+// store epilogue into its own C (A K-major).
+template <typename TC>
+inline int launch_store_group(const Problem* pbs, int count, int lb, void* const* C,
+                              const int64_t* ldc, float alpha, float beta, hipStream_t st) {
+  ML_CHECK(count >= 1 && count <= kMaxGroup, "gemm: 1..%d grouped products (got %d)", kMaxGroup,
+           count);
+  GemmGroup<EpiStore<TC>> g{};
+  g.count = count;
+  int blocks = 0;
+  for (int i = 0; i < count; ++i) {
+    g.pb[i] = pbs[i];
+    g.epi[i] = EpiStore<TC>{static_cast<TC*>(C[i]), ldc[i], pbs[i].M, pbs[i].N, alpha, beta};
+    g.first[i] = blocks;
+    blocks += grid_blocks(pbs[i]);  // a multiple of 8: every product keeps its XCD order
+  }
+  for (int i = count; i <= kMaxGroup; ++i) g.first[i] = blocks;
+  if (lb == kKMajor)
+    gemm_group_kernel<kKMajor, kKMajor, EpiStore<TC>><<<dim3(blocks), R4Cfg::THREADS, 0, st>>>(g);
+  else
+    gemm_group_kernel<kKMajor, kMNMajor, EpiStore<TC>><<<dim3(blocks), R4Cfg::THREADS, 0, st>>>(g);
   ML_LAUNCH_CHECK();
   return ML_OK;
 }

@@ -811,6 +811,34 @@ def lora_linear_out(x2: torch.Tensor, w: torch.Tensor, xa: torch.Tensor,
     return out
 
 
+def lora_qkv_out(x2: torch.Tensor, ws, xa: torch.Tensor, sbs) -> list:
+    """The q, k, v LoRA projections X W_i^T + XA_i (s_i B_i)^T (XA_i the i-th
+    block of rank columns of xa) as three K-concatenated products in ONE
+    grouped launch -> three [N, out_i] bf16 tensors."""
+    x2, xa = _al16(x2, xa)
+    ws = [_al16(w) for w in ws]
+    sbs = [_al16(sb) for sb in sbs]
+    N, K = x2.shape
+    rp = sbs[0].shape[1]
+    outs = [torch.empty(N, w.shape[0], dtype=torch.bfloat16, device=x2.device) for w in ws]
+    if N == 0:
+        return outs
+    k_lens, a_p, ldas, b_p, ldbs = [], [], [], [], []
+    for i, (w, sb) in enumerate(zip(ws, sbs)):
+        k_lens += [K, rp]
+        a_p += [x2.data_ptr(), xa.data_ptr() + i * rp * xa.element_size()]
+        ldas += [x2.stride(0), xa.stride(0)]
+        b_p += [w.data_ptr(), sb.data_ptr()]
+        ldbs += [w.stride(0), sb.stride(0)]
+    call(
+        "ml_gemm_bf16_segments_group", len(ws), geom([N] * len(ws)), geom([w.shape[0] for w in ws]),
+        _hip.ints([2] * len(ws)), geom(k_lens), _hip.ptrs(a_p), geom(ldas), _hip.ptrs(b_p),
+        geom(ldbs), 0, _hip.ptrs([o.data_ptr() for o in outs]), geom([o.stride(0) for o in outs]),
+        _hip.BF16, 1.0, 0.0, stream_of(x2),
+    )
+    return outs
+
+
 # The adapter gradients of one LoRA backward call live in one fp32 buffer:
 # each gradient starts on a 256-byte boundary, in the order the call lists
 # them. A caller that wants them in the parameters' dtype converts the buffer

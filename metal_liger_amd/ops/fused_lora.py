@@ -186,10 +186,10 @@ class _LoRA_QKV(torch.autograd.Function):
         Ws = [hip_ops._bf16_rows(W.detach()) for W in (QW, KW, VW)]
         Bs = [_pad_b(B, rp) for B in (QB, KB, VB)]
         scales = [float(QS), float(KS), float(VS)]
-        outs = []
-        for i in range(3):
-            sb = Bs[i] * scales[i] if scales[i] != 1.0 else Bs[i]
-            outs.append(cops.lora_linear_out(Xf, Ws[i], xa[:, i * rp:(i + 1) * rp], sb))
+        sbs = [Bs[i] * scales[i] if scales[i] != 1.0 else Bs[i] for i in range(3)]
+        # the three projections in one launch: k and v alone would each leave
+        # half of the GPU idle for a round of tiles
+        outs = cops.lora_qkv_out(Xf, Ws, xa, sbs)
         ctx.save_for_backward(Xf, xa, a_stack, *Ws, *Bs)
         ctx.scales = scales
         ctx.rank, ctx.rank_p = r, rp

@@ -58,6 +58,10 @@ def test_fake_kernels_flce_lora(ops):
         x = e(96, 128)
         assert ops.linear_bf16(x, e(64, 128)).shape == (96, 64)
         assert ops.lora_xa(x, e(48, 128)).shape == (96, 48)
+        qo, ko, vo = ops.lora_qkv_out(x, [e(128, 128), e(64, 128), e(64, 128)], e(96, 48),
+                                      [e(128, 16), e(64, 16), e(64, 16)])
+        assert qo.shape == (96, 128) and ko.shape == (96, 64) and vo.shape == (96, 64)
+        assert qo.dtype == BF
         # LoRA backwards: dX and one fp32 buffer of the adapter gradients,
         # each starting on a 64-element boundary (hip_ops.grad_layout)
         dX, g = ops.lora_qkv_bwd(x, [e(96, 128), e(96, 64), e(96, 64)],

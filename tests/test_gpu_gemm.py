@@ -91,3 +91,55 @@ def test_gemm_splitk_shapes(dev, cfg, ksplit, a_t, b_t, mnk):
     hip_ops.matmul(a.to(dev), b.to(dev), a_t=a_t, b_t=b_t, out=c, alpha=2.0, beta=0.5,
                    tile_cfg=cfg, ksplit=ksplit)
     assert_close(c, 2.0 * ref_mm(a, b, a_t, b_t) + 0.5 * c0.cpu(), "splitk alpha/beta")
+
+
+@pytest.mark.parametrize("b_t", [True, False])
+def test_gemm_segments_group_matches_single_launches(dev, b_t):
+    """ml_gemm_bf16_segments_group: each product of one grouped launch equals
+    the same product launched alone (same engine, segments and tile order:
+    bit for bit), for the LoRA QKV forward's shapes scaled down (q twice as
+    wide as k and v, a rank-16 segment beside each) plus ragged sizes."""
+    from metal_liger_amd import _hip
+    M, K, r = 600, 264, 16
+    outs_n = [512, 256, 136]
+    X = seeded((M, K), 30, torch.bfloat16).to(dev)
+    XA = seeded((M, 3 * r), 31, torch.bfloat16).to(dev)
+    Ws = [seeded((n, K) if b_t else (K, n), 32 + i, torch.bfloat16).to(dev) for i, n in enumerate(outs_n)]
+    SBs = [seeded((n, r) if b_t else (r, n), 40 + i, torch.bfloat16).to(dev) for i, n in enumerate(outs_n)]
+    b_layout = 0 if b_t else 1
+    a_p, ldas, b_p, ldbs, k_lens = [], [], [], [], []
+    for i in range(3):
+        k_lens += [K, r]
+        a_p += [X.data_ptr(), XA.data_ptr() + 2 * r * i]
+        ldas += [X.stride(0), XA.stride(0)]
+        b_p += [Ws[i].data_ptr(), SBs[i].data_ptr()]
+        ldbs += [Ws[i].stride(0), SBs[i].stride(0)]
+    for dtype, tag in ((torch.bfloat16, 1), (torch.float32, 0)):
+        Cg = [torch.full((M, n), float("nan"), dtype=dtype, device=dev) for n in outs_n]
+        _hip.call("ml_gemm_bf16_segments_group", 3, _hip.geom([M] * 3), _hip.geom(outs_n),
+                  _hip.ints([2, 2, 2]), _hip.geom(k_lens), _hip.ptrs(a_p), _hip.geom(ldas),
+                  _hip.ptrs(b_p), _hip.geom(ldbs), b_layout, _hip.ptrs([c.data_ptr() for c in Cg]),
+                  _hip.geom([c.stride(0) for c in Cg]), tag, 1.0, 0.0,
+                  torch.cuda.current_stream().cuda_stream)
+        for i, n in enumerate(outs_n):
+            C1 = torch.full((M, n), float("nan"), dtype=dtype, device=dev)
+            _hip.call("ml_gemm_bf16_segments", M, n, 2, _hip.geom(k_lens[2 * i:2 * i + 2]),
+                      _hip.ptrs(a_p[2 * i:2 * i + 2]), _hip.geom(ldas[2 * i:2 * i + 2]),
+                      _hip.ptrs(b_p[2 * i:2 * i + 2]), _hip.geom(ldbs[2 * i:2 * i + 2]), 0,
+                      b_layout, C1.data_ptr(), C1.stride(0), tag, 1.0, 0.0,
+                      torch.cuda.current_stream().cuda_stream)
+            torch.cuda.synchronize()
+            assert torch.equal(Cg[i], C1), (i, dtype)
+            Wf = Ws[i].float() if not b_t else Ws[i].float().t()
+            Sf = SBs[i].float() if not b_t else SBs[i].float().t()
+            ref = X.float() @ Wf + XA[:, r * i:r * (i + 1)].float() @ Sf
+            assert_close(Cg[i], ref.to(dtype), f"group product {i}")
+
+
+def test_gemm_segments_group_rejects_bad_counts(dev):
+    from metal_liger_amd import _hip
+    with pytest.raises(RuntimeError, match="grouped|products"):
+        _hip.call("ml_gemm_bf16_segments_group", 4, _hip.geom([8] * 4), _hip.geom([8] * 4),
+                  _hip.ints([1] * 4), _hip.geom([8] * 4), _hip.ptrs([0] * 4), _hip.geom([8] * 4),
+                  _hip.ptrs([0] * 4), _hip.geom([8] * 4), 0, _hip.ptrs([0] * 4),
+                  _hip.geom([8] * 4), 1, 1.0, 0.0, torch.cuda.current_stream().cuda_stream)
