@@ -385,6 +385,16 @@ int ml_lora_mlp_bwd(const void* X, int64_t n_tokens, int64_t hidden, int64_t int
                     float* dA_D, float* dB_G, float* dB_U, float* dB_D, void* workspace,
                     size_t workspace_bytes, void* stream);
 
+/* X A^T for the adapters' stacked A matrices (the rank-r products of the
+ * LoRA forwards: F.linear(x, A) in _lora_linear, ops/fused_lora.py:79-81):
+ * X [n_tokens, in_features] bf16 (row stride ldx), A [rank_total,
+ * in_features] bf16 dense, rank_total 1..64; XA [n_tokens, rank_total] bf16
+ * (row stride ldo) = X A^T with fp32 accumulation. One pass over X (no
+ * split-K partials). in_features and ldx multiples of 8, X and A 16-byte
+ * aligned. */
+int ml_lora_xa(const void* X, int64_t n_tokens, int64_t in_features, int64_t ldx, const void* A,
+               int64_t rank_total, void* XA, int64_t ldo, void* stream);
+
 /* --------------------------------------------------------------------- GEMM
  * bf16 MFMA GEMM (fp32 accumulation): C = alpha * A B + beta * C.
  * No reference counterpart: the reference's contractions are torch.mm /

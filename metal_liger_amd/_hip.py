@@ -79,6 +79,7 @@ SIGNATURES: dict[str, tuple] = {
         [_i64, _i64, _i32, _i64p, ctypes.POINTER(_p), _i64p, ctypes.POINTER(_p), _i64p, _i32, _i32,
          _p, _i64, _i32, _f32, _f32, _p],
     ),
+    "ml_lora_xa": (_i32, [_p, _i64, _i64, _i64, _p, _i64, _p, _i64, _p]),
     "ml_gemm_bf16_segments_group": (
         _i32,
         [_i32, _i64p, _i64p, ctypes.POINTER(_i32), _i64p, ctypes.POINTER(_p), _i64p,

@@ -853,12 +853,123 @@ inline int mlp_mid_pass(int N, int I, bf16* dh, bf16* dup, const bf16* gate, con
   return ML_OK;
 }
 
+// ------------------------------------------------------------------ X A^T --
+// XA [N, R] = X [N, K] A^T for the adapters' stacked A matrices (A [R, K],
+// R <= 64): the LoRA forwards' rank-r products (F.linear(x, A) of
+// ops/fused_lora.py:79-81). A workgroup of 4 waves owns 32 rows of X; wave w
+// takes the w-th quarter of the k range in steps of 32, with the MFMA
+// operands loaded straight from global memory in their register layout
+// (lane l: 16 bytes of row l % 16 at k offset 8 (l / 16)), and the four
+// waves' [32, 16 NT] fp32 sums meet in LDS in a fixed order before the bf16
+// store. X is read once from HBM, A (<= 256 KB) from L2; no split-K partials
+// and no second launch. Rows past N and columns past R are not stored;
+// lanes whose k lies past K contribute zeros (K % 8 == 0).
+constexpr int kXaRows = 32;
+
+template <int NT>
+__global__ __launch_bounds__(256) void xa_kernel(const bf16* __restrict__ X, int64_t ldx,
+                                                 const bf16* __restrict__ A, int64_t lda, int N,
+                                                 int K, int R, bf16* __restrict__ XA,
+                                                 int64_t ldo) {
+  constexpr int W = kXaRows * 16 * NT;  // one wave's sums
+  __shared__ float red[4 * W];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int m0 = blockIdx.x * kXaRows;
+  const int ksteps = (K + 31) / 32;
+  const int per = (ksteps + 3) / 4;
+  const int kb = wave * per, ke = kb + per < ksteps ? kb + per : ksteps;
+  const int lr = lane & 15, lk = 8 * (lane >> 4);
+  // row starts (rows past N / R re-read the last row and are not stored)
+  const bf16* x0 = X + (int64_t)(m0 + lr < N ? m0 + lr : N - 1) * ldx;
+  const bf16* x1 = X + (int64_t)(m0 + 16 + lr < N ? m0 + 16 + lr : N - 1) * ldx;
+  const bf16* ap[NT];
+#pragma unroll
+  for (int j = 0; j < NT; ++j) ap[j] = A + (int64_t)(16 * j + lr < R ? 16 * j + lr : R - 1) * lda;
+  f32x4_t acc[2][NT];
+#pragma unroll
+  for (int j = 0; j < NT; ++j) acc[0][j] = acc[1][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  const bf16x8_t zero = bf16x8_t{};
+  // groups of 4 k-steps: every load of a group is in flight before its MFMAs
+  // (steps past this wave's range load in-range data and are zeroed)
+  for (int s0 = kb; s0 < ke; s0 += 4) {
+    bf16x8_t a0[4], a1[4], b[4][NT];
+    bool ok[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int k = 32 * (s0 + u);
+      ok[u] = s0 + u < ke && k + lk < K;
+      const int kc = ok[u] ? k + lk : 0;  // lanes past K read the row's first 8
+      a0[u] = *reinterpret_cast<const bf16x8_t*>(x0 + kc);
+      a1[u] = *reinterpret_cast<const bf16x8_t*>(x1 + kc);
+#pragma unroll
+      for (int j = 0; j < NT; ++j) b[u][j] = *reinterpret_cast<const bf16x8_t*>(ap[j] + kc);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const bf16x8_t p0 = ok[u] ? a0[u] : zero, p1 = ok[u] ? a1[u] : zero;
+#pragma unroll
+      for (int j = 0; j < NT; ++j) {
+        const bf16x8_t q = ok[u] ? b[u][j] : zero;
+        acc[0][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(p0, q, acc[0][j], 0, 0, 0);
+        acc[1][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(p1, q, acc[1][j], 0, 0, 0);
+      }
+    }
+  }
+  // element v of tile (t, j): row 16 t + 4 (lane / 16) + v, column 16 j + lane % 16
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int j = 0; j < NT; ++j)
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        red[wave * W + (16 * t + 4 * (lane >> 4) + v) * (16 * NT) + 16 * j + lr] = acc[t][j][v];
+  __syncthreads();
+  for (int e = tid; e < W; e += 256) {
+    const int row = m0 + e / (16 * NT), col = e % (16 * NT);
+    if (row < N && col < R)
+      XA[(int64_t)row * ldo + col] =
+          from_f32<bf16>((red[e] + red[W + e]) + (red[2 * W + e] + red[3 * W + e]));
+  }
+}
+
 }  // namespace
 }  // namespace lora
 }  // namespace mla
 
 using namespace mla;
 using namespace mla::gemm;
+
+// ----------------------------------------------------------------- X A^T --
+
+extern "C" int ml_lora_xa(const void* X, int64_t n_tokens, int64_t in_features, int64_t ldx,
+                          const void* A, int64_t rank_total, void* XA, int64_t ldo,
+                          void* stream) {
+  ML_CHECK(n_tokens >= 0 && n_tokens < (1LL << 31), "lora xa: bad token count");
+  ML_CHECK(in_features >= 8 && in_features % 8 == 0 && in_features < (1LL << 31),
+           "lora xa: in_features must be a positive multiple of 8");
+  ML_CHECK(rank_total >= 1 && rank_total <= 64, "lora xa: 1..64 stacked rank rows (got %lld)",
+           (long long)rank_total);
+  ML_CHECK(ldx >= in_features && ldx % 8 == 0 && ldo >= rank_total,
+           "lora xa: bad leading dimensions");
+  ML_CHECK(X && A && XA, "lora xa: null pointer");
+  ML_CHECK(aligned16(X) && aligned16(A), "lora xa: X and A must be 16-byte aligned");
+  if (n_tokens == 0) return ML_OK;
+  const int N = (int)n_tokens, K = (int)in_features, R = (int)rank_total;
+  const dim3 grid((unsigned)((N + lora::kXaRows - 1) / lora::kXaRows));
+  hipStream_t st = (hipStream_t)stream;
+  const bf16* x = static_cast<const bf16*>(X);
+  const bf16* a = static_cast<const bf16*>(A);
+  bf16* o = static_cast<bf16*>(XA);
+  switch ((R + 15) / 16) {
+    case 1: lora::xa_kernel<1><<<grid, 256, 0, st>>>(x, ldx, a, K, N, K, R, o, ldo); break;
+    case 2: lora::xa_kernel<2><<<grid, 256, 0, st>>>(x, ldx, a, K, N, K, R, o, ldo); break;
+    case 3: lora::xa_kernel<3><<<grid, 256, 0, st>>>(x, ldx, a, K, N, K, R, o, ldo); break;
+    default: lora::xa_kernel<4><<<grid, 256, 0, st>>>(x, ldx, a, K, N, K, R, o, ldo); break;
+  }
+  ML_LAUNCH_CHECK();
+  return ML_OK;
+}
 
 // ------------------------------------------------------------------- QKV --
 

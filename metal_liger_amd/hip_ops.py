@@ -783,10 +783,17 @@ def _ksplit_for(tiles: int, k: int) -> int:
 
 
 def lora_xa(x2: torch.Tensor, a_stack: torch.Tensor) -> torch.Tensor:
-    """X A^T for stacked LoRA A matrices: [N, in] x [R, in]^T -> [N, R] bf16
-    (256x32 tiles, split-K over in)."""
+    """X A^T for stacked LoRA A matrices: [N, in] x [R, in]^T -> [N, R] bf16.
+    Up to 64 stacked rows: one pass over X (ml_lora_xa); more: 256x32
+    tiles, split-K over in."""
     N, K = x2.shape
     R = a_stack.shape[0]
+    if R <= 64 and K % 8 == 0 and x2.stride(-1) == 1 and x2.stride(0) % 8 == 0:
+        x2, a_stack = _al16(x2, a_stack.contiguous())
+        out = torch.empty(N, R, dtype=torch.bfloat16, device=x2.device)
+        call("ml_lora_xa", ptr(x2), N, K, x2.stride(0), ptr(a_stack), R, ptr(out), out.stride(0),
+             stream_of(x2))
+        return out
     tiles = ((N + 255) // 256) * ((R + 31) // 32)
     return matmul(x2, a_stack, b_t=True, out_dtype=torch.bfloat16, tile_cfg=1,
                   ksplit=_ksplit_for(tiles, K))

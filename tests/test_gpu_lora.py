@@ -260,3 +260,21 @@ def test_lora_linear_single_projection(dev, N, IN, OUT, r):
     check(Xd.grad, fdX, rdX, "dX")
     check(Ad.grad.float(), fdA, rdA, "dA")
     check(Bd.grad.float(), fdB, rdB, "dB")
+
+
+@pytest.mark.parametrize("N,K,R", [(8192, 2048, 48), (300, 200, 16), (33, 8, 24), (517, 1000, 64),
+                                   (64, 136, 8), (1000, 264, 80)])
+def test_lora_xa_rank_products(dev, N, K, R):
+    """X A^T of the LoRA forwards (F.linear(x, A), ops/fused_lora.py:79-81):
+    the one-pass kernel for up to 64 stacked rows (every tile count 1..4, a
+    k tail, ragged token counts, X a column slice with row stride > K) and
+    the split-K path above 64, against the fp32 product of the same bf16
+    inputs at the bf16 bar."""
+    from metal_liger_amd import hip_ops
+    big = seeded((N, K + 24), 7, BF).to(dev)
+    X = big[:, 8:8 + K]                       # row stride K + 24, 16-byte aligned
+    A = seeded((R, K), 8, BF, scale=0.25).to(dev)
+    out = hip_ops.lora_xa(X, A)
+    assert out.shape == (N, R) and out.dtype == BF
+    expect = X.float() @ A.float().t()
+    assert_close(out, expect.to(BF), f"xa N={N} K={K} R={R}")
