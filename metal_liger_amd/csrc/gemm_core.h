@@ -495,8 +495,13 @@ __device__ __forceinline__ bool tile_coords(const Problem& pb, int bid, int& tm,
   const int W8 = (W + kXcds - 1) / kXcds;
   const int logical = (bid % kXcds) * W8 + bid / kXcds;
   if (logical >= W) return false;
-  split = logical % pb.ksplit;
-  const int t = logical / pb.ksplit;
+  // the split is the slowest index: an XCD's concurrent workgroups take
+  // the tiles of one K range, sharing its A rows and B columns in L2 (split
+  // fastest, every tile's splits ran on one XCD and the FLCE dH product
+  // re-read its 0.62 GB operands ~5x from HBM)
+  const int tiles = pb.tiles_m * pb.tiles_n;
+  split = logical / tiles;
+  const int t = logical - split * tiles;
   const int gsize = pb.group_m * pb.tiles_n;
   const int g = t / gsize;
   const int first_m = g * pb.group_m;
