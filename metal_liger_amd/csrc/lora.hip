@@ -952,9 +952,9 @@ extern "C" int ml_lora_xa(const void* X, int64_t n_tokens, int64_t in_features, 
            (long long)rank_total);
   ML_CHECK(ldx >= in_features && ldx % 8 == 0 && ldo >= rank_total,
            "lora xa: bad leading dimensions");
+  if (n_tokens == 0) return ML_OK;  // (an empty X may have no storage)
   ML_CHECK(X && A && XA, "lora xa: null pointer");
   ML_CHECK(aligned16(X) && aligned16(A), "lora xa: X and A must be 16-byte aligned");
-  if (n_tokens == 0) return ML_OK;
   const int N = (int)n_tokens, K = (int)in_features, R = (int)rank_total;
   const dim3 grid((unsigned)((N + lora::kXaRows - 1) / lora::kXaRows));
   hipStream_t st = (hipStream_t)stream;

@@ -197,10 +197,11 @@ def test_flce_config_full_size(dev):
     torch.cuda.synchronize()
     peak_extra = torch.cuda.max_memory_allocated() - base
     # inputs cloned (2 x copies) + grads (same sizes) + workspace: one bf16
-    # [2048-token chunk, V] buffer (0.62 GB) plus partials; a full [N, V]
-    # logits tensor alone would be N * V * 2 = 2.49 GB on top.
+    # [4096-token chunk, V] buffer (1.24 GB, half of a full [N, V] bf16
+    # logits tensor) plus partials; the reference's fp32 schedule holds an
+    # fp32 copy of W and an fp32 dW (2 x 1.24 GB) besides its logits chunk.
     io = 2 * (hd.numel() + wd.numel()) * 2
-    assert peak_extra - io < 0.35 * N * V * 2, f"extra memory {peak_extra - io:.3e} B"
+    assert peak_extra - io < 0.65 * N * V * 2, f"extra memory {peak_extra - io:.3e} B"
     dh, dw = hg.grad, wg.grad
     # the oracle (fp32, same chunking) run on the GPU
     rl, lse, mask = ref.flce_forward(hd, wd, ld, None, -100, 8192)
