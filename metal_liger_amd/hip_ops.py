@@ -604,6 +604,36 @@ def _flce_operands(hidden, weight, labels, bias):
     return hidden, weight, labels, bias
 
 
+def _flce_pad8(hidden, weight, bias):
+    """bf16 operands whose vocab or hidden size is not a multiple of 8 (the
+    MFMA GEMMs move 8 bf16 per 16-byte access): hidden and weight get zero
+    columns up to a multiple of 8 (no logit changes), weight zero rows whose
+    bias is -inf (exp(-inf) = 0: no share of the softmax, zero gradient).
+    Returns (hidden, weight, bias, V, H) with V, H the original sizes."""
+    N, H = hidden.shape
+    V = weight.shape[0]
+    if V % 8 == 0 and H % 8 == 0:
+        return hidden, weight, bias, V, H
+    V8, H8 = -(-V // 8) * 8, -(-H // 8) * 8
+    if H8 != H:
+        hp = hidden.new_zeros(N, H8)
+        hp[:, :H] = hidden
+        hidden = hp
+    wp = weight.new_zeros(V8, H8)
+    wp[:V, :H] = weight
+    bp = torch.full((V8,), float("-inf"), dtype=bias.dtype if bias is not None else torch.float32,
+                    device=weight.device)
+    bp[:V] = bias if bias is not None else 0.0
+    return hidden, wp, bp, V, H
+
+
+def _flce_unpad(t, rows, cols):
+    """The [rows, cols] block of a gradient computed on padded operands."""
+    if t is None or (t.shape[0] == rows and t.shape[1] == cols):
+        return t
+    return t[:rows, :cols].contiguous()
+
+
 def _flce_f32(hidden, weight, labels, bias, ignore_index, need_dhidden, need_dweight, chunk):
     """fp32 loss, lse, n_valid and (unit grad_output) gradients by the
     vocabulary-chunked schedule (ml_flce_fwd_grad_f32)."""
@@ -630,6 +660,8 @@ def _flce_f32(hidden, weight, labels, bias, ignore_index, need_dhidden, need_dwe
 def flce_fwd(hidden, weight, labels, bias=None, ignore_index: int = -100):
     """Returns (loss 0-d fp32, lse [N] fp32, n_valid [1] fp32)."""
     hidden, weight, labels, bias = _flce_operands(hidden, weight, labels, bias)
+    if hidden.dtype == torch.bfloat16:
+        hidden, weight, bias, _, _ = _flce_pad8(hidden, weight, bias)
     N, H = hidden.shape
     V = weight.shape[0]
     dev = hidden.device
@@ -681,6 +713,7 @@ def flce_fwd_grad(hidden, weight, labels, bias=None, ignore_index: int = -100,
     if hidden.dtype == torch.float32:
         return _flce_f32(hidden, weight, labels, bias, ignore_index, need_dhidden, need_dweight,
                          vocab_chunk)
+    hidden, weight, bias, V0, H0 = _flce_pad8(hidden, weight, bias)
     N, H = hidden.shape
     V = weight.shape[0]
     dev = hidden.device
@@ -698,7 +731,7 @@ def flce_fwd_grad(hidden, weight, labels, bias=None, ignore_index: int = -100,
         N, V, H, int(ignore_index), T, ptr(loss), ptr(lse), ptr(n_valid), ptr(dh), ptr(dw), ptr(ws),
         ws.numel(), stream_of(weight),
     )
-    return loss, lse, n_valid, dh, dw
+    return loss, lse, n_valid, _flce_unpad(dh, N, H0), _flce_unpad(dw, V0, H0)
 
 
 def flce_scale_grads(grad_loss, d_hidden, d_weight):
@@ -725,6 +758,7 @@ def flce_bwd(hidden, weight, labels, bias, ignore_index, lse, n_valid, grad_loss
                                     need_dweight, chunk_size)
         flce_scale_grads(grad_loss, dh, dw)
         return dh, dw
+    hidden, weight, bias, V0, H0 = _flce_pad8(hidden, weight, bias)
     N, H = hidden.shape
     V = weight.shape[0]
     dev = hidden.device
@@ -743,7 +777,7 @@ def flce_bwd(hidden, weight, labels, bias, ignore_index, lse, n_valid, grad_loss
         int(ignore_index), ptr(lse), ptr(n_valid), ptr(g), chunk, ptr(dh), ptr(dw), ptr(ws),
         ws.numel(), stream_of(weight),
     )
-    return dh, dw
+    return _flce_unpad(dh, N, H0), _flce_unpad(dw, V0, H0)
 
 
 # -------------------------------------------------------------------- LoRA --

@@ -57,6 +57,14 @@ def _get_lora_params(linear):
     return W, A, B, scaling
 
 
+def _fp32_path(X: torch.Tensor, *features: int) -> bool:
+    """Whether a LoRA Function runs on the fp32 kernels: activations that are
+    not bf16 (fp16 is upcast), and bf16 activations whose feature sizes are
+    not all multiples of 8 (the bf16 MFMA kernels move 8 elements per access;
+    the fp32 ones take any size, and the result is cast back to bf16)."""
+    return X.dtype != torch.bfloat16 or any(int(f) % 8 for f in features)
+
+
 def _check_float(X: torch.Tensor, what: str):
     if not X.is_floating_point():
         raise TypeError(f"metal_liger_amd {what}: activations must be floating point (got {X.dtype})")
@@ -129,10 +137,11 @@ def _adapter_grads(flat, shapes, dtypes):
 def _lora_linear(X: torch.Tensor, W: torch.Tensor,
                  A: torch.Tensor, B: torch.Tensor, scaling: float) -> torch.Tensor:
     """X W^T + s (X A^T) B^T (ops/fused_lora.py:69-82) on the MFMA engine
-    (bf16 activations: bf16 products; other float dtypes: fp32 products)."""
+    (bf16 activations: bf16 products; other float dtypes, and feature sizes
+    that are not multiples of 8: fp32 products)."""
     _check_float(X, "_lora_linear")
     shape = X.shape
-    if X.dtype != torch.bfloat16:
+    if _fp32_path(X, X.shape[-1], W.shape[0]):
         X2 = _rows_f32(X)
         if A is None or B is None:
             out = cops.gemm_f32([X2], [_f32(W)], False, True, 1.0)
@@ -162,7 +171,7 @@ class _LoRA_QKV(torch.autograd.Function):
                 VW, VA, VB, VS):
         _check_float(X, "LoRA QKV")
         shape = X.shape
-        ctx.fp32 = X.dtype != torch.bfloat16
+        ctx.fp32 = _fp32_path(X, X.shape[-1], QW.shape[0], KW.shape[0], VW.shape[0])
         if ctx.fp32:
             X2 = _rows_f32(X)
             outs, xas = [], []
@@ -246,7 +255,7 @@ class _LoRA_MLP(torch.autograd.Function):
                 DW, DA, DB, DS):  # down projection
         _check_float(X, "LoRA MLP")
         shape = X.shape
-        ctx.fp32 = X.dtype != torch.bfloat16
+        ctx.fp32 = _fp32_path(X, X.shape[-1], GW.shape[0])
         if ctx.fp32:
             X2 = _rows_f32(X)
             gate, xa_g = _lora_out_f32(X2, GW, GA, GB, GS)
@@ -326,7 +335,7 @@ class _LoRA_W(torch.autograd.Function):
     def forward(ctx, X, W, A, B, S):
         _check_float(X, "LoRA projection")
         shape = X.shape
-        ctx.fp32 = X.dtype != torch.bfloat16
+        ctx.fp32 = _fp32_path(X, X.shape[-1], W.shape[0])
         if ctx.fp32:
             X2 = _rows_f32(X)
             out, xa = _lora_out_f32(X2, W, A, B, S)

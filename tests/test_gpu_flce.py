@@ -243,3 +243,30 @@ def test_flce_dw_over_16_token_chunks_full_vocab(dev):
     # same 3.6e-3)
     assert e_dw <= 3.0 * e_ref, (e_dw, e_ref)
     assert torch.allclose(dw.float(), ex_dw, rtol=2e-2, atol=1e-2)
+
+
+@pytest.mark.parametrize("N,H,V", [(77, 100, 1001), (130, 64, 1003), (64, 36, 512)])
+def test_flce_bf16_sizes_not_multiple_of_8(dev, N, H, V):
+    """bf16 with a vocabulary or hidden size that is not a multiple of 8 (the
+    reference takes any size, ops/fused_linear_cross_entropy.py:108-109): the
+    operands are padded to multiples of 8 (zero columns; zero vocab rows with
+    a -inf bias), through the one-pass schedule, the loss-only forward and
+    the vocabulary-chunked backward, with and without a bias, against the
+    oracle at the bf16 bar."""
+    from metal_liger_amd import hip_ops
+    h, w, lab = make_inputs(N, H, V, seed=V, ignore_frac=0.2, w_scale=0.3)
+    for bias in (None, seeded((V,), V + 5, torch.float32)):
+        rl, lse, mask = ref.flce_forward(h, w, lab, bias, -100, 256)
+        rdh, rdw = ref.flce_backward(h, w, lab, lse, mask, torch.tensor(1.0), bias, 256)
+        bd = bias.to(dev) if bias is not None else None
+        loss, olse, nv, dh, dw = hip_ops.flce_fwd_grad(h.to(dev), w.to(dev), lab.to(dev), bd, -100)
+        assert dh.shape == (N, H) and dw.shape == (V, H)
+        assert abs(loss.item() - rl.item()) <= 1e-3 * abs(rl.item())
+        assert_close(olse.cpu(), lse.float(), "lse")
+        check_grads(dh, dw, rdh, rdw, f"one-pass N={N} H={H} V={V} bias={bias is not None}")
+        loss2, lse2, nv2 = hip_ops.flce_fwd(h.to(dev), w.to(dev), lab.to(dev), bd, -100)
+        assert abs(loss2.item() - rl.item()) <= 1e-3 * abs(rl.item())
+        dh2, dw2 = hip_ops.flce_bwd(h.to(dev), w.to(dev), lab.to(dev), bd, -100, lse2, nv2,
+                                    torch.tensor(1.0, device=dev), 256)
+        assert dh2.shape == (N, H) and dw2.shape == (V, H)
+        check_grads(dh2, dw2, rdh, rdw, f"chunked N={N} H={H} V={V}")

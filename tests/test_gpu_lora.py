@@ -291,3 +291,36 @@ def test_lora_xa_rank_products(dev, N, K, R):
     assert out.shape == (N, R) and out.dtype == BF
     expect = X.float() @ A.float().t()
     assert_close(out, expect.to(BF), f"xa N={N} K={K} R={R}")
+
+
+def test_lora_bf16_feature_sizes_not_multiple_of_8(dev):
+    """bf16 activations with feature sizes that are not multiples of 8 (the
+    reference's Functions take any size, ops/fused_lora.py:69-266) run on
+    the fp32 kernels and come back in bf16: QKV, MLP and the single
+    projection against the oracle at the bf16 bar."""
+    from metal_liger_amd.ops.fused_lora import _LoRA_MLP, _LoRA_QKV, _LoRA_W
+    N, IN, r = 70, 100, 8
+    X = seeded((N, IN), 11, BF)
+    qkv = [adapter(o, IN, r, 20 + 3 * i, w_std=0.1, b_std=0.05) for i, o in enumerate((96, 36, 36))]
+    params = [(*a, 2.0) for a in qkv]
+    dys = [seeded((N, o), 40 + i, BF) for i, o in enumerate((96, 36, 36))]
+    outs, dX, leaves = run_qkv(dev, X, params, dys)
+    assert all(o.dtype == BF for o in outs) and dX.dtype == BF
+    flat = [t for p in params for t in p]
+    routs = ref.lora_qkv_forward(X.float(), *f32(flat))
+    for o, ro in zip(outs, routs):
+        assert_close(o, ro.to(BF), "qkv out (odd sizes)")
+    H, I = 100, 260
+    X2 = seeded((N, H), 12, BF)
+    mlp = [adapter(I, H, r, 50, w_std=0.1, b_std=0.05), adapter(I, H, r, 53, w_std=0.1, b_std=0.05),
+           adapter(H, I, r, 56, w_std=0.1, b_std=0.05)]
+    out, dX2, _ = run_mlp(dev, X2, [(*m, 2.0) for m in mlp], seeded((N, H), 60, BF))
+    rout, *_ = ref.lora_mlp_forward(X2.float(), *f32([t for m in mlp for t in (*m, 2.0)]))
+    assert out.dtype == BF and dX2.dtype == BF and dX2.shape == (N, H)
+    assert_close(out, rout.to(BF), "mlp out (odd sizes)")
+    W, A, B = adapter(44, IN, r, 70, w_std=0.1, b_std=0.05)
+    Xd = X.to(dev).requires_grad_(True)
+    Ad, Bd = A.to(dev).requires_grad_(True), B.to(dev).requires_grad_(True)
+    y = _LoRA_W.apply(Xd, W.to(dev), Ad, Bd, 2.0)
+    y.backward(seeded((N, 44), 71, BF).to(dev))
+    assert y.dtype == BF and Xd.grad.shape == (N, IN) and Ad.grad.shape == A.shape
