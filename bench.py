@@ -183,6 +183,26 @@ def time_rotating(fns, stream, rounds=6):
     return min(times)
 
 
+COPY_BYTES = 256 << 20   # per copy: 256 MB read + 256 MB written
+
+
+def copy_ceiling(dev, stream):
+    """What a plain device-to-device copy sustains from HBM on this GPU
+    (torch's copy_ of 256 MB, two source/destination pairs in rotation: a
+    1 GB working set beyond the MALL), timed like the ops' rotating-input
+    lines: the practical ceiling the streaming kernels' GB/s compare with."""
+    import torch
+    n = COPY_BYTES // 2
+    pairs = [(torch.empty(n, dtype=torch.bfloat16, device=dev).fill_(1.0),
+              torch.empty(n, dtype=torch.bfloat16, device=dev)) for _ in range(2)]
+    ms = time_rotating([lambda s=s, d=d: d.copy_(s) for s, d in pairs], stream)
+    nbytes = 2 * COPY_BYTES
+    del pairs
+    return {"bytes": nbytes, "us": round(ms * 1e3, 2), "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1),
+            "hbm_frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "what": "torch copy_ of 256 MB bf16 (read + write), 2 pairs in rotation, graph replay"}
+
+
 def rotating_copies(nbytes_per_launch):
     """Input copies needed so one round of launches touches > 512 MB."""
     return max(2, -(-(FLUSH_BYTES) // max(nbytes_per_launch, 1)))
@@ -930,6 +950,7 @@ def main():
         breakdown["lora_bwd_layer"] = bench_lora_bwd(dev, timer)
     if not args.no_train_step:
         breakdown["train_step_4layer"] = bench_train_step(dev)
+    breakdown["hbm_copy_ceiling"] = copy_ceiling(dev, stream)
     dom_ms = rot["swiglu_bwd"]
     achieved = SWIGLU_BWD_BYTES / (dom_ms * 1e-3) / 1e9
     roofline = {
