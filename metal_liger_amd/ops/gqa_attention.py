@@ -56,6 +56,8 @@ def expanded_kv_attention_forward(module, query, key, value, attention_mask, dro
         key = _repeat_heads(key, groups)
         value = _repeat_heads(value, groups)
     q_len, kv_len = query.shape[2], key.shape[2]
+    if attention_mask is not None and attention_mask.ndim == 4:
+        attention_mask = attention_mask[:, :, :, :kv_len]  # as transformers' sdpa path
     causal = getattr(module, "is_causal", True) if is_causal is None else is_causal
     causal = bool(causal) and q_len > 1 and attention_mask is None
     if causal and kv_len > q_len:

@@ -458,6 +458,18 @@ def test_efficient_attention_matches_sdpa():
             out = patched(input_ids=ids, use_cache=False, **kw).logits
             keep = slice(None) if not kw else (mask[:, :, None] > 0).expand_as(ref)
             assert torch.allclose(out[keep], ref[keep], rtol=1e-4, atol=1e-4), kw
+        # decoding with a key / value cache: a prompt, then one token per call
+        logits = []
+        for m in (base, patched):
+            o = m(input_ids=ids[:, :20], attention_mask=mask[:, :20], use_cache=True)
+            past, step = o.past_key_values, []
+            for t in range(20, 24):
+                o = m(input_ids=ids[:, t:t + 1], attention_mask=mask[:, :t + 1],
+                      past_key_values=past, use_cache=True)
+                past = o.past_key_values
+                step.append(o.logits[:, -1])
+            logits.append(torch.stack(step))
+        assert torch.allclose(logits[1], logits[0], rtol=1e-4, atol=1e-4)
     # query head h reads key / value head h // groups
     kv = torch.arange(2 * 3, dtype=torch.float32).reshape(1, 3, 2, 1)
     rep = _repeat_heads(kv, 2)
