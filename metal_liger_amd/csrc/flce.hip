@@ -572,7 +572,7 @@ int fwd_impl(const bf16* hidden, int64_t ldh, const bf16* weight, int64_t ldw, c
 }
 
 // ------------------------------------------ loss + gradients in one pass --
-constexpr int kDhTargetItems = 512;  // split-K work items for the dH product (~2 per CU)
+constexpr int kDhTargetItems = 256;  // split-K work items for the dH product (~1 per CU)
 
 int dh_ksplit(int T, int H, int V) {
   const int tiles = ((T + 255) / 256) * ((H + 255) / 256);
