@@ -572,14 +572,36 @@ int fwd_impl(const bf16* hidden, int64_t ldh, const bf16* weight, int64_t ldw, c
 }
 
 // ------------------------------------------ loss + gradients in one pass --
-constexpr int kDhTargetItems = 256;  // split-K work items for the dH product (~1 per CU)
+// Split count of the dH product (K = the vocabulary) over its 256 x 256
+// tiles. One workgroup per CU runs at a time, so a launch takes
+// ceil(tiles * ks / CUs) rounds of items 1 / ks of K long, and every split
+// writes (then the reduction reads) fp32 partials of the chunk's dH. The
+// count minimises the estimated time of both (ties to fewer splits):
+//   rounds * V / ks * (us per vocabulary column of a 256 x 256 item at
+//   ~1.2 PFLOP/s over 256 CUs) + ks * T * H * (8 B at ~6 TB/s).
+// (A fixed target of work items left 264 items at 2736-token chunks: a
+// second round of 8 items as long as the first, +34% on the product.)
+constexpr int kDhCUs = 256;                             // MI355X
+constexpr double kDhUsPerColumn = 2.0 * 65536 / 4.6875e6;  // us
+constexpr double kDhUsPerPartial = 8.0 / 6.0e6;             // us per token x hidden
+constexpr int kDhMaxSplit = 64;
 
 int dh_ksplit(int T, int H, int V) {
   const int tiles = ((T + 255) / 256) * ((H + 255) / 256);
   const int k64 = (V + kBK - 1) / kBK;
-  int ks = (kDhTargetItems + tiles - 1) / tiles;
-  ks = ks < 1 ? 1 : ks;
-  return ks < k64 ? ks : k64;
+  const int kmax = std::min(k64, kDhMaxSplit);
+  int best = 1;
+  double best_cost = 0.0;
+  for (int ks = 1; ks <= kmax; ++ks) {
+    const int64_t rounds = ((int64_t)tiles * ks + kDhCUs - 1) / kDhCUs;
+    const double cost = (double)rounds * V / ks * kDhUsPerColumn +
+                        (double)ks * T * H * kDhUsPerPartial;
+    if (ks == 1 || cost < best_cost) {
+      best = ks;
+      best_cost = cost;
+    }
+  }
+  return best;
 }
 
 // dH split-K partial bytes for a chunk of Tc tokens.
