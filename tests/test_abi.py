@@ -70,3 +70,27 @@ def test_unsupported_dtype_is_an_error():
     # host pointers are fine here: the dtype check fails before any launch
     rc = L.ml_swiglu_fwd(p, p, p, 4, 9, None)
     assert rc == 1 and b"dtype" in L.ml_last_error()
+
+
+def test_flce_dh_split_count_fills_its_rounds():
+    """The FLCE dH product splits K (the vocabulary) into work items of
+    256 x 256 tiles, one workgroup per CU (256 CUs). Its split count shows in
+    the workspace query (the fp32 partials: splits x T x H x 4 bytes, the
+    only dH-dependent buffer): at the Qwen3 head (H = 2048, V = 151936) the
+    items of the last round of a launch fill at least 3/4 of the CUs (a fixed
+    item target had left 264 items at 2736-token chunks: a second round of 8
+    items as long as the first) and the config's 4096-token chunks keep two
+    splits."""
+    L = lib()
+    H, V = 2048, 151936
+    al = lambda b: (b + 255) // 256 * 256
+    for T, want in ((4096, 2), (8192, 1), (256, 32), (2736, None), (3072, None), (2048, None)):
+        part = (L.ml_flce_fwd_grad_workspace_bytes(T, V, H, T, 1)
+                - L.ml_flce_fwd_grad_workspace_bytes(T, V, H, T, 0))
+        splits, rem = divmod(part, al(T * H * 4))
+        assert rem == 0 and splits >= 1, (T, part)
+        if want is not None:
+            assert splits == want, (T, splits)
+        items = -(-T // 256) * (H // 256) * splits
+        rounds = -(-items // 256)
+        assert rounds == 1 or items - (rounds - 1) * 256 >= 192, (T, splits, items)
