@@ -649,23 +649,25 @@ def _time_cpu(fn, warmup, reps):
 
 
 def cpu_baseline(seconds: float):
-    """Oracle (reference torch ops restated, CPU) on a bounded sample:
-    SwiGLU on 1024 of the 8192 tokens, RoPE on batch 1 of 4 (tables built
-    as the HF rotary module does, cast to bf16 as HF does)."""
+    """Oracle (reference torch ops restated, CPU) on the headline step at its
+    full shape: SwiGLU fwd + bwd on [8192, 6144] and RoPE fwd + bwd on q
+    [4,16,2048,128], k [4,8,2048,128] (tables built as the HF rotary module
+    does, cast to bf16 as HF does), repeated for about `seconds`."""
     import torch
 
     from oracle import reference_ops as ref
 
-    n = 1024
+    n = N_TOK
     g = seeded((n, INTER), 0, torch.bfloat16)
     u = seeded((n, INTER), 1, torch.bfloat16)
     dy = seeded((n, INTER), 2, torch.bfloat16)
-    q = seeded((1, RHQ, RS, RD), 3, torch.bfloat16)
-    k = seeded((1, RHK, RS, RD), 4, torch.bfloat16)
-    gq = seeded((1, RHQ, RS, RD), 5, torch.bfloat16)
-    gk = seeded((1, RHK, RS, RD), 6, torch.bfloat16)
+    q = seeded((RB, RHQ, RS, RD), 3, torch.bfloat16)
+    k = seeded((RB, RHK, RS, RD), 4, torch.bfloat16)
+    gq = seeded((RB, RHQ, RS, RD), 5, torch.bfloat16)
+    gk = seeded((RB, RHK, RS, RD), 6, torch.bfloat16)
     pos = torch.arange(RS)
-    sample_bytes = 8 * n * INTER * 2 + 2 * 2 * (RHQ + RHK) * RS * RD * 2
+    sample_bytes = 8 * n * INTER * 2 + 2 * 2 * RB * (RHQ + RHK) * RS * RD * 2
+    assert sample_bytes == STEP_BYTES
 
     def once():
         out, sig = ref.swiglu_forward(g, u)
@@ -691,9 +693,10 @@ def cpu_baseline(seconds: float):
         "unit": "GB/s",
         "cores": torch.get_num_threads(),
         "kind": "port",
-        "sample": (f"oracle torch-CPU SwiGLU fwd+bwd on [{n}, {INTER}] bf16 + RoPE fwd+bwd on "
-                   f"q [1,{RHQ},{RS},{RD}], k [1,{RHK},{RS},{RD}] bf16 (tables built per call), "
-                   f"{reps} reps in {el:.1f} s, {sample_bytes} algorithmic bytes per rep"),
+        "sample": (f"full shape: oracle torch-CPU SwiGLU fwd+bwd on [{n}, {INTER}] bf16 + RoPE "
+                   f"fwd+bwd on q [{RB},{RHQ},{RS},{RD}], k [{RB},{RHK},{RS},{RD}] bf16 (tables "
+                   f"built per call), {reps} reps in {el:.1f} s, {sample_bytes} algorithmic bytes "
+                   "per rep"),
         "host": host_cpu(),
     }
 
@@ -830,8 +833,10 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--cpu-full", action="store_true",
-                    help="only the CPU baselines of every config at full shape (one JSON line; "
-                         "minutes of CPU work)")
+                    help="only the CPU baselines of every config at full shape (one JSON line)")
+    ap.add_argument("--cpu-samples", action="store_true",
+                    help="CPU baselines of the configs on bounded samples of their shapes "
+                         "instead of the full shapes (the default; ~30 s of host time)")
     ap.add_argument("--pmc-probe", action="store_true",
                     help="only the launch sequence used for rocprofv3 --pmc traffic counting")
     ap.add_argument("--pmc-mfma-probe", action="store_true",
@@ -993,7 +998,7 @@ def main():
     }
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
-        line["cpu_baselines"] = cpu_baselines(full=False)
+        line["cpu_baselines"] = cpu_baselines(full=not args.cpu_samples)
     print(json.dumps(line), flush=True)
 
 

@@ -182,6 +182,19 @@ def _(q, k, q_weight, k_weight, cos, sin, eps, dq_out, dk_out, need_dq_weight, n
 
 # ------------------------------------------------------------------- FLCE --
 
+@torch.library.custom_op(f"{NS}::flce_fwd", mutates_args=(), device_types=_DEV)
+def flce_fwd(hidden: Tensor, weight: Tensor, labels: Tensor, bias: Optional[Tensor],
+             ignore_index: int, chunk_size: int = 8192) -> tuple[Tensor, Tensor, Tensor]:
+    return hip_ops.flce_fwd(hidden, weight, labels, bias, ignore_index, vocab_chunk=chunk_size)
+
+
+@flce_fwd.register_fake
+def _(hidden, weight, labels, bias, ignore_index, chunk_size=8192):
+    f32 = torch.float32
+    return (hidden.new_empty((), dtype=f32), hidden.new_empty((hidden.shape[0],), dtype=f32),
+            hidden.new_empty((1,), dtype=f32))
+
+
 @torch.library.custom_op(f"{NS}::flce_fwd_grad", mutates_args=(), device_types=_DEV)
 def flce_fwd_grad(hidden: Tensor, weight: Tensor, labels: Tensor, bias: Optional[Tensor],
                   ignore_index: int, need_dhidden: bool, need_dweight: bool,

@@ -657,11 +657,20 @@ def _flce_f32(hidden, weight, labels, bias, ignore_index, need_dhidden, need_dwe
     return loss, lse, n_valid, dh, dw
 
 
-def flce_fwd(hidden, weight, labels, bias=None, ignore_index: int = -100):
-    """Returns (loss 0-d fp32, lse [N] fp32, n_valid [1] fp32)."""
+def flce_fwd(hidden, weight, labels, bias=None, ignore_index: int = -100,
+             vocab_chunk: int = 8192):
+    """The loss alone. Returns (loss 0-d fp32, lse [N] fp32, n_valid [1]
+    fp32). bf16: one logits GEMM over the whole vocabulary whose epilogue
+    keeps per-row (max, sum-exp) partials and stores nothing
+    (ml_flce_fwd); fp32: the vocabulary-chunked schedule's first pass
+    (ml_flce_fwd_grad_f32 with no gradient outputs, vocab_chunk columns per
+    chunk)."""
     hidden, weight, labels, bias = _flce_operands(hidden, weight, labels, bias)
-    if hidden.dtype == torch.bfloat16:
-        hidden, weight, bias, _, _ = _flce_pad8(hidden, weight, bias)
+    if hidden.dtype == torch.float32:
+        loss, lse, n_valid, _, _ = _flce_f32(hidden, weight, labels, bias, ignore_index, False,
+                                             False, vocab_chunk)
+        return loss, lse, n_valid
+    hidden, weight, bias, _, _ = _flce_pad8(hidden, weight, bias)
     N, H = hidden.shape
     V = weight.shape[0]
     dev = hidden.device

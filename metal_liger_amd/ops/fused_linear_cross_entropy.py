@@ -17,8 +17,11 @@ The reference instead recomputes every logits chunk in its backward (four
 GEMMs). ``chunk_size`` keeps its meaning for the vocabulary-chunked backward
 that runs when the same graph is backpropagated a second time
 (retain_graph): that path starts from the saved lse and recomputes.
-Without gradients (no_grad, or nothing requires grad) only the loss is
-computed. dW is skipped when the lm_head weight is frozen.
+The module and the causal-LM loss compute the loss alone (one logits GEMM,
+no gradient buffers) when grad mode is off (``torch.no_grad()``,
+``torch.inference_mode()``), whatever requires grad; inside the
+autograd.Function, which cannot see grad mode, gradients are formed for the
+inputs that require them. dW is skipped when the lm_head weight is frozen.
 
 Semantics kept from the reference: labels are not shifted; ignore_index
 tokens contribute nothing; the mean divides by max(#valid, 1) (all-ignored
@@ -104,6 +107,19 @@ class _FusedLinearCrossEntropyFunction(torch.autograd.Function):
         return grad_hidden, grad_weight, None, None, None, None
 
 
+def _fused_loss(hidden, weight, labels, bias, ignore_index, chunk_size):
+    """The fused loss through the autograd Function, or, with grad mode off
+    (where no graph is recorded and no backward can follow), by the
+    loss-only path: the Function's forward cannot tell grad mode (autograd
+    runs it with grad disabled) and would form the gradients of every input
+    that requires grad."""
+    if torch.is_grad_enabled():
+        return _FusedLinearCrossEntropyFunction.apply(hidden, weight, labels, bias, ignore_index,
+                                                      chunk_size)
+    hidden_c, weight_c, bias_c = _compute_dtype(hidden, weight, bias)
+    return cops.flce_fwd(hidden_c, weight_c, labels, bias_c, ignore_index, chunk_size)[0]
+
+
 class MetalLigerFusedLinearCrossEntropy(nn.Module):
     """Fused lm_head + cross-entropy loss (ops/fused_linear_cross_entropy.py:188-230).
 
@@ -127,10 +143,8 @@ class MetalLigerFusedLinearCrossEntropy(nn.Module):
                      if hidden_states.ndim == 3 else hidden_states.shape[0])
         hidden_flat = hidden_states.reshape(batch_seq, hidden_states.shape[-1])
         labels_flat = labels.reshape(-1)
-        return _FusedLinearCrossEntropyFunction.apply(
-            hidden_flat, self.weight, labels_flat,
-            self.bias, self.ignore_index, self.chunk_size
-        )
+        return _fused_loss(hidden_flat, self.weight, labels_flat, self.bias, self.ignore_index,
+                           self.chunk_size)
 
 
 # ------------------------------------------------------ causal-LM loss hook --
@@ -157,8 +171,7 @@ def causal_lm_loss(hidden_states: torch.Tensor, lm_head: nn.Linear, labels: torc
     y = shift_labels.reshape(-1).to(h.device)
     if y.shape[0] != h.shape[0]:
         raise ValueError(f"fused causal-LM loss: {y.shape[0]} labels for {h.shape[0]} positions")
-    loss = _FusedLinearCrossEntropyFunction.apply(h, lm_head.weight, y, lm_head.bias,
-                                                  ignore_index, chunk_size)
+    loss = _fused_loss(h, lm_head.weight, y, lm_head.bias, ignore_index, chunk_size)
     if num_items_in_batch is not None:
         n_valid = (y != ignore_index).sum().to(loss.dtype)
         if torch.is_tensor(num_items_in_batch):

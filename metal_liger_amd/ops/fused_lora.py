@@ -179,17 +179,20 @@ class _LoRA_QKV(torch.autograd.Function):
                 o, xa = _lora_out_f32(X2, W, A, B, S)
                 outs.append(o.to(X.dtype).view(*shape[:-1], o.shape[-1]))
                 xas.append(xa)
-            ctx.save_for_backward(X2, *xas, *(_f32(W) for W in (QW, KW, VW)),
-                                  *(_f32(A) for A in (QA, KA, VA)), *(_f32(B) for B in (QB, KB, VB)))
+            # the parameters as given (upcast per use in the backward): an fp32
+            # copy of every frozen base weight would live until the backward
+            ctx.save_for_backward(X2, *xas, *(W.detach() for W in (QW, KW, VW)),
+                                  *(A.detach() for A in (QA, KA, VA)),
+                                  *(B.detach() for B in (QB, KB, VB)))
             ctx.scales = [float(QS), float(KS), float(VS)]
             ctx.orig_shape, ctx.x_dtype = shape, X.dtype
             return tuple(outs)
         Xf = hip_ops._bf16_rows(X.reshape(-1, shape[-1]))
-        ranks = {QA.shape[0], KA.shape[0], VA.shape[0]}
-        if len(ranks) != 1:
-            raise ValueError(f"LoRA QKV: q/k/v adapters must share the rank (got {sorted(ranks)})")
-        r = QA.shape[0]
-        rp = _pad_rank(r)
+        # adapters of different ranks (PEFT rank_pattern) are padded to the
+        # largest: zero A rows and B columns add nothing to the output and get
+        # zero gradients, which the backward slices off
+        ranks = [A.shape[0] for A in (QA, KA, VA)]
+        rp = _pad_rank(max(ranks))
         a_stack = _stack_a([QA, KA, VA], rp)
         xa = cops.lora_xa(Xf, a_stack)                         # [N, 3 rp], saved
         Ws = [hip_ops._bf16_rows(W.detach()) for W in (QW, KW, VW)]
@@ -201,7 +204,7 @@ class _LoRA_QKV(torch.autograd.Function):
         outs = cops.lora_qkv_out(Xf, Ws, xa, sbs)
         ctx.save_for_backward(Xf, xa, a_stack, *Ws, *Bs)
         ctx.scales = scales
-        ctx.rank, ctx.rank_p = r, rp
+        ctx.ranks, ctx.rank_p = ranks, rp
         ctx.orig_shape = shape
         ctx.param_dtypes = [(A.dtype, B.dtype) for A, B in ((QA, QB), (KA, KB), (VA, VB))]
         return tuple(o.view(*shape[:-1], o.shape[-1]) for o in outs)
@@ -214,10 +217,10 @@ class _LoRA_QKV(torch.autograd.Function):
             dys = [_rows_f32(d) for d in (dQ, dK, dV)]
             grads, a_ops, b_ops = [], [], []
             for dy, xa, W, A, B, s in zip(dys, xas, Ws, As, Bs, ctx.scales):
-                P, dA, dB = _adapter_grads_f32(dy, X2, xa, B, s)
+                P, dA, dB = _adapter_grads_f32(dy, X2, xa, _f32(B), s)
                 grads.append((dA, dB))
                 a_ops += [dy, P]
-                b_ops += [W, A]
+                b_ops += [_f32(W), _f32(A)]
             dX = cops.gemm_f32(a_ops, b_ops, False, False, 1.0)
             dX = dX.to(ctx.x_dtype).view(*ctx.orig_shape)
             return (dX,
@@ -225,7 +228,7 @@ class _LoRA_QKV(torch.autograd.Function):
                     None, grads[1][0], grads[1][1], None,
                     None, grads[2][0], grads[2][1], None)
         Xf, xa, a_stack, QW, KW, VW, QB, KB, VB = ctx.saved_tensors
-        r, rp = ctx.rank, ctx.rank_p
+        ranks, rp = ctx.ranks, ctx.rank_p
         shape = ctx.orig_shape
         dys = [hip_ops._bf16_rows(d.reshape(-1, d.shape[-1])) for d in (dQ, dK, dV)]
         dX, flat = cops.lora_qkv_bwd(Xf, dys, [QW, KW, VW], a_stack, [QB, KB, VB],
@@ -234,8 +237,8 @@ class _LoRA_QKV(torch.autograd.Function):
         dA, *dBs = _adapter_grads(flat, shapes, [t for pair in ctx.param_dtypes for t in pair])
         grads = []
         for i in range(3):
-            dAi = dA[i * rp:i * rp + r]
-            dBi = dBs[i][:, :r]
+            dAi = dA[i * rp:i * rp + ranks[i]]
+            dBi = dBs[i][:, :ranks[i]]
             grads.append((dAi, dBi))
         dX = dX.view(*shape)
         return (dX,
@@ -263,16 +266,13 @@ class _LoRA_MLP(torch.autograd.Function):
             h = cops.swiglu_fwd(gate, up)                          # silu(gate) * up, fp32
             out, ha = _lora_out_f32(h, DW, DA, DB, DS)
             ctx.save_for_backward(X2, gate, up, h, xa_g, xa_u, ha,
-                                  *(_f32(t) for t in (GW, UW, DW, GA, UA, DA, GB, UB, DB)))
+                                  *(t.detach() for t in (GW, UW, DW, GA, UA, DA, GB, UB, DB)))
             ctx.scales = [float(GS), float(US), float(DS)]
             ctx.orig_shape, ctx.x_dtype = shape, X.dtype
             return out.to(X.dtype).view(*shape[:-1], out.shape[-1])
         Xf = hip_ops._bf16_rows(X.reshape(-1, shape[-1]))
-        ranks = {GA.shape[0], UA.shape[0], DA.shape[0]}
-        if len(ranks) != 1:
-            raise ValueError(f"LoRA MLP: gate/up/down adapters must share the rank (got {sorted(ranks)})")
-        r = GA.shape[0]
-        rp = _pad_rank(r)
+        ranks = [A.shape[0] for A in (GA, UA, DA)]  # padded to the largest, as in _LoRA_QKV
+        rp = _pad_rank(max(ranks))
         scales = [float(GS), float(US), float(DS)]
         a_gu = _stack_a([GA, UA], rp)                            # [2 rp, hidden]
         a_d = _stack_a([DA], rp)                                 # [rp, inter]
@@ -287,14 +287,15 @@ class _LoRA_MLP(torch.autograd.Function):
         ctx.save_for_backward(Xf, gate, up, h, xa_gu, ha_d, a_gu, a_d, GWc, UWc, DWc, BG, BU, BD)
         ctx.scales = scales
         ctx.param_dtypes = [t.dtype for t in (GA, UA, DA, GB, UB, DB)]
-        ctx.rank, ctx.rank_p = r, rp
+        ctx.ranks, ctx.rank_p = ranks, rp
         ctx.orig_shape = shape
         return out.view(*shape)
 
     @staticmethod
     def backward(ctx, dY):
         if ctx.fp32:
-            (X2, gate, up, h, xa_g, xa_u, ha, GW, UW, DW, GA, UA, DA, GB, UB, DB) = ctx.saved_tensors
+            (X2, gate, up, h, xa_g, xa_u, ha, *params) = ctx.saved_tensors
+            GW, UW, DW, GA, UA, DA, GB, UB, DB = (_f32(t) for t in params)
             sg, su, sd = ctx.scales
             dy = _rows_f32(dY)
             PD, dA_D, dB_D = _adapter_grads_f32(dy, h, ha, DB, sd)
@@ -309,7 +310,7 @@ class _LoRA_MLP(torch.autograd.Function):
                     None, dA_U, dB_U, None,
                     None, dA_D, dB_D, None)
         (Xf, gate, up, h, xa_gu, ha_d, a_gu, a_d, GW, UW, DW, BG, BU, BD) = ctx.saved_tensors
-        r, rp = ctx.rank, ctx.rank_p
+        (rg, ru, rd), rp = ctx.ranks, ctx.rank_p
         shape = ctx.orig_shape
         dy = hip_ops._bf16_rows(dY.reshape(-1, dY.shape[-1]))
         dX, flat = cops.lora_mlp_bwd(
@@ -318,9 +319,9 @@ class _LoRA_MLP(torch.autograd.Function):
         dA_GU, dA_D, dB_G, dB_U, dB_D = _adapter_grads(flat, shapes, ctx.param_dtypes)
         dX = dX.view(*shape)
         return (dX,
-                None, dA_GU[:r], dB_G[:, :r], None,        # GW, GA, GB, GS
-                None, dA_GU[rp:rp + r], dB_U[:, :r], None,  # UW, UA, UB, US
-                None, dA_D[:r], dB_D[:, :r], None)          # DW, DA, DB, DS
+                None, dA_GU[:rg], dB_G[:, :rg], None,        # GW, GA, GB, GS
+                None, dA_GU[rp:rp + ru], dB_U[:, :ru], None,  # UW, UA, UB, US
+                None, dA_D[:rd], dB_D[:, :rd], None)          # DW, DA, DB, DS
 
 
 class _LoRA_W(torch.autograd.Function):
@@ -339,7 +340,7 @@ class _LoRA_W(torch.autograd.Function):
         if ctx.fp32:
             X2 = _rows_f32(X)
             out, xa = _lora_out_f32(X2, W, A, B, S)
-            ctx.save_for_backward(X2, xa, _f32(W), _f32(A), _f32(B))
+            ctx.save_for_backward(X2, xa, W.detach(), A.detach(), B.detach())
             ctx.scale, ctx.orig_shape, ctx.x_dtype = float(S), shape, X.dtype
             return out.to(X.dtype).view(*shape[:-1], out.shape[-1])
         Xf = hip_ops._bf16_rows(X.reshape(-1, shape[-1]))
@@ -361,7 +362,8 @@ class _LoRA_W(torch.autograd.Function):
     @staticmethod
     def backward(ctx, dY):
         if ctx.fp32:
-            X2, xa, W, A, B = ctx.saved_tensors
+            X2, xa, *params = ctx.saved_tensors
+            W, A, B = (_f32(t) for t in params)
             dy = _rows_f32(dY)
             P, dA, dB = _adapter_grads_f32(dy, X2, xa, B, ctx.scale)
             dX = cops.gemm_f32([dy, P], [W, A], False, False, 1.0)

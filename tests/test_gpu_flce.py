@@ -168,6 +168,58 @@ def test_flce_no_grad_forward_is_loss_only(dev):
     assert abs(loss.item() - rl.item()) <= 1e-3 * abs(rl.item())
 
 
+def test_flce_no_grad_with_trainable_weight_is_loss_only(dev):
+    """Under torch.no_grad() the module computes the loss alone even though
+    its lm_head weight requires grad (an evaluation loss of a model whose
+    head trains): the right loss, no gradient, and peak memory within the
+    loss-only workspace - the one-pass schedule would hold a [tokens, vocab]
+    bf16 buffer (32 MB here) and a [vocab, hidden] dW (16 MB)."""
+    from metal_liger_amd import _hip
+    from metal_liger_amd.ops.fused_linear_cross_entropy import MetalLigerFusedLinearCrossEntropy
+    N, H, V = 512, 256, 32768
+    h, w, lab = make_inputs(N, H, V, seed=23, w_scale=0.3)
+    head = torch.nn.Linear(H, V, bias=False).to(dev).to(torch.bfloat16)
+    with torch.no_grad():
+        head.weight.copy_(w.to(dev))
+    assert head.weight.requires_grad
+    mod = MetalLigerFusedLinearCrossEntropy(head)
+    hd = h.to(dev).requires_grad_(True)
+    ld = lab.to(dev)
+    torch.cuda.synchronize()
+    base = torch.cuda.memory_allocated()
+    torch.cuda.reset_peak_memory_stats()
+    with torch.no_grad():
+        loss = mod(hd, ld)
+    torch.cuda.synchronize()
+    peak_extra = torch.cuda.max_memory_allocated() - base
+    loss_only_ws = _hip.query("ml_flce_fwd_workspace_bytes", N, V)
+    assert peak_extra <= loss_only_ws + (1 << 20), (peak_extra, loss_only_ws)
+    assert not loss.requires_grad and head.weight.grad is None
+    rl, _, _ = ref.flce_forward(h, w, lab, None, -100, 8192)
+    assert abs(loss.item() - rl.item()) <= 1e-3 * abs(rl.item())
+    # grad mode on: the same module forms the gradients
+    loss2 = mod(hd, ld)
+    loss2.backward()
+    assert head.weight.grad is not None and hd.grad is not None
+    assert abs(loss2.item() - rl.item()) <= 1e-3 * abs(rl.item())
+
+
+def test_flce_fwd_fp32(dev):
+    """The loss-only entry point on fp32 operands (the fp32 schedule's first
+    pass): loss within 1e-3 and lse at the fp32 bar against the oracle."""
+    from metal_liger_amd import hip_ops
+    h, w, lab = make_inputs(192, 128, 3000, seed=29, w_scale=0.3, dtype=torch.float32)
+    b = seeded((3000,), 30, torch.float32)
+    for bias in (None, b):
+        loss, lse, n_valid = hip_ops.flce_fwd(h.to(dev), w.to(dev), lab.to(dev),
+                                              bias.to(dev) if bias is not None else None, -100,
+                                              vocab_chunk=1000)
+        rl, rlse, mask = ref.flce_forward(h, w, lab, bias, -100, 1000)
+        assert abs(loss.item() - rl.item()) <= 1e-3 * abs(rl.item())
+        assert_close(lse, rlse, "fp32 lse")
+        assert n_valid.item() == mask.sum().item()
+
+
 def test_flce_module_flattens_batch(dev):
     from metal_liger_amd.ops.fused_linear_cross_entropy import MetalLigerFusedLinearCrossEntropy
     h, w, lab = make_inputs(2 * 48, 64, 640, seed=13, w_scale=0.3)

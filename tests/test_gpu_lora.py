@@ -203,6 +203,57 @@ def test_lora_mlp_small(dev, N, H, I, r):
         check(Bd.grad.float(), fdAB[2 * i + 1], rdAB[2 * i + 1], f"mlp dB[{i}]")
 
 
+@pytest.mark.parametrize("ranks", [(16, 8, 8), (4, 16, 12)])
+def test_lora_qkv_mixed_ranks(dev, ranks):
+    """q/k/v adapters of different ranks (a PEFT rank_pattern): the
+    reference's per-adapter formulas take any ranks (ops/fused_lora.py:97-171);
+    the bf16 kernels pad every adapter to the largest rank and slice each
+    adapter's dA / dB back. Forward, dX, dA and dB against the oracle."""
+    N, IN, OUTS = 300, 256, (256, 128, 128)
+    X = seeded((N, IN), 4, BF)
+    params = [(*adapter(o, IN, r, 10 * i + 3, b_std=0.05), 2.0)
+              for i, (o, r) in enumerate(zip(OUTS, ranks))]
+    dys = [seeded((N, o), 60 + i, BF) for i, o in enumerate(OUTS)]
+    outs, dX, leaves = run_qkv(dev, X, params, dys)
+    flat = [t for p in params for t in p]
+    rQ, rK, rV = ref.lora_qkv_forward(X, *flat)
+    rdX, *rdAB = ref.lora_qkv_backward(X, *dys, *flat)
+    fQ, fK, fV = ref.lora_qkv_forward(X.float(), *f32(flat))
+    fdX, *fdAB = ref.lora_qkv_backward(X.float(), *f32(dys), *f32(flat))
+    for o, fo, ro, n in zip(outs, (fQ, fK, fV), (rQ, rK, rV), "QKV"):
+        check(o, fo, ro, f"{n} fwd ranks {ranks}")
+    check(dX, fdX, rdX, f"dX ranks {ranks}")
+    for i, (Ad, Bd) in enumerate(leaves):
+        assert Ad.grad.shape == (ranks[i], IN) and Bd.grad.shape == (OUTS[i], ranks[i])
+        check(Ad.grad.float(), fdAB[2 * i], rdAB[2 * i], f"dA[{i}] ranks {ranks}")
+        check(Bd.grad.float(), fdAB[2 * i + 1], rdAB[2 * i + 1], f"dB[{i}] ranks {ranks}")
+
+
+@pytest.mark.parametrize("ranks", [(16, 16, 8), (8, 4, 16)])
+def test_lora_mlp_mixed_ranks(dev, ranks):
+    """gate/up/down adapters of different ranks (ops/fused_lora.py:183-266),
+    against the oracle."""
+    N, H, I = 200, 256, 768
+    X = seeded((N, H), 6, BF)
+    rg, ru, rd = ranks
+    params = [(*adapter(I, H, rg, 81, w_std=0.1, b_std=0.05), 2.0),
+              (*adapter(I, H, ru, 84, w_std=0.1, b_std=0.05), 2.0),
+              (*adapter(H, I, rd, 87, w_std=0.1, b_std=0.05), 2.0)]
+    dY = seeded((N, H), 91, BF)
+    out, dX, leaves = run_mlp(dev, X, params, dY)
+    flat = [t for p in params for t in p]
+    rout, gate, up, h = ref.lora_mlp_forward(X, *flat)
+    rdX, *rdAB = ref.lora_mlp_backward(X, gate, up, h, dY, *flat)
+    fout, fg, fu, fh = ref.lora_mlp_forward(X.float(), *f32(flat))
+    fdX, *fdAB = ref.lora_mlp_backward(X.float(), fg, fu, fh, dY.float(), *f32(flat))
+    check(out, fout, rout, f"mlp out ranks {ranks}")
+    check(dX, fdX, rdX, f"mlp dX ranks {ranks}")
+    for i, (Ad, Bd) in enumerate(leaves):
+        assert Ad.grad.shape == params[i][1].shape and Bd.grad.shape == params[i][2].shape
+        check(Ad.grad.float(), fdAB[2 * i], rdAB[2 * i], f"mlp dA[{i}] ranks {ranks}")
+        check(Bd.grad.float(), fdAB[2 * i + 1], rdAB[2 * i + 1], f"mlp dB[{i}] ranks {ranks}")
+
+
 def _qwen3_layer(seed):
     H, Iq, Ik, I, r = 2048, 2048, 1024, 6144, 16
     X = seeded((8192, H), seed, BF)

@@ -328,6 +328,76 @@ class _OracleFLCE:
         return loss
 
 
+class _OracleCops:
+    """Stand-in for the custom-op module as the fused loss calls it with
+    grad mode off: the loss-only op, answered by the oracle."""
+
+    @staticmethod
+    def flce_fwd(h, w, y, b, ignore_index, chunk_size):
+        from oracle import reference_ops as ref
+        _OracleFLCE.calls += 1
+        loss, lse, mask = ref.flce_forward(h, w, y, b, ignore_index, chunk_size)
+        return loss, lse, mask.sum().float().reshape(1)
+
+
+class _RecordingCops:
+    """Records which FLCE entry point the fused loss called (no compute)."""
+
+    def __init__(self):
+        self.calls = []
+
+    def flce_fwd(self, h, w, y, b, ignore_index, chunk_size):
+        self.calls.append(("flce_fwd", h.dtype))
+        return torch.zeros(()), torch.zeros(h.shape[0]), torch.ones(1)
+
+    def flce_fwd_grad(self, h, w, y, b, ignore_index, need_h, need_w, chunk_size):
+        self.calls.append(("flce_fwd_grad", need_h, need_w))
+        e = torch.empty(0)
+        return (torch.zeros(()), torch.zeros(h.shape[0]), torch.ones(1),
+                torch.zeros_like(h) if need_h else e, torch.zeros_like(w) if need_w else e)
+
+    @staticmethod
+    def maybe(t):
+        return None if t.dim() == 1 and t.shape[0] == 0 else t
+
+    def flce_scale_grads(self, g, dh, dw):
+        self.calls.append(("flce_scale_grads",))
+
+
+def test_fused_loss_routes_no_grad_to_loss_only(monkeypatch):
+    """With grad mode off the module (and the causal-LM loss) call the
+    loss-only entry point even when the lm_head weight requires grad; with
+    grad mode on, the autograd Function's one-pass forward + gradients."""
+    import metal_liger_amd.ops.fused_linear_cross_entropy as fl
+    rec = _RecordingCops()
+    monkeypatch.setattr(fl, "cops", rec)
+    head = torch.nn.Linear(16, 40, bias=False)
+    assert head.weight.requires_grad
+    mod = fl.MetalLigerFusedLinearCrossEntropy(head)
+    h = torch.randn(2, 5, 16, requires_grad=True)
+    y = torch.randint(0, 40, (2, 5))
+    with torch.no_grad():
+        mod(h, y)
+    assert rec.calls == [("flce_fwd", torch.float32)]
+    with torch.inference_mode():
+        fl.causal_lm_loss(h.detach(), head, y)
+    assert rec.calls[-1] == ("flce_fwd", torch.float32) and len(rec.calls) == 2
+    # fp16 operands are upcast to fp32 before the loss-only op, as for the Function
+    with torch.no_grad():
+        fl.MetalLigerFusedLinearCrossEntropy(head.half())(h.half(), y)
+    assert rec.calls[-1] == ("flce_fwd", torch.float32)
+    head.float()
+    rec.calls.clear()
+    loss = mod(h, y)
+    assert rec.calls == [("flce_fwd_grad", True, True)]
+    loss.backward()
+    assert rec.calls[-1] == ("flce_scale_grads",)
+    rec.calls.clear()
+    head.weight.requires_grad_(False)
+    mod(h, y)
+    assert rec.calls == [("flce_fwd_grad", True, False)]
+
+
 def test_causal_lm_loss_hook_matches_transformers(monkeypatch):
     """fuse_lm_loss routes a causal LM's training loss through the fused
     op with transformers' label shift; the logits are not returned; with
@@ -336,6 +406,7 @@ def test_causal_lm_loss_hook_matches_transformers(monkeypatch):
 
     import metal_liger_amd.ops.fused_linear_cross_entropy as fl
     monkeypatch.setattr(fl, "_FusedLinearCrossEntropyFunction", _OracleFLCE)
+    monkeypatch.setattr(fl, "cops", _OracleCops)  # grad mode is off below: the loss-only op
     lm = qwen_tiny.build(seed=6, lora=False, peft_wrap=False)
     ref_lm = copy.deepcopy(lm)
     ids = torch.randint(0, 512, (2, 20), generator=torch.Generator().manual_seed(3))
