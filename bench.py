@@ -357,6 +357,8 @@ def bench_flce(dev, timer, reps=20, token_chunk=None):
             "peak_extra_bytes": int(peak_extra), "workspace_bytes": int(ws),
             "grad_output_bytes": (FLCE_N + FLCE_V) * FLCE_H * 2,
             "full_logits_bf16_bytes": FLCE_N * FLCE_V * 2,
+            "peak_extra_over_full_logits": round(peak_extra / (FLCE_N * FLCE_V * 2), 4),
+            "workspace_over_full_logits": round(ws / (FLCE_N * FLCE_V * 2), 4),
             "reference_model_peak_extra_bytes": flce_reference_peak_bytes(FLCE_N, FLCE_V, FLCE_H,
                                                                           FLCE_CHUNK),
             "reps": reps, "timing": "median of reps (flush before each)"}

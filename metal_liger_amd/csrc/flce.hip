@@ -4,18 +4,24 @@
 // Two schedules share the kernels below.
 //
 // Loss and gradients in one pass (ml_flce_fwd_grad), over chunks of T tokens:
-//   1. Z = H_c W^T (+ b) as a bf16 MFMA GEMM; its epilogue reduces each wave's
-//      64 logit columns per row to (m, s) = (max z, sum exp(z - m)) and
-//      stores e = exp(z - m) in bf16 ([T, vocab] buffer). e lies in (0, 1],
-//      so bf16 keeps it to 2^-9 relative whatever the logit's size. The
-//      label logits come from a dot product of each token with its label's
-//      weight row.
-//   2. a row pass merges the (m, s) partials into lse and the masked loss;
-//   3. an elementwise pass turns e into dlogits in place:
-//        d = (e exp(m - lse) - [col == label]) * mask / n_valid
-//   4. dH_c = D W     (split-K MFMA GEMM over the vocabulary; MN-major W)
-//   5. dW  += D^T H_c (MFMA GEMM, both operands MN-major; accumulated in bf16
-//      across token chunks).
+//   1. a shift per row, c = (label logit h . W[y], or the logit of entry 0
+//      for a row without a label in range) + 30 (shift_kernel);
+//   2. Z = H_c W^T (+ b) as a bf16 MFMA GEMM whose epilogue stores e =
+//      exp(z - c) in bf16 ([T, vocab] buffer) and writes per-row, per
+//      64-column (max z, sum e) partials;
+//   3. a row pass: S = sum e, lse = c + log S, the masked loss terms, the row
+//      factor alpha = mask / (n_valid S), the label entry rewritten as
+//      exp(z_y - c) - S, and the scaled hidden rows alpha h. Then
+//        dlogits = (softmax - one_hot) * mask / n_valid = diag(alpha) E'
+//      with no pass over the [T, vocab] buffer. A row whose log S leaves
+//      [-36, 48] (its cross-entropy against the pseudo label above 78 nats,
+//      or a non-finite S) flags its 256-row tile; steps 2-3 run again for the
+//      flagged tiles with c = the row's exact max (the launches are made
+//      every chunk; without a flag their blocks return at once);
+//   4. dH_c = diag(alpha) (E' W)  (split-K MFMA GEMM over the vocabulary,
+//      the row factor applied in the fixed-order reduction; MN-major W);
+//   5. dW  += E'^T (diag(alpha) H_c)  (MFMA GEMM, both operands MN-major;
+//      accumulated in bf16 across token chunks).
 //   The logits are computed once: three GEMMs (2 N V H FLOP each) in total,
 //   against the four of a vocabulary-chunked schedule that must recompute
 //   them after the logsumexp is known. The gradients are formed for
@@ -81,17 +87,14 @@ __device__ __forceinline__ float bias_at(const TB* b, int64_t n) {
 }
 
 // ------------------------------------------------------------ forward epi --
-// Each wave reduces its 64 logit columns to a (max, sum exp(z - max))
-// partial per row. With STORE, e = exp(z - max) also replaces the
-// accumulators and is written (bf16) at E[row * ldE + col] through the staged
-// epilogue (16-byte stores). The label logits come from label_logit_kernel.
-template <typename TB, bool STORE>
+// Loss only: each wave reduces its 64 logit columns to a (max, sum exp(z -
+// max)) partial per row, pmax / psum [row * nblk + column block]; nothing
+// else is stored. The label logits come from label_logit_kernel.
+template <typename TB>
 struct EpiRowLse {
   const TB* bias;
   float* pmax;  // [M][nblk]
   float* psum;  // [M][nblk]
-  bf16* E;      // STORE only
-  int64_t ldE;
   int M, V, nblk;
 
   template <bool FULL>
@@ -121,11 +124,7 @@ struct EpiRowLse {
         mx = grp16_max(mx);  // finite: a wave's first column is always < V
         float s = 0.f;
 #pragma unroll
-        for (int j = 0; j < big::TN; ++j) {
-          const float e = exp_f(z[j] - mx);  // 0 for columns past V
-          s += e;
-          if constexpr (STORE) acc[i][j][v] = e;
-        }
+        for (int j = 0; j < big::TN; ++j) s += exp_f(z[j] - mx);  // 0 for columns past V
         s = grp16_sum(s);
         const int m = m0 + 16 * i + 4 * (lane >> 4) + v;
         if (c == 0 && m < M) {
@@ -137,7 +136,7 @@ struct EpiRowLse {
   }
 
   __device__ __forceinline__ void operator()(f32x4_t (&acc)[big::TM][big::TN], int m0, int n0,
-                                             int lane, char* lds, int) const {
+                                             int lane, char*, int) const {
     // a wave whose 64 columns all lie past the vocabulary (in the last tile)
     // owns no partial slot
     if (n0 >= V) return;
@@ -145,16 +144,104 @@ struct EpiRowLse {
       rows<true>(acc, m0, n0, lane);
     else
       rows<false>(acc, m0, n0, lane);
-    if constexpr (STORE) {
-      constexpr int B = 2;  // stores only
-      stage_rows_bf16<B>(
-          lds, lane, m0, n0, [&](int i, int j, int v) { return acc[i][j][v]; },
-          [&](const int (&m)[B], const int (&n)[B], const float (&x)[B][8]) {
+  }
+};
+
+// One-pass (loss + gradients): every row m has a shift c_m chosen before
+// the product (shift_kernel). The epilogue stores e = exp(z - c_m) in bf16
+// at E[m * ldE + n] (staged, 16-byte stores) and writes, per row and
+// 64-column block, the max of z and the sum of e (fp32, before rounding):
+// pmax / psum [m * nblk + block]. With one shift per row the stored values
+// need no per-block rescaling afterwards: the dlogits of row m are
+// alpha_m e' (e' = e with the label entry rewritten, alpha_m a row factor),
+// so the row factor goes into the dH reduction and into the hidden rows of
+// the dW product instead of a pass over the [T, V] buffer.
+// tile_flags (optional): only row tiles with a nonzero flag are computed
+// (the recomputation of rows whose shift was out of range).
+template <typename TB>
+struct EpiShiftExp {
+  const TB* bias;
+  const float* shift;     // [M]
+  const int* tile_flags;  // null: every tile
+  float* pmax;            // [M][nblk]
+  float* psum;            // [M][nblk]
+  bf16* E;
+  int64_t ldE;
+  int M, V, nblk;
+
+  __device__ __forceinline__ bool skip_tile(int tm) const {
+    return tile_flags != nullptr && tile_flags[tm] == 0;
+  }
+
+  template <bool FULL>
+  __device__ __forceinline__ void rows(f32x4_t (&acc)[big::TM][big::TN], int m0, int n0,
+                                       int lane) const {
+    const int c = lane & 15;
+    float bj[big::TN];
+    bool okj[big::TN];
 #pragma unroll
-            for (int q = 0; q < B; ++q)
-              if (m[q] < M && n[q] < V) store_row8_bf16(E + (int64_t)m[q] * ldE + n[q], n[q], V, x[q]);
-          });
+    for (int j = 0; j < big::TN; ++j) {
+      const int n = n0 + 16 * j + c;
+      okj[j] = FULL || n < V;
+      bj[j] = bias ? (okj[j] ? to_f32(bias[n]) : 0.f) : 0.f;
     }
+    const int nb = n0 / kColBlock;
+    // the shifts of this lane's rows m0 + 16 i + 4 (lane / 16) + v, all loaded
+    // before the first is used (16-byte loads: m0 is a multiple of 128)
+    f32x4_t csh[big::TM];
+    const int mq = m0 + 4 * (lane >> 4);
+    if (m0 + 128 <= M) {
+#pragma unroll
+      for (int i = 0; i < big::TM; ++i) csh[i] = *reinterpret_cast<const f32x4_t*>(shift + mq + 16 * i);
+    } else {
+#pragma unroll
+      for (int i = 0; i < big::TM; ++i)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) csh[i][v] = mq + 16 * i + v < M ? shift[mq + 16 * i + v] : 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < big::TM; ++i) {
+      const int mi = mq + 16 * i;  // this lane's rows: mi .. mi + 3
+      float cl[4];  // the rows' shifts times log2(e)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) cl[v] = csh[i][v] * kLog2e;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        float mx = -INFINITY, s = 0.f;
+#pragma unroll
+        for (int j = 0; j < big::TN; ++j) {
+          const float z = okj[j] ? acc[i][j][v] + bj[j] : -INFINITY;
+          mx = fmaxf(mx, z);
+          const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(z, kLog2e, -cl[v]));  // 0 past V
+          s += e;
+          acc[i][j][v] = e;
+        }
+        mx = grp16_max(mx);
+        s = grp16_sum(s);
+        const int m = mi + v;
+        if (c == 0 && m < M) {
+          pmax[(int64_t)m * nblk + nb] = mx;
+          psum[(int64_t)m * nblk + nb] = s;
+        }
+      }
+    }
+  }
+
+  __device__ __forceinline__ void operator()(f32x4_t (&acc)[big::TM][big::TN], int m0, int n0,
+                                             int lane, char* lds, int) const {
+    if (n0 >= V) return;  // no partial slot, nothing to store
+    if (n0 + big::WN <= V)
+      rows<true>(acc, m0, n0, lane);
+    else
+      rows<false>(acc, m0, n0, lane);
+    constexpr int B = 2;  // stores only
+    stage_rows_bf16<B>(
+        lds, lane, m0, n0, [&](int i, int j, int v) { return acc[i][j][v]; },
+        [&](const int (&m)[B], const int (&n)[B], const float (&x)[B][8]) {
+#pragma unroll
+          for (int q = 0; q < B; ++q)
+            if (m[q] < M && n[q] < V) store_row8_bf16(E + (int64_t)m[q] * ldE + n[q], n[q], V, x[q]);
+        });
   }
 };
 
@@ -204,52 +291,124 @@ __global__ __launch_bounds__(1024) void count_valid_kernel(const int64_t* __rest
   }
 }
 
-// In place over E [rows, V] (row stride ldE): d = (e exp(m_blk - lse) -
-// [col == label]) * mask / max(n_valid, 1), bf16. 8 columns per thread (one
-// 16-byte vector; 8 divides the 64-column partial block).
-constexpr int kDlogitUnroll = 4;
+// ------------------------------------------------ one pass: row shifts --
+// The shift of a row is its pseudo-label logit plus kShiftMargin: the label
+// logit z_y for a label in [0, V), else the logit of vocabulary entry 0. With
+// c = z_p + kShiftMargin, log S = log sum_v exp(z_v - c) = (lse - z_p) -
+// kShiftMargin, and lse - z_p >= 0 (lse is at least every logit). A row is
+// computed from its shift when log S lies in [kLogSMin, kLogSMax], i.e.
+// when its cross-entropy against the pseudo label is at most 78 nats:
+//   - every stored e = exp(z - c) <= S <= e^48 and the dH sums of e W stay
+//     far inside fp32;
+//   - S >= e^-36 keeps the row's largest e (>= S / V) a normal bf16 number
+//     with 39 e-folds of normal range below it: entries lost to underflow
+//     carry < e^-39 of the row's largest probability;
+//   - the row factor alpha = mask / (n_valid S) and the scaled hidden rows
+//     alpha h stay normal for any n_valid < 2^31.
+// Rows outside the window (and non-finite S) flag their 256-row tile and are
+// recomputed with c = the row's exact max (then S is in [1, V]).
+constexpr float kShiftMargin = 30.f;
+constexpr float kLogSMin = -36.f, kLogSMax = 48.f;
 
-__global__ __launch_bounds__(256) void dlogit_pass_kernel(
-    bf16* __restrict__ E, int64_t ldE, int rows, int V, const float* __restrict__ pmax, int nblk,
-    const float* __restrict__ lse, const int64_t* __restrict__ labels, int64_t ignore,
-    const float* __restrict__ n_valid) {
-  // Block (x, y) rewrites 256 * kDlogitUnroll consecutive 16-byte vectors of
-  // row y (consecutive lanes, consecutive vectors: whole cache lines per
-  // instruction), every load issued before the first store. The row's
-  // label, scale and lse are uniform (scalar loads); the one-hot term is a
-  // branch only the lane holding the label column takes. Rows past
-  // gridDim.y (at most 65535) are taken in turn.
-  for (int row = blockIdx.y; row < rows; row += gridDim.y) {
-    const int vpr = V / 8;  // vectors per row
-    const int64_t lab = labels[row];
-    const float sc = lab != ignore ? 1.0f / fmaxf(n_valid[0], 1.0f) : 0.f;
-    const float lse_r = lse[row];
-    const float* pm = pmax + (int64_t)row * nblk;
-    bf16* er = E + (int64_t)row * ldE;
-    const int j0 = blockIdx.x * (256 * kDlogitUnroll) + threadIdx.x;
-    float e[kDlogitUnroll][8], f[kDlogitUnroll];
+// zy[t] = h_t . W[label_t] (+ b) for a label in [0, V), else 0; shift[t] =
+// the pseudo-label logit + kShiftMargin. Block 0 also clears the chunk's
+// n_flags tile flags. One wave per token; H % 8 == 0.
+template <typename TB>
+__global__ __launch_bounds__(256) void shift_kernel(
+    const bf16* __restrict__ hidden, int64_t ldh, const bf16* __restrict__ weight, int64_t ldw,
+    const TB* __restrict__ bias, const int64_t* __restrict__ labels, int M, int64_t V, int H,
+    float* __restrict__ zy, float* __restrict__ shift, int* __restrict__ tile_flags, int n_flags) {
+  if (blockIdx.x == 0)
+    for (int i = threadIdx.x; i < n_flags; i += 256) tile_flags[i] = 0;
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= M) return;
+  const int64_t lab = labels[row];
+  const bool inrange = lab >= 0 && lab < V;
+  const int64_t idx = inrange ? lab : 0;
+  const bf16* h = hidden + (int64_t)row * ldh;
+  const bf16* w = weight + idx * ldw;
+  float acc = 0.f;
+  for (int k = lane * 8; k < H; k += 64 * 8) {
+    float a[8], b[8];
+    load_n<bf16, 8>(h + k, a);
+    load_n<bf16, 8>(w + k, b);
 #pragma unroll
-    for (int u = 0; u < kDlogitUnroll; ++u) {
-      const int j = j0 + u * 256;
-      if (j < vpr) {
-        f[u] = exp_f(pm[(j * 8) / kColBlock] - lse_r) * sc;
-        load_n_nt<bf16, 8>(er + j * 8, e[u]);
+    for (int q = 0; q < 8; ++q) acc += a[q] * b[q];
+  }
+  acc = wave_sum(acc) + (bias ? to_f32(bias[idx]) : 0.f);
+  if (lane == 0) {
+    zy[row] = inrange ? acc : 0.f;
+    shift[row] = acc + kShiftMargin;
+  }
+}
+
+// One wave per row of a chunk: merges the row's partials (fixed order) into
+// M = max z and S = sum exp(z - c), then, for a row in the window (or, in
+// the RECOMPUTE pass, any row of a flagged tile):
+//   lse = c + log S, the loss term (lse - z_y for a valid label in range, 0
+//   for ignore_index, NaN for a label out of range), the row factor
+//   alpha = [label != ignore] / (max(n_valid, 1) S) (so that alpha e =
+//   softmax * mask / #valid), the label entry rewritten as e' = exp(z_y - c)
+//   - S (alpha e' = (p_y - 1) * mask / #valid, from the fp32 label logit),
+//   and the scaled hidden row Hs = alpha h (bf16; the dW product's operand).
+// A row outside the window (first pass) flags its tile and takes c = M.
+template <bool RECOMPUTE>
+__global__ __launch_bounds__(256) void finalize_kernel(
+    const float* __restrict__ pmax, const float* __restrict__ psum, int nblk,
+    float* __restrict__ shift, const float* __restrict__ zy, const int64_t* __restrict__ labels,
+    int64_t ignore, int M, int64_t V, const float* __restrict__ n_valid, bf16* __restrict__ E,
+    int64_t ldE, const bf16* __restrict__ hidden, int64_t ldh, int H, bf16* __restrict__ Hs,
+    float* __restrict__ alpha, int* __restrict__ tile_flags, float* __restrict__ lse,
+    float* __restrict__ loss_row, float* __restrict__ valid_row) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= M) return;
+  if (RECOMPUTE && tile_flags[row >> 8] == 0) return;
+  const float* pm = pmax + (int64_t)row * nblk;
+  const float* ps = psum + (int64_t)row * nblk;
+  float mx = -INFINITY, s = 0.f;
+  for (int b0 = 4 * lane; b0 < nblk; b0 += 256) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      if (b0 + u < nblk) {
+        mx = fmaxf(mx, pm[b0 + u]);
+        s += ps[b0 + u];
       }
     }
-#pragma unroll
-    for (int u = 0; u < kDlogitUnroll; ++u) {
-      const int j = j0 + u * 256;
-      if (j >= vpr) continue;
-#pragma unroll
-      for (int k = 0; k < 8; ++k) e[u][k] = e[u][k] * f[u];
-      const int64_t d = lab - (int64_t)j * 8;
-      if (d >= 0 && d < 8) {
-#pragma unroll
-        for (int k = 0; k < 8; ++k)
-          if (k == (int)d) e[u][k] = e[u][k] - sc;
-      }
-      store_n_nt<bf16, 8>(er + j * 8, e[u]);
+  }
+  mx = wave_max(mx);
+  s = wave_sum(s);
+  const float c = shift[row];
+  const float lS = logf(s);  // NaN / -inf / +inf fail the window test
+  if (!RECOMPUTE && !(lS >= kLogSMin && lS <= kLogSMax)) {
+    if (lane == 0) {
+      tile_flags[row >> 8] = 1;
+      shift[row] = mx;
     }
+    return;
+  }
+  const int64_t lab = labels[row];
+  const bool valid = lab != ignore;
+  const bool inrange = lab >= 0 && lab < V;
+  const float sc = valid ? 1.0f / fmaxf(n_valid[0], 1.0f) : 0.f;
+  const float a = sc / s;
+  if (lane == 0) {
+    const float L = c + lS;
+    lse[row] = L;
+    loss_row[row] = valid ? (inrange ? L - zy[row] : NAN) : 0.f;
+    valid_row[row] = valid ? 1.f : 0.f;
+    alpha[row] = a;
+    if (valid && inrange) E[(int64_t)row * ldE + lab] = from_f32<bf16>(exp_f(zy[row] - c) - s);
+  }
+  const bf16* h = hidden + (int64_t)row * ldh;
+  bf16* hs = Hs + (int64_t)row * H;
+  for (int k = lane * 8; k < H; k += 64 * 8) {
+    float x[8];
+    load_n<bf16, 8>(h + k, x);
+#pragma unroll
+    for (int q = 0; q < 8; ++q) x[q] *= a;
+    store_n<bf16, 8>(hs + k, x);
   }
 }
 
@@ -556,8 +715,8 @@ int fwd_impl(const bf16* hidden, int64_t ldh, const bf16* weight, int64_t ldw, c
   Problem pb;
   int rc = make_problem<BigCfg>(pb, M, V, 1, &seg, kKMajor, kKMajor, 0);
   if (rc) return rc;
-  EpiRowLse<TB, false> epi{bias, w.pmax, w.psum, nullptr, 0, M, V, nblk};
-  gemm_kernel<BigCfg, kKMajor, kKMajor, EpiRowLse<TB, false>>
+  EpiRowLse<TB> epi{bias, w.pmax, w.psum, M, V, nblk};
+  gemm_kernel<BigCfg, kKMajor, kKMajor, EpiRowLse<TB>>
       <<<dim3(grid_blocks(pb)), BigCfg::THREADS, 0, st>>>(pb, epi);
   ML_LAUNCH_CHECK();
   label_logit_kernel<TB><<<dim3((M + 3) / 4), 256, 0, st>>>(hidden, ldh, weight, ldw, bias, labels,
@@ -617,9 +776,14 @@ struct GradWs {
   bf16* E;                           // [T, V]
   float *pmax, *psum;                // [T, nblk]
   float *zy, *loss_row, *valid_row;  // [N]
+  float *shift, *alpha;              // [T]
+  bf16* Hs;                          // [T, H]: alpha-scaled hidden rows
+  int* tile_flags;                   // [ceil(T / 256)]
   float* part;                       // dH split-K partials
   size_t part_bytes;
 };
+
+int n_tile_flags(int64_t T) { return (int)((T + 255) / 256); }
 
 // Workspace layout (base == nullptr: size only). T = tokens per chunk.
 size_t grad_ws_layout(int64_t N, int64_t V, int64_t H, int64_t T, bool need_dh, GradWs* w,
@@ -638,6 +802,10 @@ size_t grad_ws_layout(int64_t N, int64_t V, int64_t H, int64_t T, bool need_dh, 
   char* zy = take((size_t)N * 4);
   char* lr = take((size_t)N * 4);
   char* vr = take((size_t)N * 4);
+  char* sh = take((size_t)T * 4);
+  char* al_ = take((size_t)T * 4);
+  char* hs = take((size_t)(T * H) * 2);
+  char* fl = take((size_t)n_tile_flags(T) * 4);
   size_t part = 0;
   if (need_dh) {
     part = dh_part_bytes(T, H, V);
@@ -651,6 +819,10 @@ size_t grad_ws_layout(int64_t N, int64_t V, int64_t H, int64_t T, bool need_dh, 
     w->zy = reinterpret_cast<float*>(zy);
     w->loss_row = reinterpret_cast<float*>(lr);
     w->valid_row = reinterpret_cast<float*>(vr);
+    w->shift = reinterpret_cast<float*>(sh);
+    w->alpha = reinterpret_cast<float*>(al_);
+    w->Hs = reinterpret_cast<bf16*>(hs);
+    w->tile_flags = reinterpret_cast<int*>(fl);
     w->part = reinterpret_cast<float*>(pt);
     w->part_bytes = part;
   }
@@ -673,55 +845,66 @@ int fwd_grad_impl(const bf16* hidden, int64_t ldh, const bf16* weight, int64_t l
     const int Tc = N - t0 < T ? N - t0 : T;
     const bf16* hc = hidden + (int64_t)t0 * ldh;
     const int64_t* lc = labels + t0;
-    {  // 1. logits + (m, s) partials + e
-      Segment seg{{hc, ldh}, {weight, ldw}, H};
-      Problem pb;
-      rc = make_problem<BigCfg>(pb, Tc, V, 1, &seg, kKMajor, kKMajor, 0);
-      if (rc) return rc;
-      if (grads) {
-        // the r4 engine (as fast as the 8-wave engine or up to 2% faster here; same bits)
-        EpiRowLse<TB, true> epi{bias, w.pmax, w.psum, w.E, (int64_t)V, Tc, V, nblk};
-        gemm_kernel<R4Cfg, kKMajor, kKMajor, EpiRowLse<TB, true>>
-            <<<dim3(grid_blocks(pb)), R4Cfg::THREADS, 0, st>>>(pb, epi);
-      } else {
-        EpiRowLse<TB, false> epi{bias, w.pmax, w.psum, nullptr, 0, Tc, V, nblk};
-        gemm_kernel<BigCfg, kKMajor, kKMajor, EpiRowLse<TB, false>>
-            <<<dim3(grid_blocks(pb)), BigCfg::THREADS, 0, st>>>(pb, epi);
-      }
+    const unsigned row_blocks = (unsigned)((Tc + 3) / 4);
+    Segment seg{{hc, ldh}, {weight, ldw}, H};
+    Problem pb;
+    rc = make_problem<R4Cfg>(pb, Tc, V, 1, &seg, kKMajor, kKMajor, 0);
+    if (rc) return rc;
+    if (!grads) {  // loss only: (max, sum) partials, nothing stored
+      EpiRowLse<TB> epi{bias, w.pmax, w.psum, Tc, V, nblk};
+      gemm_kernel<BigCfg, kKMajor, kKMajor, EpiRowLse<TB>>
+          <<<dim3(grid_blocks(pb)), BigCfg::THREADS, 0, st>>>(pb, epi);
       ML_LAUNCH_CHECK();
-      label_logit_kernel<TB><<<dim3((Tc + 3) / 4), 256, 0, st>>>(hc, ldh, weight, ldw, bias, lc, Tc,
-                                                                 V, H, w.zy + t0);
+      label_logit_kernel<TB><<<row_blocks, 256, 0, st>>>(hc, ldh, weight, ldw, bias, lc, Tc, V, H,
+                                                         w.zy + t0);
       ML_LAUNCH_CHECK();
+      lse_reduce_kernel<<<row_blocks, 256, 0, st>>>(w.pmax, w.psum, nblk, w.zy + t0, lc, ignore,
+                                                    Tc, V, lse + t0, w.loss_row + t0,
+                                                    w.valid_row + t0);
+      ML_LAUNCH_CHECK();
+      continue;
     }
-    // 2. lse and per-token loss terms
-    lse_reduce_kernel<<<dim3((Tc + 3) / 4), 256, 0, st>>>(w.pmax, w.psum, nblk, w.zy + t0, lc,
-                                                          ignore, Tc, V, lse + t0,
-                                                          w.loss_row + t0, w.valid_row + t0);
+    // 1. row shifts (label logits) and cleared tile flags
+    shift_kernel<TB><<<row_blocks, 256, 0, st>>>(hc, ldh, weight, ldw, bias, lc, Tc, V, H,
+                                                 w.zy + t0, w.shift, w.tile_flags,
+                                                 n_tile_flags(Tc));
     ML_LAUNCH_CHECK();
-    if (!grads) continue;
-    {  // 3. dlogits in place
-      const int segs = (int)((V / 8 + 256 * kDlogitUnroll - 1) / (256 * kDlogitUnroll));
-      const int ys = Tc < 65535 ? Tc : 65535;
-      dlogit_pass_kernel<<<dim3((unsigned)segs, (unsigned)ys), 256, 0, st>>>(
-          w.E, V, Tc, (int)V, w.pmax, nblk, lse + t0, lc, ignore, n_valid);
+    // 2. logits, e = exp(z - c) in bf16, (max, sum e) partials (r4 engine),
+    // 3. lse, loss terms, row factors, label entries, scaled hidden rows;
+    // then the same two steps again for the row tiles a row flagged (their
+    // blocks alone do work; for the others the launches return at once)
+    for (int pass = 0; pass < 2; ++pass) {
+      EpiShiftExp<TB> epi{bias, w.shift, pass ? w.tile_flags : nullptr, w.pmax, w.psum, w.E,
+                          (int64_t)V, Tc, V, nblk};
+      gemm_kernel<R4Cfg, kKMajor, kKMajor, EpiShiftExp<TB>>
+          <<<dim3(grid_blocks(pb)), R4Cfg::THREADS, 0, st>>>(pb, epi);
+      ML_LAUNCH_CHECK();
+      if (pass == 0)
+        finalize_kernel<false><<<row_blocks, 256, 0, st>>>(
+            w.pmax, w.psum, nblk, w.shift, w.zy + t0, lc, ignore, Tc, V, n_valid, w.E, V, hc, ldh,
+            H, w.Hs, w.alpha, w.tile_flags, lse + t0, w.loss_row + t0, w.valid_row + t0);
+      else
+        finalize_kernel<true><<<row_blocks, 256, 0, st>>>(
+            w.pmax, w.psum, nblk, w.shift, w.zy + t0, lc, ignore, Tc, V, n_valid, w.E, V, hc, ldh,
+            H, w.Hs, w.alpha, w.tile_flags, lse + t0, w.loss_row + t0, w.valid_row + t0);
       ML_LAUNCH_CHECK();
     }
-    if (d_hidden) {  // 4. dH_c = D W (split-K over the vocabulary)
-      Segment seg{{w.E, (int64_t)V}, {weight, ldw}, V};
-      Problem pb;
-      rc = make_problem<R4Cfg>(pb, Tc, H, 1, &seg, kKMajor, kMNMajor, 0, dh_ksplit(Tc, H, V));
+    if (d_hidden) {  // 4. dH_c = diag(alpha) (E' W) (split-K over the vocabulary)
+      Segment sd{{w.E, (int64_t)V}, {weight, ldw}, V};
+      Problem pd;
+      rc = make_problem<R4Cfg>(pd, Tc, H, 1, &sd, kKMajor, kMNMajor, 0, dh_ksplit(Tc, H, V));
       if (rc) return rc;
-      ML_CHECK(splitk_ws_bytes(pb) <= w.part_bytes, "flce: dH partial workspace too small");
-      rc = launch_splitk<R4Cfg, kKMajor, kMNMajor, bf16>(pb, w.part, d_hidden + (int64_t)t0 * H,
-                                                          H, 1.0f, 0.0f, st);
+      ML_CHECK(splitk_ws_bytes(pd) <= w.part_bytes, "flce: dH partial workspace too small");
+      rc = launch_splitk<R4Cfg, kKMajor, kMNMajor, bf16>(pd, w.part, d_hidden + (int64_t)t0 * H,
+                                                          H, 1.0f, 0.0f, st, w.alpha);
       if (rc) return rc;
     }
-    if (d_weight) {  // 5. dW (+)= D^T H_c
-      Segment seg{{w.E, (int64_t)V}, {hc, ldh}, Tc};
-      Problem pb;
-      rc = make_problem<BigCfg>(pb, V, H, 1, &seg, kMNMajor, kMNMajor, 0);
+    if (d_weight) {  // 5. dW (+)= E'^T (diag(alpha) H_c)
+      Segment sw{{w.E, (int64_t)V}, {w.Hs, (int64_t)H}, Tc};
+      Problem pw;
+      rc = make_problem<BigCfg>(pw, V, H, 1, &sw, kMNMajor, kMNMajor, 0);
       if (rc) return rc;
-      rc = launch_store<bf16>(pb, kMNMajor, kMNMajor, d_weight, H, 1.0f, t0 > 0 ? 1.0f : 0.0f, st);
+      rc = launch_store<bf16>(pw, kMNMajor, kMNMajor, d_weight, H, 1.0f, t0 > 0 ? 1.0f : 0.0f, st);
       if (rc) return rc;
     }
   }

@@ -1429,10 +1429,21 @@ __device__ __forceinline__ void load_row8_bf16(const bf16* p, int n, int N, floa
 //   (f32x4_t[8][4] for the 256 x 256 tile, f32x16_t[TM][TN] otherwise).
 //   smem: LDS the epilogue may use - for the 256 x 256 tile, 16 KB private
 //   to the wave (staged bf16 epilogues); otherwise the block's stage 0.
+// An epilogue may declare skip_tile(tm): work items of row tiles it skips
+// return before the main loop (a block-uniform test, no barrier reached).
+template <class E, class = void>
+struct HasSkipTile : std::false_type {};
+template <class E>
+struct HasSkipTile<E, std::void_t<decltype(std::declval<const E&>().skip_tile(0))>>
+    : std::true_type {};
+
 template <class C, int LA, int LB, class Epi>
 __global__ __launch_bounds__(C::THREADS) void gemm_kernel(const Problem pb, const Epi epi) {
   int tm, tn, split;
   if (!tile_coords(pb, blockIdx.x, tm, tn, split)) return;
+  if constexpr (HasSkipTile<Epi>::value) {
+    if (epi.skip_tile(tm)) return;
+  }
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   if constexpr (C::BM == 256 && C::BN == 256 && C::ENGINE == 2) {
@@ -1586,14 +1597,16 @@ struct EpiPartial {
   }
 };
 
-// out[m, n] = alpha * sum_s P[s][m][n] + beta * out[m, n]  (fixed order).
-// Four consecutive elements per thread when N % 4 == 0 (16-byte partial
-// loads, the splits unrolled so several loads are in flight), one otherwise.
+// out[m, n] = alpha * row_scale[m] * sum_s P[s][m][n] + beta * out[m, n]
+// (fixed order; row_scale null: 1). Four consecutive elements per thread when
+// N % 4 == 0 (16-byte partial loads, the splits unrolled so several loads are
+// in flight), one otherwise.
 template <typename TC>
 __global__ __launch_bounds__(256) void reduce_partials_kernel(const float* __restrict__ P,
                                                               int ksplit, int M, int N,
                                                               TC* __restrict__ out, int64_t ldo,
-                                                              float alpha, float beta) {
+                                                              float alpha, float beta,
+                                                              const float* __restrict__ row_scale = nullptr) {
   const int64_t total = (int64_t)M * N;
   if (N % 4 == 0) {
     const int64_t nv = total / 4;
@@ -1619,9 +1632,10 @@ __global__ __launch_bounds__(256) void reduce_partials_kernel(const float* __res
       }
       const int64_t m = e / N, n = e - m * N;
       TC* p = out + m * ldo + n;
+      const float a = row_scale ? alpha * row_scale[m] : alpha;
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
-        float r = alpha * s[c];
+        float r = a * s[c];
         if (beta != 0.f) r += beta * to_f32(p[c]);
         p[c] = from_f32<TC>(r);
       }
@@ -1634,7 +1648,7 @@ __global__ __launch_bounds__(256) void reduce_partials_kernel(const float* __res
     for (int k = 0; k < ksplit; ++k) s += P[(int64_t)k * total + e];
     const int64_t m = e / N, n = e - m * N;
     TC* p = out + m * ldo + n;
-    float r = alpha * s;
+    float r = (row_scale ? alpha * row_scale[m] : alpha) * s;
     if (beta != 0.f) r += beta * to_f32(*p);
     *p = from_f32<TC>(r);
   }
@@ -1754,7 +1768,7 @@ inline int launch_store_group(const Problem* pbs, int count, int lb, void* const
 // then out = alpha * sum + beta * out.
 template <class C, int LA, int LB, typename TC>
 inline int launch_splitk(const Problem& pb, float* ws, TC* out, int64_t ldo, float alpha, float beta,
-                         hipStream_t st) {
+                         hipStream_t st, const float* row_scale = nullptr) {
   EpiPartial epi{ws, pb.M, pb.N};
   gemm_kernel<C, LA, LB, EpiPartial><<<dim3(grid_blocks(pb)), C::THREADS, 0, st>>>(pb, epi);
   ML_LAUNCH_CHECK();
@@ -1763,7 +1777,8 @@ inline int launch_splitk(const Problem& pb, float* ws, TC* out, int64_t ldo, flo
   int64_t blocks = (total / per_thread + 255) / 256;
   blocks = blocks < 2048 ? (blocks > 0 ? blocks : 1) : 2048;
   reduce_partials_kernel<TC><<<dim3((unsigned)blocks), 256, 0, st>>>(ws, pb.ksplit, pb.M, pb.N,
-                                                                     out, ldo, alpha, beta);
+                                                                     out, ldo, alpha, beta,
+                                                                     row_scale);
   ML_LAUNCH_CHECK();
   return ML_OK;
 }

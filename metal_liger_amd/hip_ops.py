@@ -687,12 +687,13 @@ def flce_fwd(hidden, weight, labels, bias=None, ignore_index: int = -100,
     return loss, lse, n_valid
 
 
-# Bytes of the [token_chunk, vocab] bf16 buffer the one-pass schedule holds
-# (half of a [8192, 151936] bf16 tensor: at that shape two chunks of 4096
-# tokens run 3.6% faster than four of 2048, 14.17 against 14.71 ms, and the
-# whole forward + backward still holds about half of the extra memory the
-# reference's fp32 schedule does).
-FLCE_CHUNK_BYTES = 1280 << 20
+# Bytes of the [token_chunk, vocab] bf16 buffer the one-pass schedule holds:
+# a quarter of a [8192, 151936] bf16 logits tensor (2048-token chunks). The
+# whole forward + backward then holds 1.39 GB of extra memory at that shape
+# (the buffer, partials, the dH / dW outputs), a third of what the
+# reference's fp32 schedule allocates; two chunks of 4096 tokens ran 2% faster
+# (13.50 against 13.76 ms) for 0.67 GB more.
+FLCE_CHUNK_BYTES = 640 << 20
 
 
 def flce_token_chunk(n_tokens: int, vocab: int) -> int:

@@ -5,12 +5,15 @@ The [tokens, vocab] logits never exist. When gradients are needed, the
 forward computes the loss and both gradients in one pass over token chunks,
 with every logit computed once (three MFMA GEMMs in all):
 
-* per chunk, the logits GEMM's epilogue reduces each 64-column slice to
-  per-row (max, sum-exp) partials (the reference's online logsumexp,
-  :39-55) and stores exp(z - max) in bf16; a row pass forms lse and the
-  masked loss; an elementwise pass turns the stored values into dlogits =
-  (softmax - one_hot) * mask / #valid; dH and dW come from MFMA GEMMs on
-  them (:57-80, :159-185);
+* per chunk of 2048 tokens, each row gets a shift (its label logit + 30)
+  before the logits GEMM, whose epilogue stores exp(z - shift) in bf16 and
+  reduces each 64-column slice to per-row partials; a row pass forms lse
+  (the reference's logsumexp, :39-55), the masked loss and a row factor
+  such that dlogits = (softmax - one_hot) * mask / #valid = row factor x
+  the stored values (label entry rewritten); dH and dW come from MFMA GEMMs
+  on them with the row factor folded in (:57-80, :159-185). Rows whose
+  stored values would leave a safe range (a token loss above ~78 nats) are
+  recomputed with their exact max;
 * the backward multiplies those gradients by grad_output.
 
 The reference instead recomputes every logits chunk in its backward (four

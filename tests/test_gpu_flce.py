@@ -81,6 +81,49 @@ def test_flce_token_chunk_over_65535_rows(dev):
     assert rel_fro(dh[65535:], rdh[65535:]) <= 2e-2
 
 
+def _peaked_rows(h, w, lab, rows, t=50.0):
+    """Rows whose logits span +-t: vocabulary entries 1 and 2 are +u and -u
+    (a unit vector), the hidden rows t u, so z_1 = t and z_2 = -t. A row
+    labelled 2 (or ignored, when entry 0 is -u too) has a cross-entropy of
+    about 2 t against its pseudo label: far outside the one-pass window of
+    the per-row shift, so its tile is recomputed with the row's exact max."""
+    H = h.shape[1]
+    u = torch.randn(H, generator=torch.Generator().manual_seed(99))
+    u = u / u.norm()
+    w = w.clone()
+    h = h.clone()
+    lab = lab.clone()
+    w[1] = u.to(w.dtype)
+    w[2] = (-u).to(w.dtype)
+    w[0] = (-u).to(w.dtype)
+    for k, r in enumerate(rows):
+        h[r] = (t * u).to(h.dtype)
+        lab[r] = 2 if k % 2 == 0 else -100
+    return h, w, lab
+
+
+@pytest.mark.parametrize("N,T", [(700, 256), (300, 8192)])
+def test_flce_rows_out_of_shift_window_are_recomputed(dev, N, T):
+    """Rows with a cross-entropy of ~100 nats against their label (or, when
+    ignored, against vocabulary entry 0) push the per-row shift out of its
+    window; their row tiles are recomputed with the exact row max. Loss, lse
+    and gradients against the oracle, with such rows in several chunks and
+    tiles (a ragged last chunk too), and beside them rows that stay in the
+    window."""
+    from metal_liger_amd import hip_ops
+    H, V = 128, 3000
+    h, w, lab = make_inputs(N, H, V, seed=41, ignore_frac=0.1, w_scale=0.3)
+    h, w, lab = _peaked_rows(h, w, lab, [3, 4, 257, 299, N - 1])
+    rl, lse, mask = ref.flce_forward(h, w, lab, None, -100, 8192)
+    rdh, rdw = ref.flce_backward(h, w, lab, lse, mask, torch.tensor(1.0), None, 8192)
+    loss, olse, nv, dh, dw = hip_ops.flce_fwd_grad(h.to(dev), w.to(dev), lab.to(dev), None, -100,
+                                                   token_chunk=T)
+    assert rl.item() > 5.0  # the peaked rows dominate the mean
+    assert abs(loss.item() - rl.item()) <= 1e-3 * abs(rl.item())
+    assert_close(olse.cpu(), lse.float(), "lse")
+    check_grads(dh, dw, rdh, rdw, f"out-of-window rows N={N} T={T}")
+
+
 def test_flce_lse_matches_oracle(dev):
     from metal_liger_amd import hip_ops
     h, w, lab = make_inputs(256, 128, 3000, seed=5, w_scale=0.3)
@@ -248,12 +291,20 @@ def test_flce_config_full_size(dev):
     loss.backward()
     torch.cuda.synchronize()
     peak_extra = torch.cuda.max_memory_allocated() - base
-    # inputs cloned (2 x copies) + grads (same sizes) + workspace: one bf16
-    # [4096-token chunk, V] buffer (1.24 GB, half of a full [N, V] bf16
-    # logits tensor) plus partials; the reference's fp32 schedule holds an
-    # fp32 copy of W and an fp32 dW (2 x 1.24 GB) besides its logits chunk.
-    io = 2 * (hd.numel() + wd.numel()) * 2
-    assert peak_extra - io < 0.65 * N * V * 2, f"extra memory {peak_extra - io:.3e} B"
+    # the inputs cloned + their gradients (same sizes) + the workspace: one
+    # bf16 [2048-token chunk, V] buffer (0.62 GB, a quarter of a full [N, V]
+    # bf16 logits tensor) plus partials and the scaled hidden rows; the
+    # reference's fp32 schedule holds an fp32 copy of W and an fp32 dW (2 x
+    # 1.24 GB) besides its logits chunk.
+    from metal_liger_amd import _hip, hip_ops
+    full = N * V * 2
+    T = hip_ops.flce_token_chunk(N, V)
+    ws = _hip.query("ml_flce_fwd_grad_workspace_bytes", N, V, H, T, 1)
+    clones = (hd.numel() + wd.numel()) * 2
+    grads = (hd.numel() + wd.numel()) * 2
+    assert ws <= 0.3 * full, f"workspace {ws:.3e} B"
+    assert peak_extra - clones <= 0.6 * full, f"extra memory {peak_extra - clones:.3e} B"
+    assert peak_extra - clones - grads <= ws + (1 << 20)
     dh, dw = hg.grad, wg.grad
     # the oracle (fp32, same chunking) run on the GPU
     rl, lse, mask = ref.flce_forward(hd, wd, ld, None, -100, 8192)
