@@ -147,17 +147,65 @@ struct EpiRowLse {
   }
 };
 
+// Reduction of x[k] (k < 16) over the 16 lanes of each 16-lane group, for
+// 16 values at once, by recursive halving: four exchanges with the partner
+// lane (row_mirror: c <-> 15 - c; row_half_mirror: c <-> c ^ 7; quad_perm
+// xor 2 and xor 1), at each of which a lane keeps the half of its values
+// selected by the bit in which it differs from its partner (bits 3, 2, 1, 0)
+// and adds the partner's copy of that half. Lane c of the group ends with
+// the reduction of value c (60 operations for 16 rows, against 128 for
+// sixteen separate butterflies, and one result per lane instead of a copy
+// of each in every lane).
+template <bool MAX>
+__device__ __forceinline__ float grp16_reduce16(float (&x)[16], int c) {
+  auto op = [](float a, float b) { return MAX ? fmaxf(a, b) : a + b; };
+  {
+    const bool hi = (c >> 3) & 1;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const float send = hi ? x[k] : x[k + 8];
+      const float keep = hi ? x[k + 8] : x[k];
+      x[k] = op(keep, dpp_f<kDppMirror>(send));
+    }
+  }
+  {
+    const bool hi = (c >> 2) & 1;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const float send = hi ? x[k] : x[k + 4];
+      const float keep = hi ? x[k + 4] : x[k];
+      x[k] = op(keep, dpp_f<kDppHalfMirror>(send));
+    }
+  }
+  {
+    const bool hi = (c >> 1) & 1;
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const float send = hi ? x[k] : x[k + 2];
+      const float keep = hi ? x[k + 2] : x[k];
+      x[k] = op(keep, dpp_f<kDppXor2>(send));
+    }
+  }
+  const bool hi = c & 1;
+  const float send = hi ? x[0] : x[1];
+  const float keep = hi ? x[1] : x[0];
+  return op(keep, dpp_f<kDppXor1>(send));
+}
+
 // One-pass (loss + gradients): every row m has a shift c_m chosen before
-// the product (shift_kernel). The epilogue stores e = exp(z - c_m) in bf16
-// at E[m * ldE + n] (staged, 16-byte stores) and writes, per row and
-// 64-column block, the max of z and the sum of e (fp32, before rounding):
-// pmax / psum [m * nblk + block]. With one shift per row the stored values
-// need no per-block rescaling afterwards: the dlogits of row m are
-// alpha_m e' (e' = e with the label entry rewritten, alpha_m a row factor),
-// so the row factor goes into the dH reduction and into the hidden rows of
-// the dW product instead of a pass over the [T, V] buffer.
+// the product (shift_kernel). The epilogue (r4 engine, a wave's whole 128 x
+// 128 sub-tile at once) stores e = exp(z - c_m) in bf16 at E[m * ldE + n]
+// and writes, per row and 128-column block, the max of z and the sum of e
+// (fp32, before rounding): pmax / psum [m * nblk + block]. With one shift
+// per row the stored values need no per-block rescaling afterwards: the
+// dlogits of row m are alpha_m e' (e' = e with the label entry rewritten,
+// alpha_m a row factor), so the row factor goes into the dH reduction and
+// into the hidden rows of the dW product instead of a pass over the [T, V]
+// buffer.
 // tile_flags (optional): only row tiles with a nonzero flag are computed
 // (the recomputation of rows whose shift was out of range).
+constexpr int kShiftBlock = 128;  // columns per partial: one r4 wave's sub-tile
+
 template <typename TB>
 struct EpiShiftExp {
   const TB* bias;
@@ -173,23 +221,20 @@ struct EpiShiftExp {
     return tile_flags != nullptr && tile_flags[tm] == 0;
   }
 
+  // acc[h][i][j][v]: row m0 + 16 i + 4 (lane / 16) + v, column n0 + 64 h +
+  // 16 j + lane % 16. Each e is rounded to bf16 as soon as it is formed and
+  // written to the wave's LDS (16 KB per 128 x 64 half, the staged layout of
+  // stage_rows_bf16: column-major 16 x 16 blocks, 8-byte writes); the halves
+  // are then read back as rows of 8 columns (transposing reads) and stored
+  // with 16-byte stores.
   template <bool FULL>
-  __device__ __forceinline__ void rows(f32x4_t (&acc)[big::TM][big::TN], int m0, int n0,
-                                       int lane) const {
-    const int c = lane & 15;
-    float bj[big::TN];
-    bool okj[big::TN];
-#pragma unroll
-    for (int j = 0; j < big::TN; ++j) {
-      const int n = n0 + 16 * j + c;
-      okj[j] = FULL || n < V;
-      bj[j] = bias ? (okj[j] ? to_f32(bias[n]) : 0.f) : 0.f;
-    }
-    const int nb = n0 / kColBlock;
-    // the shifts of this lane's rows m0 + 16 i + 4 (lane / 16) + v, all loaded
-    // before the first is used (16-byte loads: m0 is a multiple of 128)
+  __device__ __forceinline__ void tile(const f32x4_t (&acc)[2][big::TM][4], int m0, int n0,
+                                       int lane, char* lds) const {
+    const int c = lane & 15, G = lane >> 4;
+    const int mq = m0 + 4 * G;
+    // the shifts of this lane's rows mq + 16 i + v, all loaded before the
+    // first is used (16-byte loads: m0 is a multiple of 128)
     f32x4_t csh[big::TM];
-    const int mq = m0 + 4 * (lane >> 4);
     if (m0 + 128 <= M) {
 #pragma unroll
       for (int i = 0; i < big::TM; ++i) csh[i] = *reinterpret_cast<const f32x4_t*>(shift + mq + 16 * i);
@@ -199,49 +244,101 @@ struct EpiShiftExp {
 #pragma unroll
         for (int v = 0; v < 4; ++v) csh[i][v] = mq + 16 * i + v < M ? shift[mq + 16 * i + v] : 0.f;
     }
+    float bj[2][4];
+    bool okj[2][4];
 #pragma unroll
-    for (int i = 0; i < big::TM; ++i) {
-      const int mi = mq + 16 * i;  // this lane's rows: mi .. mi + 3
-      float cl[4];  // the rows' shifts times log2(e)
+    for (int h = 0; h < 2; ++h)
 #pragma unroll
-      for (int v = 0; v < 4; ++v) cl[v] = csh[i][v] * kLog2e;
+      for (int j = 0; j < 4; ++j) {
+        const int n = n0 + 64 * h + 16 * j + c;
+        okj[h][j] = FULL || n < V;
+        bj[h][j] = bias ? (okj[h][j] ? to_f32(bias[n]) : 0.f) : 0.f;
+      }
+    char* wr = lds + (c * 16 + 4 * G) * 2;
+    const int nb = n0 / kShiftBlock;
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        float mx = -INFINITY, s = 0.f;
+    for (int b = 0; b < 2; ++b) {  // rows of i = 4 b .. 4 b + 3: 16 per lane group
+      float xm[16], xs[16];
 #pragma unroll
-        for (int j = 0; j < big::TN; ++j) {
-          const float z = okj[j] ? acc[i][j][v] + bj[j] : -INFINITY;
-          mx = fmaxf(mx, z);
-          const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(z, kLog2e, -cl[v]));  // 0 past V
-          s += e;
-          acc[i][j][v] = e;
+      for (int ii = 0; ii < 4; ++ii) {
+        const int i = 4 * b + ii;
+        float cl[4], mx[4], sm[4];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          cl[v] = csh[i][v] * kLog2e;
+          mx[v] = -INFINITY;
+          sm[v] = 0.f;
         }
-        mx = grp16_max(mx);
-        s = grp16_sum(s);
-        const int m = mi + v;
-        if (c == 0 && m < M) {
-          pmax[(int64_t)m * nblk + nb] = mx;
-          psum[(int64_t)m * nblk + nb] = s;
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            bf16x4_t w;
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+              float z = acc[h][i][j][v];
+              if (bias) z += bj[h][j];
+              if (!FULL) z = okj[h][j] ? z : -INFINITY;
+              mx[v] = fmaxf(mx[v], z);
+              const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(z, kLog2e, -cl[v]));  // 0 past V
+              sm[v] += e;
+              w[v] = static_cast<bf16>(e);
+            }
+            *reinterpret_cast<bf16x4_t*>(wr + h * r4::EPI_BYTES + (i * 4 + j) * 512) = w;
+          }
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          xm[4 * ii + v] = mx[v];
+          xs[4 * ii + v] = sm[v];
+        }
+      }
+      // lane c of group G gets row 16 (4 b + c / 4) + 4 G + c % 4
+      const float rm = grp16_reduce16<true>(xm, c);
+      const float rs = grp16_reduce16<false>(xs, c);
+      const int m = m0 + 16 * (4 * b + (c >> 2)) + 4 * G + (c & 3);
+      if (m < M) {
+        pmax[(int64_t)m * nblk + nb] = rm;
+        psum[(int64_t)m * nblk + nb] = rs;
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's writes are in LDS
+    __builtin_amdgcn_wave_barrier();
+    typedef __attribute__((address_space(3))) i16x4_t* lp;
+    typedef short i16x8_t __attribute__((ext_vector_type(8)));
+    const int L = lane & 15, a = L >> 2, bq = L & 3;
+    const int cb = 8 * ((lane >> 4) & 1);
+    const int jo = lane >> 5;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const char* rd = lds + h * r4::EPI_BYTES + jo * 512 + ((cb + a) * 16 + 4 * bq) * 2;
+#pragma unroll
+      for (int q = 0; q < big::TM * 2; ++q) {
+        const int i = q >> 1, jp = q & 1;
+        const char* blk = rd + (i * 4 + 2 * jp) * 512;
+        const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lp)(blk));
+        const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lp)(blk + 4 * 32));
+        const int m = m0 + 16 * i + L;
+        const int n = n0 + 64 * h + 16 * (2 * jp + jo) + cb;
+        if (m >= M) continue;
+        bf16* dst = E + (int64_t)m * ldE + n;
+        if (FULL || n + 8 <= V) {
+          *reinterpret_cast<i16x8_t*>(dst) = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+        } else {
+#pragma unroll
+          for (int k = 0; k < 8; ++k)
+            if (n + k < V) dst[k] = __builtin_bit_cast(bf16, k < 4 ? lo[k] : hi[k - 4]);
         }
       }
     }
   }
 
-  __device__ __forceinline__ void operator()(f32x4_t (&acc)[big::TM][big::TN], int m0, int n0,
-                                             int lane, char* lds, int) const {
+  __device__ __forceinline__ void full_tile(f32x4_t (&acc)[2][big::TM][4], int m0, int n0,
+                                            int lane, char* lds) const {
     if (n0 >= V) return;  // no partial slot, nothing to store
-    if (n0 + big::WN <= V)
-      rows<true>(acc, m0, n0, lane);
+    if (n0 + kShiftBlock <= V)
+      tile<true>(acc, m0, n0, lane, lds);
     else
-      rows<false>(acc, m0, n0, lane);
-    constexpr int B = 2;  // stores only
-    stage_rows_bf16<B>(
-        lds, lane, m0, n0, [&](int i, int j, int v) { return acc[i][j][v]; },
-        [&](const int (&m)[B], const int (&n)[B], const float (&x)[B][8]) {
-#pragma unroll
-          for (int q = 0; q < B; ++q)
-            if (m[q] < M && n[q] < V) store_row8_bf16(E + (int64_t)m[q] * ldE + n[q], n[q], V, x[q]);
-        });
+      tile<false>(acc, m0, n0, lane, lds);
   }
 };
 
@@ -836,7 +933,8 @@ int fwd_grad_impl(const bf16* hidden, int64_t ldh, const bf16* weight, int64_t l
                   hipStream_t st) {
   GradWs w;
   grad_ws_layout(N, V, H, T, d_hidden != nullptr, &w, ws);
-  const int nblk = (int)nblocks(V);
+  const int nblk = (int)nblocks(V);                                // loss only: 64 columns
+  const int nsb = (int)((V + kShiftBlock - 1) / kShiftBlock);       // one pass: 128 columns
   const bool grads = d_hidden || d_weight;
   count_valid_kernel<<<1, 1024, 0, st>>>(labels, N, ignore, n_valid);
   ML_LAUNCH_CHECK();
@@ -875,17 +973,17 @@ int fwd_grad_impl(const bf16* hidden, int64_t ldh, const bf16* weight, int64_t l
     // blocks alone do work; for the others the launches return at once)
     for (int pass = 0; pass < 2; ++pass) {
       EpiShiftExp<TB> epi{bias, w.shift, pass ? w.tile_flags : nullptr, w.pmax, w.psum, w.E,
-                          (int64_t)V, Tc, V, nblk};
+                          (int64_t)V, Tc, V, nsb};
       gemm_kernel<R4Cfg, kKMajor, kKMajor, EpiShiftExp<TB>>
           <<<dim3(grid_blocks(pb)), R4Cfg::THREADS, 0, st>>>(pb, epi);
       ML_LAUNCH_CHECK();
       if (pass == 0)
         finalize_kernel<false><<<row_blocks, 256, 0, st>>>(
-            w.pmax, w.psum, nblk, w.shift, w.zy + t0, lc, ignore, Tc, V, n_valid, w.E, V, hc, ldh,
+            w.pmax, w.psum, nsb, w.shift, w.zy + t0, lc, ignore, Tc, V, n_valid, w.E, V, hc, ldh,
             H, w.Hs, w.alpha, w.tile_flags, lse + t0, w.loss_row + t0, w.valid_row + t0);
       else
         finalize_kernel<true><<<row_blocks, 256, 0, st>>>(
-            w.pmax, w.psum, nblk, w.shift, w.zy + t0, lc, ignore, Tc, V, n_valid, w.E, V, hc, ldh,
+            w.pmax, w.psum, nsb, w.shift, w.zy + t0, lc, ignore, Tc, V, n_valid, w.E, V, hc, ldh,
             H, w.Hs, w.alpha, w.tile_flags, lse + t0, w.loss_row + t0, w.valid_row + t0);
       ML_LAUNCH_CHECK();
     }

@@ -1437,6 +1437,17 @@ template <class E>
 struct HasSkipTile<E, std::void_t<decltype(std::declval<const E&>().skip_tile(0))>>
     : std::true_type {};
 
+// An epilogue of the r4 engine may take a wave's whole 128 x 128 sub-tile in
+// one call: full_tile(acc, m0, n0, lane, lds) with acc[h][i][j] the MFMA
+// tile (i, 4 h + j) and lds the wave's 2 x 16 KB; otherwise it is called per
+// 128 x 64 half.
+template <class E, class = void>
+struct HasFullTile : std::false_type {};
+template <class E>
+struct HasFullTile<E, std::void_t<decltype(std::declval<const E&>().full_tile(
+                          std::declval<f32x4_t (&)[2][r4::TM][4]>(), 0, 0, 0,
+                          static_cast<char*>(nullptr)))>> : std::true_type {};
+
 template <class C, int LA, int LB, class Epi>
 __global__ __launch_bounds__(C::THREADS) void gemm_kernel(const Problem pb, const Epi epi) {
   int tm, tn, split;
@@ -1455,8 +1466,12 @@ __global__ __launch_bounds__(C::THREADS) void gemm_kernel(const Problem pb, cons
     const int w = __builtin_amdgcn_readfirstlane(wave);
     char* wl = lds + w * 2 * r4::EPI_BYTES;
     const int em = tm * 256 + (w >> 1) * r4::WM, en = tn * 256 + (w & 1) * r4::WN;
-    epi(acc[0], em, en, tid & 63, wl, split);
-    epi(acc[1], em, en + 64, tid & 63, wl + r4::EPI_BYTES, split);
+    if constexpr (HasFullTile<Epi>::value) {
+      epi.full_tile(acc, em, en, tid & 63, wl);
+    } else {
+      epi(acc[0], em, en, tid & 63, wl, split);
+      epi(acc[1], em, en + 64, tid & 63, wl + r4::EPI_BYTES, split);
+    }
   } else if constexpr (C::BM == 256 && C::BN == 256) {
     __shared__ __attribute__((aligned(16))) char lds[big::STAGES * big::STAGE_BYTES];
     f32x4_t acc[big::TM][big::TN];

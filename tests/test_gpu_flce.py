@@ -304,7 +304,8 @@ def test_flce_config_full_size(dev):
     grads = (hd.numel() + wd.numel()) * 2
     assert ws <= 0.3 * full, f"workspace {ws:.3e} B"
     assert peak_extra - clones <= 0.6 * full, f"extra memory {peak_extra - clones:.3e} B"
-    assert peak_extra - clones - grads <= ws + (1 << 20)
+    # beyond the workspace and the gradients: the loss, lse [N] and n_valid
+    assert peak_extra - clones - grads <= ws + (4 << 20)
     dh, dw = hg.grad, wg.grad
     # the oracle (fp32, same chunking) run on the GPU
     rl, lse, mask = ref.flce_forward(hd, wd, ld, None, -100, 8192)
