@@ -1402,6 +1402,74 @@ __device__ __forceinline__ void stage_rows_bf16(char* lds, int lane, int m0, int
   }
 }
 
+// Staged read-modify-write of a wave's 128 x 64 bf16 sub-tile:
+//   C[m, n] = bf16(bf16(alpha acc) + beta C[m, n])
+// in the layout of stage_rows_bf16. The lane's 16 old row vectors (8
+// columns each) are loaded, kept packed, before the tile is staged, so one
+// memory latency per tile is exposed instead of one per batch of rows.
+__device__ __forceinline__ void stage_rmw_bf16(char* lds, int lane, int m0, int n0,
+                                               const f32x4_t (&acc)[big::TM][big::TN], float alpha,
+                                               float beta, bf16* C, int64_t ldc, int M, int N) {
+  constexpr int TN = big::TN, kVecs = big::TM * big::TN / 2;
+  typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+  const int G = lane >> 4, c = lane & 15;
+  const int L = lane & 15, a = L >> 2, b = L & 3;
+  const int cb = 8 * ((lane >> 4) & 1);
+  const int jo = lane >> 5;
+  u32x4_t old[kVecs];
+#pragma unroll
+  for (int q = 0; q < kVecs; ++q) {
+    const int i = q / (TN / 2), jp = q % (TN / 2);
+    const int m = m0 + 16 * i + L, n = n0 + 16 * (2 * jp + jo) + cb;
+    old[q] = u32x4_t{0u, 0u, 0u, 0u};
+    if (m < M && n + 8 <= N) old[q] = *reinterpret_cast<const u32x4_t*>(C + (int64_t)m * ldc + n);
+  }
+  char* wr = lds + (c * 16 + 4 * G) * 2;
+#pragma unroll
+  for (int i = 0; i < big::TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      bf16x4_t w;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) w[v] = static_cast<bf16>(alpha * acc[i][j][v]);
+      *reinterpret_cast<bf16x4_t*>(wr + (i * TN + j) * 512) = w;
+    }
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's writes are in LDS
+  __builtin_amdgcn_wave_barrier();
+  typedef __attribute__((address_space(3))) i16x4_t* lp;
+  const char* rd = lds + jo * 512 + ((cb + a) * 16 + 4 * b) * 2;
+#pragma unroll
+  for (int q = 0; q < kVecs; ++q) {
+    const int i = q / (TN / 2), jp = q % (TN / 2);
+    const char* blk = rd + (i * TN + 2 * jp) * 512;
+    const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lp)(blk));
+    const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lp)(blk + 4 * 32));
+    const int m = m0 + 16 * i + L, n = n0 + 16 * (2 * jp + jo) + cb;
+    if (m >= M || n >= N) continue;
+    float x[8];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      x[e] = __builtin_bit_cast(float, (uint32_t)(uint16_t)lo[e] << 16);
+      x[4 + e] = __builtin_bit_cast(float, (uint32_t)(uint16_t)hi[e] << 16);
+    }
+    bf16* p = C + (int64_t)m * ldc + n;
+    if (n + 8 <= N) {
+      float y[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const uint32_t w = old[q][k >> 1];
+        const float o = __builtin_bit_cast(float, (k & 1) ? (w & 0xFFFF0000u) : (w << 16));
+        y[k] = x[k] + beta * o;
+      }
+      store_n<bf16, 8>(p, y);
+    } else {
+#pragma unroll
+      for (int k = 0; k < 8; ++k)
+        if (n + k < N) p[k] = from_f32<bf16>(x[k] + beta * to_f32(p[k]));
+    }
+  }
+}
+
 // Stores x[0..7] at p[0..7] as bf16 (one 16-byte store when all 8 columns are
 // inside [.., N), element by element otherwise).
 __device__ __forceinline__ void store_row8_bf16(bf16* p, int n, int N, const float (&x)[8]) {
@@ -1540,6 +1608,10 @@ struct EpiStore {
   __device__ __forceinline__ void operator()(f32x4_t (&acc)[big::TM][big::TN], int m0, int n0,
                                              int lane, char* lds, int) const {
     if constexpr (std::is_same_v<TC, bf16>) {
+      if (beta != 0.f) {
+        stage_rmw_bf16(lds, lane, m0, n0, acc, alpha, beta, C, ldc, M, N);
+        return;
+      }
       stage_rows_bf16(
           lds, lane, m0, n0, [&](int i, int j, int v) { return alpha * acc[i][j][v]; },
           [&](const int (&m)[kStageBatch], const int (&n)[kStageBatch],
