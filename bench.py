@@ -447,23 +447,25 @@ def bench_lora_bwd(dev, timer, reps=20):
             "timing": "median of reps (flush before each)"}
 
 
-def build_train_model(dev, layers=None):
+def build_train_model(dev, layers=None, efficient_attention=True):
     """The 4-layer Qwen3-style LoRA train-step model (tests/qwen_tiny.py,
     build_train_config: hidden 2048, 16 q / 8 kv heads, head_dim 128, MLP
     6144, vocab 151936, tied embeddings, rank-16 LoRA on q, k, v, o, gate,
-    up, down, bf16) with every fused op patched in and its grouped-query
-    attention on SDPA's memory-efficient kernel (efficient_attention); only
-    the adapters train."""
+    up, down, bf16) with every fused op patched in and, with
+    efficient_attention, its grouped-query attention on SDPA's
+    memory-efficient kernel (otherwise transformers' own SDPA call); only the
+    adapters train."""
     from metal_liger_amd import apply_metal_liger_to_qwen3vl
     from tests import qwen_tiny
     model = qwen_tiny.build_train_config(dev, layers or qwen_tiny.TRAIN_LAYERS)
     model = apply_metal_liger_to_qwen3vl(model, fuse_qk_norm_rope=True, fuse_lm_loss=True,
-                                         fuse_residual_norm=True, efficient_attention=True)
+                                         fuse_residual_norm=True,
+                                         efficient_attention=efficient_attention)
     qwen_tiny.freeze_all_but_lora(model)
     return model
 
 
-def bench_train_step(dev, steps=5, warmup=2):
+def bench_train_step(dev, steps=5, warmup=2, efficient_attention=True):
     """4-layer Qwen3-style LoRA train step: token ids [4, 2048] uniform in
     [0, 151936), forward through the patched decoder (fused RMSNorm, SwiGLU,
     LoRA QKV / MLP / o_proj, q/k norm + RoPE from the rotary module's tables,
@@ -472,15 +474,17 @@ def bench_train_step(dev, steps=5, warmup=2):
     fused linear cross-entropy (transformers' label shift: the last position
     of each sequence ignored; no logits formed), backward, AdamW on the
     adapters.
-    Attention is torch's scaled_dot_product_attention over key / value heads
-    repeated to the 16 query heads, on its memory-efficient kernel (flash
-    after it; an unavailable kernel raises instead of falling back to the
-    batched-matmul path). tokens/s = 8192 / step time."""
+    Attention is torch's scaled_dot_product_attention: with
+    efficient_attention over key / value heads repeated to the 16 query
+    heads, on its memory-efficient kernel; without it, transformers' own GQA
+    call (enable_gqa, the flash kernel). Either way an unavailable kernel
+    raises instead of falling back to the batched-matmul path. tokens/s =
+    8192 / step time."""
     import torch
     from torch.nn.attention import SDPBackend, sdpa_kernel
 
     from tests import qwen_tiny
-    model = build_train_model(dev)
+    model = build_train_model(dev, efficient_attention=efficient_attention)
     model.train()
     params = [p for p in model.parameters() if p.requires_grad]
     opt = torch.optim.AdamW(params, lr=1e-4, foreach=True)
@@ -510,6 +514,8 @@ def bench_train_step(dev, steps=5, warmup=2):
         torch.cuda.synchronize()
         dt = (time.perf_counter() - t0) / steps
     last = loss.item()
+    del model, opt, params
+    torch.cuda.empty_cache()
     if not (math.isfinite(first) and math.isfinite(last)):
         raise RuntimeError(f"train step: non-finite loss {first} -> {last}")
     n_tok = qwen_tiny.TRAIN_B * qwen_tiny.TRAIN_S
@@ -517,7 +523,10 @@ def bench_train_step(dev, steps=5, warmup=2):
             "tokens_per_s": round(n_tok / dt, 1), "loss_first": round(first, 4),
             "loss_last": round(last, 4), "steps": steps, "warmup": warmup,
             "includes": "fwd + FLCE loss (model(input_ids, labels=input_ids, use_cache=False)) + bwd + AdamW on LoRA params",
-            "attention": "torch SDPA, memory-efficient kernel, key/value heads repeated (efficient_attention=True)"}
+            "attention": ("torch SDPA, memory-efficient kernel, key/value heads repeated "
+                          "(efficient_attention=True)" if efficient_attention else
+                          "transformers' SDPA call with enable_gqa (flash kernel; "
+                          "efficient_attention=False)")}
 
 
 def pmc_probe(dev):
@@ -957,6 +966,10 @@ def main():
         breakdown["lora_bwd_layer"] = bench_lora_bwd(dev, timer)
     if not args.no_train_step:
         breakdown["train_step_4layer"] = bench_train_step(dev)
+        # the same step with transformers' own attention call: what the fused
+        # ops alone give, without the opt-in attention routing
+        breakdown["train_step_4layer_hf_attention"] = bench_train_step(dev,
+                                                                       efficient_attention=False)
     breakdown["hbm_copy_ceiling"] = copy_ceiling(dev, stream)
     dom_ms = rot["swiglu_bwd"]
     achieved = SWIGLU_BWD_BYTES / (dom_ms * 1e-3) / 1e9
