@@ -282,11 +282,17 @@ int ml_flce_bwd(const void* hidden, int64_t ldh, const void* weight, int64_t ldw
  * _FusedLinearCrossEntropyFunction uses; replaces its forward + backward,
  * ops/fused_linear_cross_entropy.py:93-185, whose backward recomputes every
  * logits chunk). Tokens go in chunks of token_chunk: per chunk one bf16
- * [token_chunk, vocab] workspace buffer holds exp(z - max) and then the
- * dlogits, dH rows come from a split-K GEMM and dW accumulates (bf16).
- * Outputs as ml_flce_fwd, plus d_hidden [n_tokens, hidden_size] and d_weight
- * [vocab, hidden_size] (bf16, dense; either may be NULL) formed for
- * d(loss) = 1. With both NULL this is the loss-only forward.
+ * [token_chunk, vocab] workspace buffer holds exp(z - c) with one shift c
+ * per row (the row's label logit + 30; rows whose values would leave the
+ * safe range, a token loss above ~78 nats, are recomputed with their exact
+ * max), so that the dlogits are a row factor times the buffer (label entry
+ * rewritten): dH rows come from a split-K GEMM whose reduction applies the
+ * row factors and dW accumulates (bf16) from the buffer and the
+ * factor-scaled hidden rows. Outputs as ml_flce_fwd, plus d_hidden
+ * [n_tokens, hidden_size] and d_weight [vocab, hidden_size] (bf16, dense;
+ * either may be NULL) formed for d(loss) = 1. With both NULL this is the
+ * loss-only forward (its workspace query still counts the buffer; the
+ * smaller ml_flce_fwd is the loss-only entry point).
  */
 size_t ml_flce_fwd_grad_workspace_bytes(int64_t n_tokens, int64_t vocab, int64_t hidden_size,
                                         int64_t token_chunk, int need_dhidden);
