@@ -9,7 +9,8 @@
 //   - 8 waves, two per SIMD in ping-pong, k-tiles of 32, four LDS stages
 //     (see "256 x 256" below): the FLCE logits (row-LSE epilogue) and dW
 //     (MN-major A) products;
-//   - r4: 4 waves of 128 x 128, k-tiles of 64, two stages (see "r4" below):
+//   - r4: 4 waves of 128 x 128, k-tiles of 64, five 32 KB operand slots
+//     (see "r4" below):
 //     the products with a K-major A and a store or split-K epilogue (LoRA
 //     forward / dX / dH, FLCE dH, the plain GEMM entry points).
 // Narrow tiles Cfg<BM, BN, WAVES_M> (256 x 32, 64 x 256: the rank-r LoRA
@@ -59,9 +60,9 @@ constexpr int kRowBytes = kBK * 2;  // 128
 constexpr int kXcds = 8;
 
 // Default m-tiles per tile-order group (group_m = 0): with 32 blocks
-// resident per XCD, groups of 8 give each XCD an 8 x 4 patch of tiles.
+// resident per XCD, groups of 4 give each XCD a 4 x 8 patch of tiles.
 #ifndef ML_GEMM_GROUP_M
-#define ML_GEMM_GROUP_M 8
+#define ML_GEMM_GROUP_M 4
 #endif
 
 
@@ -987,25 +988,31 @@ __device__ __forceinline__ void big_mainloop(const Problem& pb, int tm, int tn, 
 // K segment), so rows / k-rows past the end read zeros; per lane, K-major
 // chunks past the segment's K and MN-major columns past N get an offset past
 // every range (zeros as well). No load is ever issued out of the tensor.
-// Pipeline, per k-tile t (stage t % 2 holds t):
+// Pipeline: the 160 KB of LDS are five 32 KB operand slots; k-tile t sits
+// in two of them, k-tile t + 1 in two more, and one is free. Per k-tile t:
 //   phase 0: the 64 MFMAs of k-step 0 (fragments in registers), interleaved
-//            with the fragment reads of k-step 1; then each wave waits for its
-//            loads of k-tile t + 1 and its LDS reads, and a barrier publishes
-//            k-tile t + 1 and retires every read of stage t % 2;
+//            with the fragment reads of k-step 1 and the 8 A loads of k-tile
+//            t + 2 into the free slot (one every eighth MFMA); then each wave
+//            waits for its loads of k-tile t + 1 and its LDS reads, and a
+//            barrier publishes k-tile t + 1 and frees t's two slots;
 //   phase 1: the 64 MFMAs of k-step 1, interleaved with the fragment reads of
-//            k-step 0 of k-tile t + 1 and the 16 loads of k-tile t + 2 into
-//            stage t % 2.
+//            k-step 0 of k-tile t + 1 and the 8 B loads of k-tile t + 2 into
+//            t's A slot (t's B slot is the next free slot).
+// A wave issues its loads in order with its MFMAs, so a load the memory
+// pipeline cannot yet take holds the MFMAs behind it: the fifth slot lets
+// the 16 loads of a k-tile spread over both phases instead of one (with two
+// 64 KB stages and all 16 in phase 1 the products ran 1-2% slower; with
+// them bunched into the first half of phase 1, 2-4% slower still).
 namespace r4 {
 constexpr int THREADS = 256;
 constexpr int BK = 64;
 constexpr int TM = 8, TN = 8;
 constexpr int WM = 128, WN = 128;
-constexpr int OP_BYTES = 256 * BK * 2;      // 32 KB per operand per stage
-constexpr int STAGE_BYTES = 2 * OP_BYTES;   // 64 KB
-constexpr int LDS_BYTES = 2 * STAGE_BYTES;  // two stages
+constexpr int OP_BYTES = 256 * BK * 2;      // 32 KB: one operand of one k-tile
+constexpr int LDS_BYTES = 5 * OP_BYTES;    // five operand slots
 constexpr int LOADS = 8;                    // 1-KB loads per wave per operand per k-tile
 constexpr int EPI_BYTES = 16384;            // per wave per 128 x 64 half of its sub-tile
-static_assert(4 * 2 * EPI_BYTES <= LDS_BYTES, "epilogue LDS inside the stages");
+static_assert(4 * 2 * EPI_BYTES <= LDS_BYTES, "epilogue LDS inside the slots");
 constexpr uint32_t kOob = 0x80000000u;  // past every resource range used here
 constexpr int64_t kRangeMax = 0x7FFFFFFF;
 constexpr int kRsrcFlags = 0x00020000;  // raw buffer, 32-bit data format
@@ -1162,7 +1169,7 @@ struct R4Frags {
   bf16x8_t a[r4::TM], b[r4::TN];
 };
 
-// Main loop of the r4 engine; lds holds two stages (A tile, then B tile).
+// Main loop of the r4 engine; lds holds the five operand slots.
 // Wave w computes rows 128 (w >> 1) .. + 127 and columns 128 (w & 1) .. +
 // 127 of the block tile; acc[h][i][j] is MFMA tile (i, 4 h + j).
 template <int LA, int LB>
@@ -1233,65 +1240,81 @@ __device__ __forceinline__ void r4_mainloop(const Problem& pb, int tm, int tn, i
       }
     }
   };
-  // Load w (0 .. 15; A for w < 8) of the current resources into stage `stage`.
-  auto load = [&](char* stage, int w) __attribute__((always_inline)) {
-    const int i = w & 7;
-    char* dst = stage + (w < 8 ? 0 : r4::OP_BYTES) + (wave + 4 * i) * 1024;
-    if (w < 8)
-      buf_load_lds(rsa, va[i & 1] + (uint32_t)i * sa, dst);
-    else
+  // Load i (0 .. 7) of operand A (OPB false) or B of the current resources
+  // into the operand slot `slot`.
+  auto load = [&](auto opb, char* slot, int i) __attribute__((always_inline)) {
+    char* dst = slot + (wave + 4 * i) * 1024;
+    if constexpr (decltype(opb)::value)
       buf_load_lds(rsb, vb[i & 1] + (uint32_t)i * sb, dst);
+    else
+      buf_load_lds(rsa, va[i & 1] + (uint32_t)i * sa, dst);
   };
+  using OpA = std::integral_constant<bool, false>;
+  using OpB = std::integral_constant<bool, true>;
 
+  // Five 32 KB operand slots: k-tile t in (ca, cb), t + 1 in (na, nb), and
+  // a free slot fr. Phase 0 of k-tile t loads A of t + 2 into fr; phase 1
+  // (after the barrier has freed ca and cb) loads B of t + 2 into ca.
+  char* ca = lds;
+  char* cb = lds + r4::OP_BYTES;
+  char* na = lds + 2 * r4::OP_BYTES;
+  char* nb = lds + 3 * r4::OP_BYTES;
+  char* fr = lds + 4 * r4::OP_BYTES;
   R4Frags f0, f1;
-  // Prologue: k-tile 0 into stage 0 and k-tile 1 into stage 1; k-tile 0
-  // published, its k-step 0 fragments read.
   next_tile();
 #pragma unroll
-  for (int w = 0; w < 2 * r4::LOADS; ++w) load(lds, w);
+  for (int i = 0; i < r4::LOADS; ++i) load(OpA{}, ca, i);
+#pragma unroll
+  for (int i = 0; i < r4::LOADS; ++i) load(OpB{}, cb, i);
   next_tile();
 #pragma unroll
-  for (int w = 0; w < 2 * r4::LOADS; ++w) load(lds + r4::STAGE_BYTES, w);
+  for (int i = 0; i < r4::LOADS; ++i) load(OpA{}, na, i);
+#pragma unroll
+  for (int i = 0; i < r4::LOADS; ++i) load(OpB{}, nb, i);
   __builtin_amdgcn_s_waitcnt(big::wait_vm(2 * r4::LOADS));  // this wave's k-tile 0 landed
   lds_barrier();
 #pragma unroll
-  for (int j = 0; j < r4::TN; ++j) f0.b[j] = r4_read_frag<LB>(lds + r4::OP_BYTES, fb, 0, j);
+  for (int j = 0; j < r4::TN; ++j) f0.b[j] = r4_read_frag<LB>(cb, fb, 0, j);
 #pragma unroll
-  for (int i = 0; i < r4::TM; ++i) f0.a[i] = r4_read_frag<LA>(lds, fa, 0, i);
+  for (int i = 0; i < r4::TM; ++i) f0.a[i] = r4_read_frag<LA>(ca, fa, 0, i);
 
   // One phase: the 64 MFMAs of fragment set fc, with the reads of the next
-  // k-step (k-step NS of stage `src`) into fn, interleaved; phase 0 also
-  // moves the cursor to k-tile t + 2 (next_tile), phase 1 issues that
-  // k-tile's loads into stage `dst`.
-  auto phase = [&](auto pc, R4Frags& fc, R4Frags& fn, const char* src, char* dst)
+  // k-step (k-step NS of slots sa_/sb_) into fn interleaved; phase 0 moves
+  // the cursor to k-tile t + 2 and issues its A loads into ld, phase 1 its
+  // B loads into ld.
+  auto phase = [&](auto pc, R4Frags& fc, R4Frags& fn, const char* ra_, const char* rb_, char* ld)
                    __attribute__((always_inline)) {
     constexpr int P = decltype(pc)::value;
     constexpr int NS = P ^ 1;
+    if constexpr (P == 0) next_tile();
     static_for<r4::TM * r4::TN>([&](auto qc) {
       constexpr int q = decltype(qc)::value;
       constexpr int i = q / r4::TN, j = q % r4::TN;
-      // next k-step: B fragments at slots 0, 2, .., 14, A at 16, 18, .., 30
-      // (all sixteen reads land well before the next phase's first MFMA)
-      if constexpr ((q & 1) == 0 && q < 16) fn.b[q >> 1] = r4_read_frag<LB>(src + r4::OP_BYTES, fb, NS, q >> 1);
-      if constexpr ((q & 1) == 0 && q >= 16 && q < 32) fn.a[(q - 16) >> 1] = r4_read_frag<LA>(src, fa, NS, (q - 16) >> 1);
-      if constexpr (P == 1 && (q & 3) == 3) load(dst, q >> 2);
-      // the cursor's scalar work for k-tile t + 2 runs in the shadow of
-      // phase 0's MFMAs (phase 0 issues no loads)
-      if constexpr (P == 0 && q == 40) next_tile();
+      if constexpr ((q & 1) == 0 && q < 16) fn.b[q >> 1] = r4_read_frag<LB>(rb_, fb, NS, q >> 1);
+      if constexpr ((q & 1) == 0 && q >= 16 && q < 32) fn.a[(q - 16) >> 1] = r4_read_frag<LA>(ra_, fa, NS, (q - 16) >> 1);
+      if constexpr ((q & 7) == 3) {
+        if constexpr (P == 0) load(OpA{}, ld, q >> 3);
+        else load(OpB{}, ld, q >> 3);
+      }
       r4_mfma(acc[j >> 2][i][j & 3], fc.a[i], fc.b[j]);
       __builtin_amdgcn_sched_barrier(0);
     });
   };
   for (int t = 0; t < nk; ++t) {
-    const int cur = (t & 1) * r4::STAGE_BYTES;
-    char* cs = lds + cur;
-    char* ns = lds + (cur ^ r4::STAGE_BYTES);
-    phase(std::integral_constant<int, 0>{}, f0, f1, cs, ns);
-    // this wave's loads of k-tile t + 1 have landed (no other vector memory
-    // operation is in flight); the barrier publishes them
-    __builtin_amdgcn_s_waitcnt(big::kWaitVm0);
+    phase(std::integral_constant<int, 0>{}, f0, f1, ca, cb, fr);
+    // this wave's loads of k-tile t + 1 have landed (only the A loads of
+    // t + 2 may still be in flight); the barrier publishes them and frees
+    // ca and cb
+    __builtin_amdgcn_s_waitcnt(big::wait_vm(r4::LOADS));
     lds_barrier();
-    phase(std::integral_constant<int, 1>{}, f1, f0, ns, cs);
+    phase(std::integral_constant<int, 1>{}, f1, f0, na, nb, ca);
+    char* const oa = ca;
+    char* const ob = cb;
+    ca = na;
+    cb = nb;
+    na = fr;
+    nb = oa;
+    fr = ob;
   }
   // the epilogue reads the accumulators: wait for the last MFMAs (the
   // asm statements carry no hazard information for the compiler), and for
