@@ -433,8 +433,8 @@ def bench_lora_bwd(dev, timer, reps=20):
     def qkv():
         hip_ops.lora_qkv_bwd(x, dqkv, Wqkv, a_qkv, Bqkv, [s, s, s], xa, r)
 
-    def mlp():
-        hip_ops.lora_mlp_bwd(x, gate, up, hmid, dy, WG, WU, WD, a_gu, a_d, BG, BU, BD,
+    def mlp():  # h recomputed from gate and up, as the autograd path calls it
+        hip_ops.lora_mlp_bwd(x, gate, up, None, dy, WG, WU, WD, a_gu, a_d, BG, BU, BD,
                              [s, s, s], xa_gu, ha_d, r)
 
     q = timer.time(qkv, reps)

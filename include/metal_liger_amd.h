@@ -380,6 +380,11 @@ int ml_lora_linear_bwd(const void* X, int64_t n_tokens, int64_t in_features, con
  * hidden], dA_D [rank, intermediate], dB_G, dB_U [intermediate, rank], dB_D
  * [hidden, rank]. dH = dY W_D + s_D (dY B_D) A_D is formed in bf16 and the
  * SwiGLU backward then runs over it in place.
+ * h may be NULL: it is then silu(gate) * up rounded to bf16 exactly as
+ * ml_swiglu_fwd forms it (the reference saves that product from its
+ * forward, :197-204), recomputed from gate and up instead of read (at rank
+ * 16 inside the pass that runs the SwiGLU backward; otherwise formed in the
+ * workspace). A caller that passes h gets it used as given.
  */
 size_t ml_lora_mlp_bwd_workspace_bytes(int64_t n_tokens, int64_t hidden, int64_t intermediate,
                                        int64_t rank);

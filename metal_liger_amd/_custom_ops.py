@@ -340,10 +340,11 @@ def _(x2, dy, w, a, b, scale, xa, rank):
 
 
 @torch.library.custom_op(f"{NS}::lora_mlp_bwd", mutates_args=(), device_types=_DEV)
-def lora_mlp_bwd(x2: Tensor, gate: Tensor, up: Tensor, h: Tensor, dy: Tensor, wg: Tensor,
-                 wu: Tensor, wd: Tensor, a_gu: Tensor, a_d: Tensor, bg: Tensor, bu: Tensor,
-                 bd: Tensor, scales: List[float], xa_gu: Tensor, ha_d: Tensor,
+def lora_mlp_bwd(x2: Tensor, gate: Tensor, up: Tensor, h: Optional[Tensor], dy: Tensor,
+                 wg: Tensor, wu: Tensor, wd: Tensor, a_gu: Tensor, a_d: Tensor, bg: Tensor,
+                 bu: Tensor, bd: Tensor, scales: List[float], xa_gu: Tensor, ha_d: Tensor,
                  rank: int) -> tuple[Tensor, Tensor]:
+    # h None: silu(gate) * up is recomputed by the kernels
     return hip_ops.lora_mlp_bwd(x2, gate, up, h, dy, wg, wu, wd, a_gu, a_d, bg, bu, bd, scales,
                                 xa_gu, ha_d, rank)
 

@@ -554,7 +554,7 @@ struct MlpMidArgs {
   bf16* dup;  // [N, I]
   const bf16* gate;
   const bf16* up;
-  const bf16* h;   // [N, I] each, dense
+  const bf16* h;   // [N, I] each, dense (h: unused when the kernel recomputes it)
   const bf16* xa;  // [N, 32]: XA_G | XA_U, row stride ldxa
   const bf16* pd;  // [N, 16]: P_D, row stride ldpd
   const bf16* b[2];  // B_G, B_U [I, 16], row stride ldb
@@ -573,6 +573,9 @@ __device__ __forceinline__ u32x4_t keep16(bool ok, u32x4_t v) {
   return ok ? v : u32x4_t{0u, 0u, 0u, 0u};
 }
 
+// RH: h = silu(gate) up is recomputed from the gate / up vectors (rounded to
+// bf16 as the SwiGLU forward rounds it) instead of read.
+template <bool RH>
 __global__ __launch_bounds__(256) void mlp_mid_kernel(const MlpMidArgs args) {
   typedef Pack<bf16, 8> V8;
   __shared__ __attribute__((aligned(16))) char lds[kMidBytes];
@@ -655,7 +658,7 @@ __global__ __launch_bounds__(256) void mlp_mid_kernel(const MlpMidArgs args) {
       vd[i] = nt16(args.dh, cb, off);
       vg[i] = nt16(args.gate, cb, off);
       vu[i] = nt16(args.up, cb, off);
-      vh[i] = nt16(args.h, cb, off);
+      if constexpr (!RH) vh[i] = nt16(args.h, cb, off);
     }
     const int r = rb + srow;
     vs = *reinterpret_cast<const u32x4_t*>(sbase + (int64_t)(r < N ? r : N - 1) * sld + scol);
@@ -678,14 +681,20 @@ __global__ __launch_bounds__(256) void mlp_mid_kernel(const MlpMidArgs args) {
       const bool ok = okc && r < N;
       const V8 g8 = __builtin_bit_cast(V8, vg[i]), u8 = __builtin_bit_cast(V8, vu[i]),
                y8 = __builtin_bit_cast(V8, vd[i]);
-      V8 pg, pu;
+      V8 pg, pu, ph;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        float dgf, duf;
-        swiglu_bwd_elem(to_f32(g8.v[e]), to_f32(u8.v[e]), to_f32(y8.v[e]), dgf, duf);
+        float dgf, duf, hf;
+        if constexpr (RH) {
+          swiglu_bwd_fwd_elem(to_f32(g8.v[e]), to_f32(u8.v[e]), to_f32(y8.v[e]), dgf, duf, hf);
+          ph.v[e] = from_f32<bf16>(hf);
+        } else {
+          swiglu_bwd_elem(to_f32(g8.v[e]), to_f32(u8.v[e]), to_f32(y8.v[e]), dgf, duf);
+        }
         pg.v[e] = from_f32<bf16>(dgf);
         pu.v[e] = from_f32<bf16>(duf);
       }
+      if constexpr (RH) vh[i] = __builtin_bit_cast(u32x4_t, ph);
       const u32x4_t xg = __builtin_bit_cast(u32x4_t, pg), xu = __builtin_bit_cast(u32x4_t, pu);
       if (ok) {
         const int64_t cb = (int64_t)rb * I * 2;
@@ -807,7 +816,7 @@ inline bool mlp_mid_ok(int I, const void* const* ptrs, int n, int64_t ldxa, int6
 
 // Host side: d_gate (over dH) and d_up; P_G, P_U (bf16, s times the sums,
 // row stride ldp) and dB_G, dB_U (fp32 [I, lddb]); dA_D (fp32 [16, I], row
-// stride I).
+// stride I). h null: recomputed from gate and up.
 inline int mlp_mid_pass(int N, int I, bf16* dh, bf16* dup, const bf16* gate, const bf16* up,
                         const bf16* h, const bf16* xa, int64_t ldxa, const bf16* pd,
                         int64_t ldpd, const bf16* bg, const bf16* bu, int64_t ldb, float sg,
@@ -839,7 +848,10 @@ inline int mlp_mid_pass(int N, int I, bf16* dh, bf16* dup, const bf16* gate, con
   }
   a.dapart = reinterpret_cast<float*>(w);
   const unsigned blocks = (unsigned)(a.ctiles * dy_rtiles(N));
-  mlp_mid_kernel<<<dim3(blocks), 256, 0, st>>>(a);
+  if (h)
+    mlp_mid_kernel<false><<<dim3(blocks), 256, 0, st>>>(a);
+  else
+    mlp_mid_kernel<true><<<dim3(blocks), 256, 0, st>>>(a);
   ML_LAUNCH_CHECK();
   DyReduceArgs red{};
   red.job[0] = DyReduceJob{a.ppart[0], a.ctiles, N, pg, ldp, sg, 0};
@@ -1152,7 +1164,7 @@ extern "C" int ml_lora_mlp_bwd(const void* X, int64_t n_tokens, int64_t hidden,
            "lora mlp: sizes too large");
   ML_CHECK(hidden % 8 == 0 && intermediate % 8 == 0 && rank % 8 == 0,
            "lora mlp: hidden, intermediate and rank must be multiples of 8");
-  ML_CHECK(X && gate && up && h && dY && WG && WU && WD && A_GU && A_D && BG && BU && BD && scale &&
+  ML_CHECK(X && gate && up && dY && WG && WU && WD && A_GU && A_D && BG && BU && BD && scale &&
                XA_GU && hA_D && dX && dA_GU && dA_D && dB_G && dB_U && dB_D,
            "lora mlp: null pointer");
   const size_t need = ml_lora_mlp_bwd_workspace_bytes(n_tokens, hidden, intermediate, rank);
@@ -1177,9 +1189,9 @@ extern "C" int ml_lora_mlp_bwd(const void* X, int64_t n_tokens, int64_t hidden,
   int rc;
   // rank 16 with 16-byte aligned operands: the SwiGLU backward, the gate /
   // up adapters' P and dB, and dA_D in one pass (lora::mlp_mid_pass)
-  const void* mid_ptrs[9] = {gate, up, h, dgate, dup, xa, PD, BG, BU};
+  const void* mid_ptrs[9] = {gate, up, dgate, dup, xa, PD, BG, BU, h};
   const bool fused_mid = R == lora::kDyRank && (int64_t)N * I < (1LL << 31) &&
-                         lora::mlp_mid_ok(I, mid_ptrs, 9, R2, R);
+                         lora::mlp_mid_ok(I, mid_ptrs, h ? 9 : 8, R2, R);
 
   // down projection: P_D, dA_D = P_D^T h, dB_D = s_D dY^T hA_D
   if (R == lora::kDyRank) {  // P_D and dB_D in one pass over dY
@@ -1196,6 +1208,13 @@ extern "C" int ml_lora_mlp_bwd(const void* X, int64_t n_tokens, int64_t hidden,
     rc = lora::skinny<TallCfg, kMNMajor, kMNMajor, float>(H, R, s3, dB_D, R, scale[2], part,
                                                            part_bytes, st);
     if (rc) return rc;
+  }
+  if (!fused_mid && !h) {
+    // h = silu(gate) up, as the SwiGLU forward forms it, into d_gate's buffer
+    // (free until dH is written there below)
+    rc = ml_swiglu_fwd(gate, up, dgate, (int64_t)N * I, ML_BF16, st);
+    if (rc) return rc;
+    h = dgate;
   }
   if (fused_mid) {
     rc = ML_OK;  // dA_D comes from the fused pass below

@@ -30,4 +30,16 @@ __device__ __forceinline__ void swiglu_bwd_elem(float g, float u, float dy, floa
   dg = ((dy * u) * s) * (1.0f + g * (1.0f - s));
 }
 
+// swiglu_bwd_elem, and h = silu(g) u as swiglu_fwd_elem forms it (the same
+// operations on the same sigmoid, so the same bits)
+__device__ __forceinline__ void swiglu_bwd_fwd_elem(float g, float u, float dy, float& dg,
+                                                    float& du, float& h) {
+#pragma clang fp contract(off)
+  const float s = sigmoid_f(g);
+  const float gs = g * s;
+  h = gs * u;
+  du = dy * gs;
+  dg = ((dy * u) * s) * (1.0f + g * (1.0f - s));
+}
+
 }  // namespace mla

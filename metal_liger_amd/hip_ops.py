@@ -993,7 +993,9 @@ def lora_mlp_grad_shapes(H, I, rank):
 
 def lora_mlp_bwd(x2, gate, up, h, dy, wg, wu, wd, a_gu, a_d, bg, bu, bd, scales, xa_gu, ha_d, rank):
     """Returns (dX, grads fp32) with grads holding dA_GU [2r, H], dA_D [r, I],
-    dB_G [I, r], dB_U [I, r], dB_D [H, r] as laid out by grad_layout."""
+    dB_G [I, r], dB_U [I, r], dB_D [H, r] as laid out by grad_layout. h None:
+    silu(gate) * up (bf16, as swiglu_fwd rounds it) is recomputed from gate
+    and up instead of read."""
     ensure_rocm_device(x2, gate, up, h, dy, wg, wu, wd, a_gu, a_d, bg, bu, bd, xa_gu, ha_d)
     (x2, gate, up, h, dy, wg, wu, wd, a_gu, a_d, bg, bu, bd, xa_gu, ha_d) = _dense16(
         x2, gate, up, h, dy, wg, wu, wd, a_gu, a_d, bg, bu, bd, xa_gu, ha_d)

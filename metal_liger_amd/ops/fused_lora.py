@@ -284,7 +284,9 @@ class _LoRA_MLP(torch.autograd.Function):
         h = cops.swiglu_fwd(gate, up)                             # silu(gate) * up, bf16
         ha_d = cops.lora_xa(h, a_d)                               # [N, rp]
         out = cops.lora_linear_out(h, DWc, ha_d, BD * scales[2])
-        ctx.save_for_backward(Xf, gate, up, h, xa_gu, ha_d, a_gu, a_d, GWc, UWc, DWc, BG, BU, BD)
+        # h is not saved: the backward recomputes it from gate and up (the
+        # same kernel math, so the same bits), one [N, inter] tensor less
+        ctx.save_for_backward(Xf, gate, up, xa_gu, ha_d, a_gu, a_d, GWc, UWc, DWc, BG, BU, BD)
         ctx.scales = scales
         ctx.param_dtypes = [t.dtype for t in (GA, UA, DA, GB, UB, DB)]
         ctx.ranks, ctx.rank_p = ranks, rp
@@ -309,12 +311,12 @@ class _LoRA_MLP(torch.autograd.Function):
                     None, dA_G, dB_G, None,
                     None, dA_U, dB_U, None,
                     None, dA_D, dB_D, None)
-        (Xf, gate, up, h, xa_gu, ha_d, a_gu, a_d, GW, UW, DW, BG, BU, BD) = ctx.saved_tensors
+        (Xf, gate, up, xa_gu, ha_d, a_gu, a_d, GW, UW, DW, BG, BU, BD) = ctx.saved_tensors
         (rg, ru, rd), rp = ctx.ranks, ctx.rank_p
         shape = ctx.orig_shape
         dy = hip_ops._bf16_rows(dY.reshape(-1, dY.shape[-1]))
         dX, flat = cops.lora_mlp_bwd(
-            Xf, gate, up, h, dy, GW, UW, DW, a_gu, a_d, BG, BU, BD, ctx.scales, xa_gu, ha_d, rp)
+            Xf, gate, up, None, dy, GW, UW, DW, a_gu, a_d, BG, BU, BD, ctx.scales, xa_gu, ha_d, rp)
         shapes = hip_ops.lora_mlp_grad_shapes(Xf.shape[1], gate.shape[1], rp)
         dA_GU, dA_D, dB_G, dB_U, dB_D = _adapter_grads(flat, shapes, ctx.param_dtypes)
         dX = dX.view(*shape)

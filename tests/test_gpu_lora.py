@@ -176,6 +176,36 @@ def test_lora_special_cases(dev):
     assert rel_fro(dX, expect) <= 1e-2
 
 
+@pytest.mark.parametrize("N,H,I,r", [(200, 256, 768, 16), (130, 128, 328, 8)])
+def test_lora_mlp_bwd_recomputed_h_is_bit_identical(dev, N, H, I, r):
+    """h = None (what the autograd path passes) against h from the SwiGLU
+    forward: the kernels recompute silu(gate) up with the forward's math, so
+    every output is the same bit for bit, at rank 16 (inside the pass that
+    runs the SwiGLU backward) and at rank 8 (h formed in the workspace)."""
+    from metal_liger_amd import hip_ops
+    s = 2.0
+    x = seeded((N, H), 5, BF).to(dev)
+    WG, WU = seeded((I, H), 6, BF, scale=0.1).to(dev), seeded((I, H), 7, BF, scale=0.1).to(dev)
+    WD = seeded((H, I), 8, BF, scale=0.1).to(dev)
+    a_gu = seeded((2 * r, H), 9, BF, scale=0.25).to(dev)
+    a_d = seeded((r, I), 10, BF, scale=0.25).to(dev)
+    BG, BU = seeded((I, r), 11, BF, scale=0.05).to(dev), seeded((I, r), 12, BF, scale=0.05).to(dev)
+    BD = seeded((H, r), 13, BF, scale=0.05).to(dev)
+    dy = seeded((N, H), 14, BF).to(dev)
+    xa_gu = hip_ops.lora_xa(x, a_gu)
+    gate = hip_ops.lora_linear_out(x, WG, xa_gu[:, :r], BG * s)
+    up = hip_ops.lora_linear_out(x, WU, xa_gu[:, r:], BU * s)
+    h = hip_ops.swiglu_fwd(gate, up)
+    ha_d = hip_ops.lora_xa(h, a_d)
+    args = (dy, WG, WU, WD, a_gu, a_d, BG, BU, BD, [s, s, s], xa_gu, ha_d, r)
+    dX0, g0 = hip_ops.lora_mlp_bwd(x, gate, up, h, *args)
+    dX1, g1 = hip_ops.lora_mlp_bwd(x, gate, up, None, *args)
+    torch.cuda.synchronize()
+    assert torch.equal(dX0, dX1)
+    assert torch.equal(g0, g1)
+    assert g0.abs().max().item() > 0
+
+
 def run_mlp(dev, X, params, dY):
     from metal_liger_amd.ops.fused_lora import _LoRA_MLP
     Xd = X.to(dev).requires_grad_(True)
