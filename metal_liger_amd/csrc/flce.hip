@@ -810,11 +810,11 @@ int fwd_impl(const bf16* hidden, int64_t ldh, const bf16* weight, int64_t ldw, c
 
   Segment seg{{hidden, ldh}, {weight, ldw}, H};
   Problem pb;
-  int rc = make_problem<BigCfg>(pb, M, V, 1, &seg, kKMajor, kKMajor, 0);
+  int rc = make_problem<R4Cfg>(pb, M, V, 1, &seg, kKMajor, kKMajor, 0);
   if (rc) return rc;
   EpiRowLse<TB> epi{bias, w.pmax, w.psum, M, V, nblk};
-  gemm_kernel<BigCfg, kKMajor, kKMajor, EpiRowLse<TB>>
-      <<<dim3(grid_blocks(pb)), BigCfg::THREADS, 0, st>>>(pb, epi);
+  gemm_kernel<R4Cfg, kKMajor, kKMajor, EpiRowLse<TB>>
+      <<<dim3(grid_blocks(pb)), R4Cfg::THREADS, 0, st>>>(pb, epi);
   ML_LAUNCH_CHECK();
   label_logit_kernel<TB><<<dim3((M + 3) / 4), 256, 0, st>>>(hidden, ldh, weight, ldw, bias, labels,
                                                             M, V, H, w.zy);
@@ -950,8 +950,8 @@ int fwd_grad_impl(const bf16* hidden, int64_t ldh, const bf16* weight, int64_t l
     if (rc) return rc;
     if (!grads) {  // loss only: (max, sum) partials, nothing stored
       EpiRowLse<TB> epi{bias, w.pmax, w.psum, Tc, V, nblk};
-      gemm_kernel<BigCfg, kKMajor, kKMajor, EpiRowLse<TB>>
-          <<<dim3(grid_blocks(pb)), BigCfg::THREADS, 0, st>>>(pb, epi);
+      gemm_kernel<R4Cfg, kKMajor, kKMajor, EpiRowLse<TB>>
+          <<<dim3(grid_blocks(pb)), R4Cfg::THREADS, 0, st>>>(pb, epi);
       ML_LAUNCH_CHECK();
       label_logit_kernel<TB><<<row_blocks, 256, 0, st>>>(hc, ldh, weight, ldw, bias, lc, Tc, V, H,
                                                          w.zy + t0);

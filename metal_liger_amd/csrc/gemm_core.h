@@ -7,12 +7,12 @@
 //   both layouts, transposing LDS reads (ds_read_b64_tr_b16) for MN-major
 //   operands; two engines:
 //   - 8 waves, two per SIMD in ping-pong, k-tiles of 32, four LDS stages
-//     (see "256 x 256" below): the FLCE logits (row-LSE epilogue) and dW
-//     (MN-major A) products;
+//     (see "256 x 256" below): the FLCE dW product, the FLCE products of a
+//     repeated (retain_graph) backward and the products with an MN-major A;
 //   - r4: 4 waves of 128 x 128, k-tiles of 64, five 32 KB operand slots
 //     (see "r4" below):
-//     the products with a K-major A and a store or split-K epilogue (LoRA
-//     forward / dX / dH, FLCE dH, the plain GEMM entry points).
+//     the products with a K-major A (LoRA forward / dX / dH, the FLCE logits
+//     and dH products, the plain GEMM entry points).
 // Narrow tiles Cfg<BM, BN, WAVES_M> (256 x 32, 64 x 256: the rank-r LoRA
 //   products, which would waste most of a 256 x 256 tile on padding):
 //   256 threads = 4 wave64s in a WAVES_M x (4 / WAVES_M) grid; a wave owns a
