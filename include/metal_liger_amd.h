@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define ML_ABI_VERSION 5
+#define ML_ABI_VERSION 6
 
 /* dtype tags */
 #define ML_F32 0

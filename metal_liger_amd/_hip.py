@@ -139,7 +139,7 @@ SIGNATURES: dict[str, tuple] = {
     ),
 }
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 _lib = None
 _lock = threading.Lock()
