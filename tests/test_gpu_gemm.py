@@ -35,6 +35,29 @@ def test_gemm_layouts(dev, a_t, b_t, mnk):
     assert_close(outb, ref.to(torch.bfloat16), "gemm bf16 out")
 
 
+@pytest.mark.parametrize("K", [128, 136, 192, 320, 384, 448, 520])
+@pytest.mark.parametrize("b_t", [True, False])
+def test_gemm_r4_k_tile_counts(dev, K, b_t):
+    """A K-major A runs the r4 engine, whose five 32 KB LDS slots hold two
+    k-tiles and a free slot and rotate every k-tile (a period of 5): 2, 3,
+    3, 5, 6, 7 and 9 k-tiles of 64 cover every count modulo 5, with ragged
+    K (136, 520); both B layouts; bf16 and fp32 outputs and a beta pass."""
+    from metal_liger_amd import hip_ops
+    M, N = 520, 776
+    a = seeded((M, K), 40, torch.bfloat16)
+    b = seeded((N, K) if b_t else (K, N), 41, torch.bfloat16)
+    ref = ref_mm(a, b, False, b_t)
+    out = hip_ops.matmul(a.to(dev), b.to(dev), b_t=b_t)
+    assert_close(out, ref, f"r4 K={K} b_t={b_t}")
+    outb = hip_ops.matmul(a.to(dev), b.to(dev), b_t=b_t, out_dtype=torch.bfloat16)
+    assert_close(outb, ref.to(torch.bfloat16), f"r4 K={K} b_t={b_t} bf16 out")
+    c0 = seeded((M, N), 42, torch.bfloat16)
+    c = c0.to(dev).clone()
+    hip_ops.matmul(a.to(dev), b.to(dev), b_t=b_t, out=c, alpha=0.5, beta=1.0)
+    assert_close(c, (0.5 * ref.to(torch.bfloat16).float() + c0.float()).to(torch.bfloat16),
+                 f"r4 K={K} b_t={b_t} beta")
+
+
 def test_gemm_alpha_beta_and_strides(dev):
     from metal_liger_amd import hip_ops
     big = seeded((600, 1040), 3, torch.bfloat16).to(dev)
