@@ -801,9 +801,15 @@ __global__ __launch_bounds__(256) void mlp_mid_kernel(const MlpMidArgs args) {
     }
 }
 
+// The fused pass's dA_D partials: one [16, I] fp32 block per row tile of the
+// pass itself (its row tiles are the dY pass's, not the P^T X pass's).
+inline size_t mlp_mid_dapart_bytes(int N, int I) {
+  return (size_t)dy_rtiles(N) * kDyRank * I * sizeof(float);
+}
+
 inline size_t mlp_mid_ws_bytes(int N, int I) {
   const int O[2] = {I, I};
-  return dy_pass_ws_bytes(N, O, 2) + align256(ptx_pass_ws_bytes(N, kDyRank, I));
+  return dy_pass_ws_bytes(N, O, 2) + align256(mlp_mid_dapart_bytes(N, I));
 }
 
 // Whether the fused pass takes these operands (16-byte aligned vectors).
