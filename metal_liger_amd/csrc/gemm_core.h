@@ -1279,7 +1279,7 @@ __device__ __forceinline__ void r4_mainloop(const Problem& pb, int tm, int tn, i
   for (int i = 0; i < r4::TM; ++i) f0.a[i] = r4_read_frag<LA>(ca, fa, 0, i);
 
   // One phase: the 64 MFMAs of fragment set fc, with the reads of the next
-  // k-step (k-step NS of slots sa_/sb_) into fn interleaved; phase 0 moves
+  // k-step (k-step NS of slots ra_ / rb_) into fn interleaved; phase 0 moves
   // the cursor to k-tile t + 2 and issues its A loads into ld, phase 1 its
   // B loads into ld.
   auto phase = [&](auto pc, R4Frags& fc, R4Frags& fn, const char* ra_, const char* rb_, char* ld)
