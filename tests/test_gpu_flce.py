@@ -310,6 +310,12 @@ def test_flce_config_full_size(dev):
     # the oracle (fp32, same chunking) run on the GPU
     rl, lse, mask = ref.flce_forward(hd, wd, ld, None, -100, 8192)
     assert abs(loss.item() - rl.item()) <= 1e-3 * abs(rl.item())
+    # the loss-only forward (the no-grad path) at the same size, every row's lse
+    l0, lse0, nv0 = hip_ops.flce_fwd(hd, wd, ld)
+    assert abs(l0.item() - rl.item()) <= 1e-3 * abs(rl.item())
+    assert nv0.item() == mask.sum().item()
+    assert_close(lse0, lse.float(), "loss-only lse, full size")
+    del lse0
     rdh, rdw = ref.flce_backward(hd, wd, ld, lse, mask, torch.tensor(1.0, device=dev), None, 8192)
     assert rel_fro(dh, rdh) <= 2e-2, rel_fro(dh, rdh)
     assert rel_fro(dw, rdw) <= 2e-2, rel_fro(dw, rdw)
