@@ -419,7 +419,9 @@ int ml_lora_xa(const void* X, int64_t n_tokens, int64_t in_features, int64_t ldx
  *          1: B is [K, N] row-major.
  * K (and every segment length) must be a multiple of 8, leading dimensions
  * multiples of 8, pointers 16-byte aligned, and M (N) a multiple of 8 when A
- * (B) is stored transposed. C is fp32 or bf16 (c_dtype), row-major with ldc.
+ * (B) is stored transposed. C is fp32 or bf16 (c_dtype), row-major with ldc;
+ * a bf16 C needs ldc a multiple of 8 and a 16-byte aligned base (refused
+ * otherwise), an fp32 C any ldc >= N.
  */
 int ml_gemm_bf16(int64_t M, int64_t N, int64_t K, const void* A, int64_t lda, int a_layout,
                  const void* B, int64_t ldb, int b_layout, void* C, int64_t ldc, int c_dtype,

@@ -15,6 +15,10 @@ int run(int64_t M, int64_t N, int nseg, const Segment* segs, int la, int lb, voi
   ML_CHECK(lb == kKMajor || lb == kMNMajor, "gemm: bad B layout %d", lb);
   ML_CHECK(C != nullptr && ldc >= N, "gemm: bad C (ldc %lld < N %lld)", (long long)ldc,
            (long long)N);
+  // the bf16 store epilogue writes rows of 8 columns as 16-byte vectors
+  ML_CHECK(c_dtype != ML_BF16 || (ldc % 8 == 0 && aligned16(C)),
+           "gemm: a bf16 C needs ldc a multiple of 8 and a 16-byte aligned base (ldc %lld)",
+           (long long)ldc);
   Problem pb;
   int rc = make_problem<BigCfg>(pb, (int)M, (int)N, nseg, segs, la, lb, 0);
   if (rc) return rc;
@@ -107,6 +111,9 @@ extern "C" int ml_gemm_bf16_segments_group(int count, const int64_t* M, const in
     ML_CHECK(M[g] > 0 && N[g] > 0 && M[g] < (1LL << 31) && N[g] < (1LL << 31),
              "gemm group: bad M=%lld N=%lld (product %d)", (long long)M[g], (long long)N[g], g);
     ML_CHECK(C[g] != nullptr && ldc[g] >= N[g], "gemm group: bad C (product %d)", g);
+    ML_CHECK(c_dtype != ML_BF16 || (ldc[g] % 8 == 0 && aligned16(C[g])),
+             "gemm group: a bf16 C needs ldc a multiple of 8 and a 16-byte aligned base "
+             "(product %d, ldc %lld)", g, (long long)ldc[g]);
     ML_CHECK(nseg[g] >= 1 && nseg[g] <= gemm::kMaxSeg, "gemm group: 1..%d segments (product %d)",
              gemm::kMaxSeg, g);
     gemm::Segment segs[gemm::kMaxSeg];

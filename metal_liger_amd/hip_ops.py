@@ -506,6 +506,10 @@ def matmul(a: torch.Tensor, b: torch.Tensor, *, a_t: bool = False, b_t: bool = F
     if K != Kb:
         raise ValueError(f"gemm: inner dimensions differ ({K} vs {Kb})")
     if out is None:
+        if out_dtype == torch.bfloat16 and N % 8 != 0 and tile_cfg == 0 and ksplit == 1:
+            # the engines store bf16 rows as 16-byte vectors (row stride a
+            # multiple of 8): compute in fp32 and round once
+            return matmul(a, b, a_t=a_t, b_t=b_t, out_dtype=torch.float32, alpha=alpha).to(out_dtype)
         out = torch.empty(M, N, dtype=out_dtype, device=a.device)
         beta = 0.0
     elif out.shape != (M, N) or out.stride(1) != 1:

@@ -60,6 +60,10 @@ def test_host_side_argument_errors():
     assert rc == 1 and b"even" in L.ml_last_error()
     with pytest.raises(RuntimeError, match="ml_swiglu_fwd"):
         _hip.call("ml_swiglu_fwd", None, None, None, 16, 0, None)
+    # a bf16 C must have a row stride that is a multiple of 8 (16-byte row
+    # vectors); refused before any HIP call (the pointers are never read)
+    rc = L.ml_gemm_bf16(8, 1003, 64, 4096, 64, 0, 8192, 64, 0, 16384, 1003, 1, 1.0, 0.0, None)
+    assert rc == 1 and b"bf16 C" in L.ml_last_error()
     assert L.ml_rmsnorm_bwd_workspace_bytes(8192, 2048) >= 8192 // 8 * 2048 * 4 // 8
 
 

@@ -86,6 +86,21 @@ def test_gemm_segments(dev):
     assert_close(C, ref, "segments")
 
 
+def test_gemm_bf16_output_row_stride(dev):
+    """A bf16 C is stored as 16-byte rows of 8 columns: the C ABI refuses a
+    row stride that is not a multiple of 8, and matmul with an odd N and no
+    `out` computes in fp32 and rounds once."""
+    from metal_liger_amd import hip_ops
+    a = seeded((300, 264), 50, torch.bfloat16)
+    b = seeded((1003, 264), 51, torch.bfloat16)
+    out = hip_ops.matmul(a.to(dev), b.to(dev), b_t=True, out_dtype=torch.bfloat16)
+    assert out.shape == (300, 1003) and out.dtype == torch.bfloat16
+    assert_close(out, ref_mm(a, b, False, True).to(torch.bfloat16), "bf16 out, N = 1003")
+    c = torch.empty(300, 1003, dtype=torch.bfloat16, device=dev)
+    with pytest.raises(RuntimeError, match="bf16 C"):
+        hip_ops.matmul(a.to(dev), b.to(dev), b_t=True, out=c)
+
+
 def test_gemm_rejects_bad_shapes(dev):
     from metal_liger_amd import hip_ops
     a = torch.zeros(64, 12, dtype=torch.bfloat16, device=dev)   # K = 12 not a multiple of 8
