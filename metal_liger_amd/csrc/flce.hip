@@ -1282,6 +1282,8 @@ extern "C" int ml_flce_bwd(const void* hidden, int64_t ldh, const void* weight, 
   if (rc) return rc;
   ML_CHECK(chunk > 0 && chunk % 8 == 0 && chunk < (1LL << 31),
            "flce: chunk size must be a positive multiple of 8 (got %lld)", (long long)chunk);
+  ML_CHECK((!d_hidden || aligned16(d_hidden)) && (!d_weight || aligned16(d_weight)),
+           "flce: gradients must be 16-byte aligned");
   hipStream_t st = (hipStream_t)stream;
   const int64_t H = hidden_size;
   if (n_tokens == 0) {
@@ -1329,6 +1331,9 @@ extern "C" int ml_flce_fwd_grad(const void* hidden, int64_t ldh, const void* wei
                               bias_dtype);
   if (rc) return rc;
   ML_CHECK(loss && n_valid && (n_tokens == 0 || lse), "flce: null output pointer");
+  // dW is written as 16-byte row vectors; dH is scaled as 16-byte vectors later
+  ML_CHECK((!d_hidden || aligned16(d_hidden)) && (!d_weight || aligned16(d_weight)),
+           "flce: gradients must be 16-byte aligned");
   ML_CHECK(token_chunk > 0 && token_chunk < (1LL << 31), "flce: token_chunk must be positive");
   hipStream_t st = (hipStream_t)stream;
   const int64_t H = hidden_size;
@@ -1365,6 +1370,8 @@ extern "C" int ml_flce_scale_grads(const float* grad_loss, void* d_hidden, int64
   ML_CHECK(grad_loss, "flce: null grad_loss");
   ML_CHECK(n_hidden >= 0 && n_weight >= 0, "flce: negative sizes");
   ML_CHECK((n_hidden == 0 || d_hidden) && (n_weight == 0 || d_weight), "flce: null gradient");
+  ML_CHECK((n_hidden == 0 || aligned16(d_hidden)) && (n_weight == 0 || aligned16(d_weight)),
+           "flce: gradients must be 16-byte aligned");
   hipStream_t st = (hipStream_t)stream;
   void* ptrs[2] = {d_hidden, d_weight};
   const int64_t ns[2] = {n_hidden, n_weight};

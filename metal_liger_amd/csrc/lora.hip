@@ -1033,6 +1033,8 @@ static int adapters_bwd(const char* what, int nadp, const void* X, int64_t n_tok
              "%s: out_features[%d] must be a positive multiple of 8", what, i);
   }
   const size_t need = adapters_bwd_ws_bytes(n_tokens, in_features, out_features, nadp, rank);
+  ML_CHECK(aligned16(dX), "%s: dX must be 16-byte aligned (it is written as 16-byte rows)",
+           what);
   ML_CHECK(workspace && workspace_bytes >= need, "%s: workspace too small (%zu < %zu)", what,
            workspace_bytes, need);
   const int N = (int)n_tokens, IN = (int)in_features, R = (int)rank, RS = nadp * (int)rank;
@@ -1173,6 +1175,7 @@ extern "C" int ml_lora_mlp_bwd(const void* X, int64_t n_tokens, int64_t hidden,
   ML_CHECK(X && gate && up && dY && WG && WU && WD && A_GU && A_D && BG && BU && BD && scale &&
                XA_GU && hA_D && dX && dA_GU && dA_D && dB_G && dB_U && dB_D,
            "lora mlp: null pointer");
+  ML_CHECK(aligned16(dX), "lora mlp: dX must be 16-byte aligned (it is written as 16-byte rows)");
   const size_t need = ml_lora_mlp_bwd_workspace_bytes(n_tokens, hidden, intermediate, rank);
   ML_CHECK(workspace && workspace_bytes >= need, "lora mlp: workspace too small (%zu < %zu)",
            workspace_bytes, need);

@@ -64,6 +64,10 @@ def test_host_side_argument_errors():
     # vectors); refused before any HIP call (the pointers are never read)
     rc = L.ml_gemm_bf16(8, 1003, 64, 4096, 64, 0, 8192, 64, 0, 16384, 1003, 1, 1.0, 0.0, None)
     assert rc == 1 and b"bf16 C" in L.ml_last_error()
+    # the one-pass FLCE writes dW as 16-byte vectors: a misaligned dW is refused
+    rc = L.ml_flce_fwd_grad(4096, 64, 8192, 64, None, 0, 12288, 8, 64, 64, -100, 8, 16384, 20480,
+                            24576, None, 28674, None, 0, None)
+    assert rc == 1 and b"16-byte aligned" in L.ml_last_error()
     assert L.ml_rmsnorm_bwd_workspace_bytes(8192, 2048) >= 8192 // 8 * 2048 * 4 // 8
 
 
