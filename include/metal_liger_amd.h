@@ -254,6 +254,8 @@ int ml_qk_norm_rope_bwd(const void* q, const void* dq_out, void* dq, const int64
  * Forward: loss = sum_valid (lse - z_label) / max(#valid, 1) (fp32 scalar),
  * lse fp32 [n_tokens], n_valid fp32 scalar (#valid tokens). No [tokens,
  * vocab] tensor is ever allocated; the workspace holds per-row partials.
+ * Gradient outputs of the entry points below are written as 16-byte vectors
+ * and must be 16-byte aligned (refused otherwise).
  */
 size_t ml_flce_fwd_workspace_bytes(int64_t n_tokens, int64_t vocab);
 int ml_flce_fwd(const void* hidden, int64_t ldh, const void* weight, int64_t ldw, const void* bias,
@@ -341,8 +343,9 @@ int ml_flce_scale_grads_f32(const float* grad_loss, float* d_hidden, int64_t n_h
  * A_stack [3 rank, in] stacks A_q, A_k, A_v (bf16); XA [n_tokens, 3 rank] is
  * X A_stack^T from the forward. Outputs: dX bf16 [n_tokens, in];
  * dA fp32 [3 rank, in] (dA_q, dA_k, dA_v stacked); dB[i] fp32 [out, rank].
- * in_features, out_features and rank must be multiples of 8. No gradient
- * for the frozen base weights, as in the reference.
+ * in_features, out_features and rank must be multiples of 8; dX is written
+ * as 16-byte rows and must be 16-byte aligned. No gradient for the frozen
+ * base weights, as in the reference.
  */
 size_t ml_lora_qkv_bwd_workspace_bytes(int64_t n_tokens, int64_t in_features,
                                        const int64_t* out_features, int64_t rank);
@@ -378,8 +381,9 @@ int ml_lora_linear_bwd(const void* X, int64_t n_tokens, int64_t in_features, con
  * intermediate], BG, BU [intermediate, rank], BD [hidden, rank]; scale = HOST
  * floats {s_G, s_U, s_D}. Outputs: dX bf16 [n, hidden]; fp32 dA_GU [2 rank,
  * hidden], dA_D [rank, intermediate], dB_G, dB_U [intermediate, rank], dB_D
- * [hidden, rank]. dH = dY W_D + s_D (dY B_D) A_D is formed in bf16 and the
- * SwiGLU backward then runs over it in place.
+ * [hidden, rank] (dX 16-byte aligned: it is written as 16-byte rows).
+ * dH = dY W_D + s_D (dY B_D) A_D is formed in bf16 and the SwiGLU backward
+ * then runs over it in place.
  * h may be NULL: it is then silu(gate) * up rounded to bf16 exactly as
  * ml_swiglu_fwd forms it (the reference saves that product from its
  * forward, :197-204), recomputed from gate and up instead of read (at rank
