@@ -52,7 +52,8 @@ def check_grads(dh, dw, rdh, rdw, what):
 
 
 @pytest.mark.parametrize("N,H,V,chunk", [(200, 64, 1000, 256), (64, 128, 2048, 8192),
-                                         (333, 256, 4104, 1000), (8, 64, 64, 8)])
+                                         (333, 256, 4104, 1000), (8, 64, 64, 8), (1, 64, 1000, 256),
+                                         (3, 128, 520, 8)])
 def test_flce_small(dev, N, H, V, chunk):
     h, w, lab = make_inputs(N, H, V, seed=N, ignore_frac=0.25, w_scale=0.3)
     loss, dh, dw = run_ours(dev, h, w, lab, chunk=chunk)

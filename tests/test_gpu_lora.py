@@ -102,7 +102,8 @@ def run_qkv(dev, X, params, dys):
 
 @pytest.mark.parametrize("N,IN,OUTS,r", [(32, 128, (128, 128, 128), 8), (300, 256, (256, 128, 128), 16),
                                          (64, 64, (64, 32, 32), 4), (77, 64, (384, 136, 8), 16),
-                                         (130, 256, (256, 128, 128), 32), (96, 128, (128, 64, 64), 64)])
+                                         (130, 256, (256, 128, 128), 32), (96, 128, (128, 64, 64), 64),
+                                         (1, 64, (64, 32, 32), 16), (5, 128, (128, 64, 64), 8)])
 def test_lora_qkv_small(dev, N, IN, OUTS, r):
     X = seeded((N, IN), 1, BF)
     params = [(*adapter(o, IN, r, 10 * i + 2, b_std=0.05), 2.0) for i, o in enumerate(OUTS)]
@@ -222,7 +223,7 @@ def run_mlp(dev, X, params, dY):
 
 
 @pytest.mark.parametrize("N,H,I,r", [(48, 128, 256, 8), (200, 256, 768, 16), (130, 128, 328, 16),
-                                     (130, 256, 512, 32)])
+                                     (130, 256, 512, 32), (3, 128, 256, 16)])
 def test_lora_mlp_small(dev, N, H, I, r):
     X = seeded((N, H), 5, BF)
     G = adapter(I, H, r, 80, w_std=0.1, b_std=0.05)
