@@ -87,12 +87,12 @@ def test_flce_dh_split_count_fills_its_rounds():
     only dH-dependent buffer): at the Qwen3 head (H = 2048, V = 151936) the
     items of the last round of a launch fill at least 3/4 of the CUs (a fixed
     item target had left 264 items at 2736-token chunks: a second round of 8
-    items as long as the first) and the config's 4096-token chunks keep two
-    splits."""
+    items as long as the first); 2048-token chunks (the default at the
+    config) take four splits and 4096-token chunks two."""
     L = lib()
     H, V = 2048, 151936
     al = lambda b: (b + 255) // 256 * 256
-    for T, want in ((4096, 2), (8192, 1), (256, 32), (2736, None), (3072, None), (2048, None)):
+    for T, want in ((4096, 2), (8192, 1), (256, 32), (2736, None), (3072, None), (2048, 4)):
         part = (L.ml_flce_fwd_grad_workspace_bytes(T, V, H, T, 1)
                 - L.ml_flce_fwd_grad_workspace_bytes(T, V, H, T, 0))
         splits, rem = divmod(part, al(T * H * 4))

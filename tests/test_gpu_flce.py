@@ -66,9 +66,10 @@ def test_flce_small(dev, N, H, V, chunk):
 
 
 def test_flce_token_chunk_over_65535_rows(dev):
-    """A small vocabulary lets the whole batch be one token chunk: 70000
-    rows, more than a grid dimension's 65535 blocks, so the dlogit pass
-    walks its rows in two rounds; the rows past 65535 are checked alone."""
+    """A small vocabulary lets the whole batch be one token chunk of 70000
+    rows, more than a grid dimension's 65535 blocks (no row-indexed launch
+    may depend on one block per row there); the rows past 65535 are checked
+    alone."""
     from metal_liger_amd import hip_ops
     N, H, V = 70000, 64, 512
     assert hip_ops.flce_token_chunk(N, V) == N
