@@ -68,21 +68,6 @@ struct alignas(sizeof(T) * N) Pack {
   T v[N];
 };
 
-template <typename T, int N>
-__device__ __forceinline__ void load_pack(const T* __restrict__ p, float (&out)[N]) {
-  Pack<T, N> pk = *reinterpret_cast<const Pack<T, N>*>(p);
-#pragma unroll
-  for (int i = 0; i < N; ++i) out[i] = to_f32(pk.v[i]);
-}
-
-template <typename T, int N>
-__device__ __forceinline__ void store_pack(T* __restrict__ p, const float (&in)[N]) {
-  Pack<T, N> pk;
-#pragma unroll
-  for (int i = 0; i < N; ++i) pk.v[i] = from_f32<T>(in[i]);
-  *reinterpret_cast<Pack<T, N>*>(p) = pk;
-}
-
 // Elements of T per 16-byte transaction.
 template <typename T>
 constexpr int vec16() { return 16 / static_cast<int>(sizeof(T)); }
