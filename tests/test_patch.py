@@ -364,6 +364,52 @@ class _RecordingCops:
         self.calls.append(("flce_scale_grads",))
 
 
+class _RecordingLoraCops:
+    """Stand-in for the custom-op module in the bf16 LoRA MLP Function:
+    outputs of the right shapes, and the h its backward is called with."""
+
+    def __init__(self):
+        self.h = "not called"
+
+    def lora_xa(self, x, a):
+        return torch.zeros(x.shape[0], a.shape[0], dtype=torch.bfloat16)
+
+    def lora_linear_out(self, x, w, xa, sb):
+        return torch.zeros(x.shape[0], w.shape[0], dtype=torch.bfloat16)
+
+    def swiglu_fwd(self, g, u):
+        return torch.zeros_like(g)
+
+    def lora_mlp_bwd(self, x2, gate, up, h, dy, *rest):
+        from metal_liger_amd import hip_ops
+        self.h = h
+        shapes = hip_ops.lora_mlp_grad_shapes(x2.shape[1], gate.shape[1], rest[-1])
+        return torch.zeros_like(x2), torch.zeros(hip_ops.grad_layout(shapes)[1])
+
+
+def test_lora_mlp_saves_no_h_and_recomputes_it(monkeypatch):
+    """The bf16 MLP Function keeps gate and up for its backward but not
+    h = silu(gate) up (the reference saves all three,
+    ops/fused_lora.py:197-204), and calls the fused backward with h = None:
+    the kernels recompute h with the SwiGLU forward's math."""
+    import metal_liger_amd.ops.fused_lora as fl
+    rec = _RecordingLoraCops()
+    monkeypatch.setattr(fl, "cops", rec)
+    N, H, I, r = 24, 32, 48, 8
+    bf = torch.bfloat16
+
+    def adapter(o, i):
+        return (torch.randn(o, i, dtype=bf), torch.randn(r, i, dtype=bf, requires_grad=True),
+                torch.randn(o, r, dtype=bf, requires_grad=True), 2.0)
+
+    X = torch.randn(N, H, dtype=bf, requires_grad=True)
+    out = fl._LoRA_MLP.apply(X, *adapter(I, H), *adapter(I, H), *adapter(H, I))
+    saved = out.grad_fn.saved_tensors
+    assert sum(1 for t in saved if tuple(t.shape) == (N, I)) == 2  # gate and up only
+    out.backward(torch.ones_like(out))
+    assert rec.h is None and X.grad is not None
+
+
 def test_fused_loss_routes_no_grad_to_loss_only(monkeypatch):
     """With grad mode off the module (and the causal-LM loss) call the
     loss-only entry point even when the lm_head weight requires grad; with
