@@ -51,7 +51,8 @@ def test_rmsnorm_parity(dev, dtype, shape):
 
 
 def test_rmsnorm_config_fp32_saved_rrms(dev):
-    """x [8192, 2048] fp32, weight 1 + 0.1 N(0,1), eps 1e-6."""
+    """The fp32 RMSNorm workload: x [8192, 2048] fp32, weight 1 + 0.1 N(0,1),
+    eps 1e-6, the rrms the forward saves."""
     from metal_liger_amd import hip_ops
     x = seeded((8192, 2048), 0)
     w = seeded((2048,), 1, scale=0.1, shift=1.0)
@@ -279,7 +280,7 @@ def test_rope_mixed_dtype_promotes(dev):
 
 
 def test_rope_positions_config(dev):
-    """configs[1] RoPE: q [4,16,2048,128], k [4,8,2048,128] bf16, positions 0..2047,
+    """The bf16 RoPE workload: q [4,16,2048,128], k [4,8,2048,128] bf16, positions 0..2047,
     theta 1e6, cos/sin computed in-kernel. Compared with the oracle's rotation
     using the HF-style fp32 tables (the kernel rounds once, to bf16)."""
     from metal_liger_amd.ops.fused_rope import apply_fused_rotary_inline
